@@ -1,0 +1,128 @@
+/*
+ * palladium_hip: the C ABI between palladium_amd's Python host layer (or a
+ * jax.ffi handler) and the HIP runtime on MI355X (gfx950).
+ *
+ * Everything crossing this boundary is a plain pointer, size or integer.
+ * Every function returns PH_OK (0) or an error code and, where it takes a
+ * `char **err`, stores a heap message there that the caller releases with
+ * ph_free_error().
+ *
+ * Each entry point names the reference interface it replaces
+ * (paths relative to nicholasjng/palladium).
+ */
+#ifndef PALLADIUM_HIP_H
+#define PALLADIUM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  PH_OK = 0,
+  PH_ERR_INVALID_ARGUMENT = 1,
+  PH_ERR_COMPILE = 2,
+  PH_ERR_RUNTIME = 3,
+};
+
+/* Math modes, same ordinals as the reference's MRMathMode
+ * (src/palladium/ffi.py:38): SAFE = IEEE order, no contraction;
+ * RELAXED = FMA contraction; FAST = contraction, reassociation and
+ * approximate transcendentals/division (infinities and NaNs still honoured). */
+enum { PH_MATH_SAFE = 0, PH_MATH_RELAXED = 1, PH_MATH_FAST = 2 };
+
+typedef struct ph_kernel ph_kernel;
+
+/* Library version string, e.g. "0.1.0". */
+const char *ph_version(void);
+
+/* Releases a message returned through an `err` out-parameter.
+ * Replaces mr_free_error_message (native/ffi/palladium_ffi.cpp:60-61). */
+void ph_free_error(char *err);
+
+/* Compiles HIP source with hiprtc for `arch` (NULL = "gfx950") and returns
+ * the code object (release with ph_free_code_object). Needs no GPU.
+ * Replaces mr_compile_library (native/ffi/palladium_ffi.cpp:57-58). */
+int ph_compile_code_object(const char *src, size_t src_len, const char *name,
+                           int math_mode, const char *arch, void **code,
+                           size_t *code_size, char **err);
+void ph_free_code_object(void *code);
+
+/* The hiprtc option string used for a math mode (static storage). */
+const char *ph_compile_options(int math_mode);
+
+/* Compile (outside the cache lock), load on the current device and look up
+ * `name`; cached for the process lifetime by (source, name, math mode,
+ * device). Concurrent first calls may compile twice; the loser is unloaded.
+ * Replaces KernelCache::get_or_compile (native/ffi/palladium_ffi.cpp:25-91)
+ * plus mr_get_pipeline. */
+int ph_get_kernel(const char *src, size_t src_len, const char *name,
+                  int math_mode, ph_kernel **out, char **err);
+
+/* Number of distinct kernels in the cache (for tests). */
+size_t ph_kernel_cache_size(void);
+
+/* Launch on `stream` (NULL = default stream), asynchronously. `params` is
+ * the hipModuleLaunchKernel argument array (one pointer to each argument
+ * value). Replaces the dispatch half of mr_dispatch
+ * (native/ffi/palladium_ffi.cpp:150-165). */
+int ph_launch(ph_kernel *k, unsigned int grid_x, unsigned int grid_y,
+              unsigned int grid_z, unsigned int block_x, unsigned int block_y,
+              unsigned int block_z, unsigned int shared_bytes, void *stream,
+              void **params, char **err);
+
+/* Launch a kernel whose arguments are exactly `n_ptrs` device pointers
+ * (the signature emit_hip produces), over a 1-D grid. */
+int ph_launch_ptrs(ph_kernel *k, unsigned int blocks, unsigned int block,
+                   void *stream, void *const *ptrs, size_t n_ptrs, char **err);
+
+/* One synchronous dispatch of emitted source over host buffers: compile or
+ * hit the cache, stage inputs host->device, launch ceil(prod(grid)/block)
+ * workgroups of `block` lanes (0 = 256), copy outputs device->host, wait.
+ * Attribute-for-attribute the reference's XLA FFI handler on the "cpu"
+ * platform (native/ffi/palladium_ffi.cpp:110-209): source, function name,
+ * grid, block (threadgroup), math mode, then inputs, then outputs. */
+int ph_dispatch(const char *src, size_t src_len, const char *name,
+                int64_t grid_x, int64_t grid_y, int64_t grid_z,
+                int64_t block_x, int64_t math_mode, const void *const *inputs,
+                const size_t *input_bytes, size_t n_inputs,
+                void *const *outputs, const size_t *output_bytes,
+                size_t n_outputs, char **err);
+
+/* Device memory, streams, events and graphs: the role metal-runtime's
+ * Buffer/Batch/gpu_time play for the reference
+ * (src/palladium/dispatch.py:18,183-225). Streams are created at the
+ * default priority. */
+int ph_device_count(int *count);
+int ph_device_name(char *buf, size_t len);
+int ph_malloc(size_t bytes, void **ptr, char **err);
+int ph_free(void *ptr);
+int ph_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream, char **err);
+int ph_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream, char **err);
+int ph_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream, char **err);
+int ph_stream_create(void **stream, char **err);
+int ph_stream_destroy(void *stream);
+int ph_stream_synchronize(void *stream, char **err);
+int ph_event_create(void **event, char **err);
+int ph_event_destroy(void *event);
+int ph_event_record(void *event, void *stream, char **err);
+int ph_event_synchronize(void *event, char **err);
+int ph_event_query(void *event); /* 1 = complete, 0 = pending, <0 error */
+int ph_event_elapsed_ms(void *start, void *stop, float *ms, char **err);
+int ph_device_synchronize(char **err);
+
+/* Stream capture into a HIP graph and replay: the multi-launch batch of
+ * the reference's Gray-Scott driver (examples/04_reaction_diffusion.py:
+ * 100-107) as one graph launch. */
+int ph_stream_begin_capture(void *stream, char **err);
+int ph_stream_end_capture(void *stream, void **graph_exec, char **err);
+int ph_graph_launch(void *graph_exec, void *stream, char **err);
+int ph_graph_destroy(void *graph_exec);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PALLADIUM_HIP_H */

@@ -1,0 +1,422 @@
+// palladium_hip: hiprtc compile cache, module loading and launches for
+// palladium_amd kernels on MI355X (gfx950). C ABI in include/palladium_hip.h.
+//
+// The kernel cache follows the reference handler's discipline
+// (native/ffi/palladium_ffi.cpp:25-91): look up under a mutex, compile
+// outside it so different kernels compile concurrently, re-check on
+// insert and release the loser of a race.
+
+#include "palladium_hip.h"
+
+#include <hip/hip_runtime.h>
+#include <hip/hiprtc.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+struct ph_kernel {
+  hipModule_t module;
+  hipFunction_t function;
+  int device;
+};
+
+namespace {
+
+char *dup_message(const std::string &s) {
+  char *p = static_cast<char *>(std::malloc(s.size() + 1));
+  if (p) std::memcpy(p, s.c_str(), s.size() + 1);
+  return p;
+}
+
+int fail(char **err, int code, const std::string &msg) {
+  if (err) *err = dup_message(msg);
+  return code;
+}
+
+int hip_fail(char **err, hipError_t e, const char *what) {
+  return fail(err, PH_ERR_RUNTIME,
+              std::string(what) + ": " + hipGetErrorName(e) + " (" +
+                  hipGetErrorString(e) + ")");
+}
+
+const char *kOptions[3] = {
+    "-ffp-contract=off",
+    "-ffp-contract=fast",
+    "-ffp-contract=fast -ffast-math -fno-finite-math-only "
+    "-fno-hip-fp32-correctly-rounded-divide-sqrt",
+};
+
+std::vector<std::string> build_options(int math_mode, const char *arch) {
+  std::vector<std::string> o;
+  o.push_back(std::string("--offload-arch=") + (arch && *arch ? arch : "gfx950"));
+  o.push_back("-O3");
+  o.push_back("-std=c++17");
+  // Packed FP32 VALU forms are kept out of every code object.
+  o.push_back("-Xclang");
+  o.push_back("-target-feature");
+  o.push_back("-Xclang");
+  o.push_back("-packed-fp32-ops");
+  o.push_back("-DPH_MATH_MODE=" + std::to_string(math_mode));
+  std::string mode = kOptions[math_mode];
+  size_t pos = 0;
+  while (pos < mode.size()) {
+    size_t sp = mode.find(' ', pos);
+    if (sp == std::string::npos) sp = mode.size();
+    if (sp > pos) o.push_back(mode.substr(pos, sp - pos));
+    pos = sp + 1;
+  }
+  return o;
+}
+
+int compile(const char *src, size_t src_len, const char *name, int math_mode,
+            const char *arch, std::vector<char> *code, char **err) {
+  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_FAST)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip: math_mode out of range");
+  std::string source(src, src_len);
+  std::string fname = std::string(name ? name : "kernel") + ".hip";
+  hiprtcProgram prog;
+  hiprtcResult r = hiprtcCreateProgram(&prog, source.c_str(), fname.c_str(), 0,
+                                       nullptr, nullptr);
+  if (r != HIPRTC_SUCCESS)
+    return fail(err, PH_ERR_COMPILE,
+                std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(r));
+  std::vector<std::string> opts = build_options(math_mode, arch);
+  std::vector<const char *> copts;
+  for (auto &s : opts) copts.push_back(s.c_str());
+  r = hiprtcCompileProgram(prog, (int)copts.size(), copts.data());
+  if (r != HIPRTC_SUCCESS) {
+    size_t log_size = 0;
+    hiprtcGetProgramLogSize(prog, &log_size);
+    std::string log(log_size, '\0');
+    if (log_size) hiprtcGetProgramLog(prog, &log[0]);
+    hiprtcDestroyProgram(&prog);
+    return fail(err, PH_ERR_COMPILE,
+                std::string("hiprtc compile failed (") + hiprtcGetErrorString(r) +
+                    "):\n" + log);
+  }
+  size_t size = 0;
+  hiprtcGetCodeSize(prog, &size);
+  code->resize(size);
+  hiprtcGetCode(prog, code->data());
+  hiprtcDestroyProgram(&prog);
+  return PH_OK;
+}
+
+class KernelCache {
+ public:
+  static KernelCache &instance() {
+    static KernelCache *cache = new KernelCache();  // never destroyed: modules
+    return *cache;                                  // outlive static teardown
+  }
+
+  int get(const char *src, size_t src_len, const char *name, int math_mode,
+          ph_kernel **out, char **err) {
+    int device = 0;
+    hipError_t he = hipGetDevice(&device);
+    if (he != hipSuccess) return hip_fail(err, he, "hipGetDevice");
+    std::string key;
+    key.reserve(src_len + 64);
+    key.append(src, src_len);
+    key.push_back('\0');
+    key.append(name);
+    key.push_back('\0');
+    key.append(std::to_string(math_mode));
+    key.push_back('\0');
+    key.append(std::to_string(device));
+    {
+      std::lock_guard<std::mutex> lock(mutex_);
+      auto it = entries_.find(key);
+      if (it != entries_.end()) {
+        *out = it->second.get();
+        return PH_OK;
+      }
+    }
+    std::vector<char> code;
+    int rc = compile(src, src_len, name, math_mode, "gfx950", &code, err);
+    if (rc != PH_OK) return rc;
+    auto k = std::make_unique<ph_kernel>();
+    k->device = device;
+    he = hipModuleLoadData(&k->module, code.data());
+    if (he != hipSuccess) return hip_fail(err, he, "hipModuleLoadData");
+    he = hipModuleGetFunction(&k->function, k->module, name);
+    if (he != hipSuccess) {
+      hipModuleUnload(k->module);
+      return hip_fail(err, he, (std::string("hipModuleGetFunction(") + name + ")").c_str());
+    }
+    std::lock_guard<std::mutex> lock(mutex_);
+    auto it = entries_.find(key);
+    if (it != entries_.end()) {
+      hipModuleUnload(k->module);
+      *out = it->second.get();
+      return PH_OK;
+    }
+    *out = k.get();
+    entries_.emplace(std::move(key), std::move(k));
+    return PH_OK;
+  }
+
+  size_t size() {
+    std::lock_guard<std::mutex> lock(mutex_);
+    return entries_.size();
+  }
+
+ private:
+  std::mutex mutex_;
+  std::unordered_map<std::string, std::unique_ptr<ph_kernel>> entries_;
+};
+
+}  // namespace
+
+extern "C" {
+
+const char *ph_version(void) { return "0.1.0"; }
+
+void ph_free_error(char *err) { std::free(err); }
+
+int ph_compile_code_object(const char *src, size_t src_len, const char *name,
+                           int math_mode, const char *arch, void **code,
+                           size_t *code_size, char **err) {
+  if (!src || !name || !code || !code_size)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_compile_code_object: null argument");
+  std::vector<char> buf;
+  int rc = compile(src, src_len, name, math_mode, arch, &buf, err);
+  if (rc != PH_OK) return rc;
+  void *p = std::malloc(buf.size());
+  if (!p) return fail(err, PH_ERR_RUNTIME, "out of host memory");
+  std::memcpy(p, buf.data(), buf.size());
+  *code = p;
+  *code_size = buf.size();
+  return PH_OK;
+}
+
+void ph_free_code_object(void *code) { std::free(code); }
+
+const char *ph_compile_options(int math_mode) {
+  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_FAST) return "";
+  return kOptions[math_mode];
+}
+
+int ph_get_kernel(const char *src, size_t src_len, const char *name,
+                  int math_mode, ph_kernel **out, char **err) {
+  if (!src || !name || !out)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_get_kernel: null argument");
+  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_FAST)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip: math_mode out of range");
+  return KernelCache::instance().get(src, src_len, name, math_mode, out, err);
+}
+
+size_t ph_kernel_cache_size(void) { return KernelCache::instance().size(); }
+
+int ph_launch(ph_kernel *k, unsigned int gx, unsigned int gy, unsigned int gz,
+              unsigned int bx, unsigned int by, unsigned int bz,
+              unsigned int shared, void *stream, void **params, char **err) {
+  if (!k) return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_launch: null kernel");
+  if (gx == 0 || gy == 0 || gz == 0 || bx == 0 || by == 0 || bz == 0 ||
+      (size_t)bx * by * bz > 1024)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_launch: invalid launch geometry");
+  hipError_t e = hipModuleLaunchKernel(k->function, gx, gy, gz, bx, by, bz, shared,
+                                       (hipStream_t)stream, params, nullptr);
+  if (e != hipSuccess) return hip_fail(err, e, "hipModuleLaunchKernel");
+  return PH_OK;
+}
+
+int ph_launch_ptrs(ph_kernel *k, unsigned int blocks, unsigned int block,
+                   void *stream, void *const *ptrs, size_t n_ptrs, char **err) {
+  std::vector<void *> values(ptrs, ptrs + n_ptrs);
+  std::vector<void *> params(n_ptrs);
+  for (size_t i = 0; i < n_ptrs; ++i) params[i] = &values[i];
+  return ph_launch(k, blocks, 1, 1, block, 1, 1, 0, stream,
+                   n_ptrs ? params.data() : nullptr, err);
+}
+
+int ph_dispatch(const char *src, size_t src_len, const char *name,
+                int64_t grid_x, int64_t grid_y, int64_t grid_z, int64_t block_x,
+                int64_t math_mode, const void *const *inputs,
+                const size_t *input_bytes, size_t n_inputs,
+                void *const *outputs, const size_t *output_bytes,
+                size_t n_outputs, char **err) {
+  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_FAST)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: math_mode out of range");
+  if (grid_x <= 0 || grid_y <= 0 || grid_z <= 0)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: grid dims must be positive");
+  int64_t programs = grid_x * grid_y * grid_z;
+  int64_t block = block_x > 0 ? block_x : 256;
+  if (block > 1024 || block % 64)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: block must be a multiple of 64, at most 1024");
+  if (programs >= (int64_t(1) << 31))
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: too many program instances");
+  ph_kernel *k = nullptr;
+  int rc = ph_get_kernel(src, src_len, name, (int)math_mode, &k, err);
+  if (rc != PH_OK) return rc;
+
+  hipStream_t stream = nullptr;
+  hipError_t e = hipStreamCreate(&stream);
+  if (e != hipSuccess) return hip_fail(err, e, "hipStreamCreate");
+  std::vector<void *> dev(n_inputs + n_outputs, nullptr);
+  auto cleanup = [&]() {
+    for (void *p : dev)
+      if (p) hipFree(p);
+    hipStreamDestroy(stream);
+  };
+  for (size_t i = 0; i < n_inputs + n_outputs; ++i) {
+    size_t bytes = i < n_inputs ? input_bytes[i] : output_bytes[i - n_inputs];
+    e = hipMalloc(&dev[i], bytes ? bytes : 4);
+    if (e != hipSuccess) {
+      cleanup();
+      return hip_fail(err, e, "hipMalloc");
+    }
+  }
+  for (size_t i = 0; i < n_inputs; ++i) {
+    if (!input_bytes[i]) continue;
+    e = hipMemcpyHtoDAsync(dev[i], const_cast<void *>(inputs[i]), input_bytes[i], stream);
+    if (e != hipSuccess) {
+      cleanup();
+      return hip_fail(err, e, "hipMemcpyHtoDAsync");
+    }
+  }
+  unsigned int blocks = (unsigned int)((programs + block - 1) / block);
+  rc = ph_launch_ptrs(k, blocks, (unsigned int)block, stream, dev.data(), dev.size(), err);
+  if (rc != PH_OK) {
+    cleanup();
+    return rc;
+  }
+  for (size_t i = 0; i < n_outputs; ++i) {
+    if (!output_bytes[i]) continue;
+    e = hipMemcpyDtoHAsync(outputs[i], dev[n_inputs + i], output_bytes[i], stream);
+    if (e != hipSuccess) {
+      cleanup();
+      return hip_fail(err, e, "hipMemcpyDtoHAsync");
+    }
+  }
+  e = hipStreamSynchronize(stream);
+  cleanup();
+  if (e != hipSuccess) return hip_fail(err, e, "hipStreamSynchronize");
+  return PH_OK;
+}
+
+int ph_device_count(int *count) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *count = n;
+  return PH_OK;
+}
+
+int ph_device_name(char *buf, size_t len) {
+  hipDeviceProp_t prop;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
+    return PH_ERR_RUNTIME;
+  std::snprintf(buf, len, "%s (%s)", prop.name, prop.gcnArchName);
+  return PH_OK;
+}
+
+int ph_malloc(size_t bytes, void **ptr, char **err) {
+  hipError_t e = hipMalloc(ptr, bytes ? bytes : 4);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipMalloc");
+}
+
+int ph_free(void *ptr) { return hipFree(ptr) == hipSuccess ? PH_OK : PH_ERR_RUNTIME; }
+
+int ph_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream, char **err) {
+  hipError_t e = hipMemcpyHtoDAsync(dst, const_cast<void *>(src), bytes, (hipStream_t)stream);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipMemcpyHtoDAsync");
+}
+
+int ph_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream, char **err) {
+  hipError_t e = hipMemcpyDtoHAsync(dst, const_cast<void *>(src), bytes, (hipStream_t)stream);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipMemcpyDtoHAsync");
+}
+
+int ph_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream, char **err) {
+  hipError_t e = hipMemcpyDtoDAsync(dst, const_cast<void *>(src), bytes, (hipStream_t)stream);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipMemcpyDtoDAsync");
+}
+
+int ph_stream_create(void **stream, char **err) {
+  hipStream_t s;
+  hipError_t e = hipStreamCreate(&s);
+  if (e != hipSuccess) return hip_fail(err, e, "hipStreamCreate");
+  *stream = s;
+  return PH_OK;
+}
+
+int ph_stream_destroy(void *stream) {
+  return hipStreamDestroy((hipStream_t)stream) == hipSuccess ? PH_OK : PH_ERR_RUNTIME;
+}
+
+int ph_stream_synchronize(void *stream, char **err) {
+  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipStreamSynchronize");
+}
+
+int ph_event_create(void **event, char **err) {
+  hipEvent_t ev;
+  hipError_t e = hipEventCreate(&ev);
+  if (e != hipSuccess) return hip_fail(err, e, "hipEventCreate");
+  *event = ev;
+  return PH_OK;
+}
+
+int ph_event_destroy(void *event) {
+  return hipEventDestroy((hipEvent_t)event) == hipSuccess ? PH_OK : PH_ERR_RUNTIME;
+}
+
+int ph_event_record(void *event, void *stream, char **err) {
+  hipError_t e = hipEventRecord((hipEvent_t)event, (hipStream_t)stream);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipEventRecord");
+}
+
+int ph_event_synchronize(void *event, char **err) {
+  hipError_t e = hipEventSynchronize((hipEvent_t)event);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipEventSynchronize");
+}
+
+int ph_event_query(void *event) {
+  hipError_t e = hipEventQuery((hipEvent_t)event);
+  if (e == hipSuccess) return 1;
+  if (e == hipErrorNotReady) return 0;
+  return -1;
+}
+
+int ph_event_elapsed_ms(void *start, void *stop, float *ms, char **err) {
+  hipError_t e = hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipEventElapsedTime");
+}
+
+int ph_device_synchronize(char **err) {
+  hipError_t e = hipDeviceSynchronize();
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipDeviceSynchronize");
+}
+
+int ph_stream_begin_capture(void *stream, char **err) {
+  hipError_t e = hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipStreamBeginCapture");
+}
+
+int ph_stream_end_capture(void *stream, void **graph_exec, char **err) {
+  hipGraph_t graph;
+  hipError_t e = hipStreamEndCapture((hipStream_t)stream, &graph);
+  if (e != hipSuccess) return hip_fail(err, e, "hipStreamEndCapture");
+  hipGraphExec_t exec;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  hipGraphDestroy(graph);
+  if (e != hipSuccess) return hip_fail(err, e, "hipGraphInstantiate");
+  *graph_exec = exec;
+  return PH_OK;
+}
+
+int ph_graph_launch(void *graph_exec, void *stream, char **err) {
+  hipError_t e = hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipGraphLaunch");
+}
+
+int ph_graph_destroy(void *graph_exec) {
+  return hipGraphExecDestroy((hipGraphExec_t)graph_exec) == hipSuccess ? PH_OK : PH_ERR_RUNTIME;
+}
+
+}  // extern "C"

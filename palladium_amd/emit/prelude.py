@@ -1,0 +1,128 @@
+"""Device-side helpers prepended to every emitted kernel.
+
+- `ph_threefry2x32`: Threefry-2x32 with 20 rounds (Salmon et al., SC'11),
+  the generator behind `jax.random` and the reference's emitted RNG
+  (`src/palladium/emit/rules.py:121-165`): rotations (13,15,26,6) /
+  (17,29,16,24), key schedule k0, k1, k0^k1^0x1BD11BDA with a round
+  counter added every four rounds.
+- `ph_pow`: under SAFE math (`PH_MATH_MODE == 0`) a deterministic power
+  function built only from IEEE double add/mul/div/fma, so a host build of
+  the same sequence returns bit-identical results; this is what makes
+  adaptive accept/reject decisions reproducible on the CPU. Under
+  RELAXED/FAST it is the device `powf`.
+  Method: x = m * 2^e with m in [sqrt(1/2), sqrt(2)); ln m = 2 atanh(t),
+  t = (m-1)/(m+1), as an odd series in t; exp by reduction z = k ln2 + r,
+  |r| <= ln2/2, and a degree-13 Taylor polynomial; both carried in double,
+  so the float result is the correctly rounded double value rounded once.
+- `ph_fmin`/`ph_fmax`: NaN-suppressing min/max (C fminf/fmaxf), the
+  reference's lowering of `min`/`max` (`src/palladium/emit/core.py:574-575`).
+"""
+
+PRELUDE = r"""
+#ifndef PH_MATH_MODE
+#define PH_MATH_MODE 2
+#endif
+
+__device__ __forceinline__ unsigned int ph_rotl32(unsigned int x, unsigned int r) {
+    return (x << r) | (x >> (32u - r));
+}
+
+__device__ __forceinline__ void ph_threefry2x32(unsigned int k0, unsigned int k1,
+                                                unsigned int c0, unsigned int c1,
+                                                unsigned int* o0, unsigned int* o1) {
+    const unsigned int k2 = k0 ^ k1 ^ 0x1BD11BDAu;
+    unsigned int x0 = c0 + k0;
+    unsigned int x1 = c1 + k1;
+#define PH_TF_ROUND(r) x0 += x1; x1 = ph_rotl32(x1, r); x1 ^= x0;
+    PH_TF_ROUND(13) PH_TF_ROUND(15) PH_TF_ROUND(26) PH_TF_ROUND(6)
+    x0 += k1; x1 += k2 + 1u;
+    PH_TF_ROUND(17) PH_TF_ROUND(29) PH_TF_ROUND(16) PH_TF_ROUND(24)
+    x0 += k2; x1 += k0 + 2u;
+    PH_TF_ROUND(13) PH_TF_ROUND(15) PH_TF_ROUND(26) PH_TF_ROUND(6)
+    x0 += k0; x1 += k1 + 3u;
+    PH_TF_ROUND(17) PH_TF_ROUND(29) PH_TF_ROUND(16) PH_TF_ROUND(24)
+    x0 += k1; x1 += k2 + 4u;
+    PH_TF_ROUND(13) PH_TF_ROUND(15) PH_TF_ROUND(26) PH_TF_ROUND(6)
+    x0 += k2; x1 += k0 + 5u;
+#undef PH_TF_ROUND
+    *o0 = x0;
+    *o1 = x1;
+}
+
+__device__ __forceinline__ float ph_fmin(float a, float b) { return fminf(a, b); }
+__device__ __forceinline__ float ph_fmax(float a, float b) { return fmaxf(a, b); }
+
+#if PH_MATH_MODE == 0
+__device__ __noinline__ double ph_ln_pos(double x) {
+    int e;
+    double m = frexp(x, &e);          /* x = m 2^e, m in [0.5, 1) */
+    if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
+    double t = (m - 1.0) / (m + 1.0);
+    double t2 = t * t;
+    double p = 1.0 / 23.0;
+    p = fma(p, t2, 1.0 / 21.0);
+    p = fma(p, t2, 1.0 / 19.0);
+    p = fma(p, t2, 1.0 / 17.0);
+    p = fma(p, t2, 1.0 / 15.0);
+    p = fma(p, t2, 1.0 / 13.0);
+    p = fma(p, t2, 1.0 / 11.0);
+    p = fma(p, t2, 1.0 / 9.0);
+    p = fma(p, t2, 1.0 / 7.0);
+    p = fma(p, t2, 1.0 / 5.0);
+    p = fma(p, t2, 1.0 / 3.0);
+    p = fma(p, t2, 1.0);
+    double lnm = 2.0 * t * p;
+    const double ln2_hi = 6.93147180369123816490e-01;
+    const double ln2_lo = 1.90821492927058770002e-10;
+    double de = (double)e;
+    return fma(de, ln2_hi, fma(de, ln2_lo, lnm));
+}
+
+__device__ __noinline__ double ph_exp_dbl(double z) {
+    const double inv_ln2 = 1.44269504088896338700e+00;
+    const double ln2_hi = 6.93147180369123816490e-01;
+    const double ln2_lo = 1.90821492927058770002e-10;
+    double kd = rint(z * inv_ln2);
+    double r = fma(-kd, ln2_hi, z);
+    r = fma(-kd, ln2_lo, r);
+    double p = 1.0 / 6227020800.0;        /* 1/13! */
+    p = fma(p, r, 1.0 / 479001600.0);
+    p = fma(p, r, 1.0 / 39916800.0);
+    p = fma(p, r, 1.0 / 3628800.0);
+    p = fma(p, r, 1.0 / 362880.0);
+    p = fma(p, r, 1.0 / 40320.0);
+    p = fma(p, r, 1.0 / 5040.0);
+    p = fma(p, r, 1.0 / 720.0);
+    p = fma(p, r, 1.0 / 120.0);
+    p = fma(p, r, 1.0 / 24.0);
+    p = fma(p, r, 1.0 / 6.0);
+    p = fma(p, r, 0.5);
+    p = fma(p, r, 1.0);
+    p = fma(p, r, 1.0);
+    return ldexp(p, (int)kd);
+}
+
+__device__ __noinline__ float ph_pow(float x, float y) {
+    if (y == 0.0f || x == 1.0f) return 1.0f;
+    if (x != x || y != y) return x + y;
+    float ax = fabsf(x);
+    float ay = fabsf(y);
+    bool y_int = (ay < 16777216.0f) ? (truncf(y) == y) : true;
+    bool y_odd = y_int && (ay < 16777216.0f) && (fmodf(ay, 2.0f) == 1.0f);
+    if (x < 0.0f && !y_int && ax != __builtin_inff()) return __builtin_nanf("");
+    if (ay == __builtin_inff()) {
+        if (ax == 1.0f) return 1.0f;
+        return ((ax > 1.0f) == (y > 0.0f)) ? __builtin_inff() : 0.0f;
+    }
+    float sign = (x < 0.0f && y_odd) ? -1.0f : 1.0f;
+    if (ax == 0.0f) return (y < 0.0f) ? sign * __builtin_inff() : sign * 0.0f;
+    if (ax == __builtin_inff()) return (y < 0.0f) ? sign * 0.0f : sign * __builtin_inff();
+    double z = (double)y * ph_ln_pos((double)ax);
+    if (z > 89.0) return sign * __builtin_inff();
+    if (z < -104.0) return sign * 0.0f;
+    return sign * (float)ph_exp_dbl(z);
+}
+#else
+__device__ __forceinline__ float ph_pow(float x, float y) { return powf(x, y); }
+#endif
+"""

@@ -1,0 +1,663 @@
+"""Lowering rules: one program instance per GPU lane.
+
+Every rule prints HIP C++ through the Cursor and binds its outvars in the
+Environment. Size-1 values are scalars, larger values local arrays whose
+element loops are fully unrolled (constant trip counts, so SROA keeps them
+in registers). Primitive semantics follow the reference's templates
+(`src/palladium/emit/core.py:568-601`, `src/palladium/emit/rules.py`),
+with each rule citing the reference rule it replaces.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Any, Callable
+
+import numpy as np
+
+from palladium_amd.emit.core import (
+    PRIMITIVE_INVARS,
+    REGISTER_BLOCK_LIMIT,
+    RULES,
+    Cursor,
+    CVal,
+    EmitError,
+    Environment,
+    ctype_of,
+    declare,
+    element_strides,
+    emit_jaxpr,
+    flat_index,
+    literal_cval,
+    ref_view,
+    rule,
+)
+from palladium_amd.ir import JaxprEqn, KeyAval, Literal, Var
+
+F32 = "float"
+
+
+def _is_float(c: CVal) -> bool:
+    return c.ctype == "float"
+
+
+# ---------------------------------------------------------------------------
+# element-wise templates. Fields a, b, c ... are the operands in jaxpr order.
+
+
+def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
+    f = _is_float(ops[0]) if ops else False
+    if opname == "add":
+        return "({a} + {b})"
+    if opname == "sub":
+        return "({a} - {b})"
+    if opname == "mul":
+        return "({a} * {b})"
+    if opname == "div":
+        return "({a} / {b})"
+    if opname == "rem":
+        return "fmodf({a}, {b})" if f else "({a} % {b})"
+    if opname == "min":
+        return "ph_fmin({a}, {b})" if f else "(({a} < {b}) ? {a} : {b})"
+    if opname == "max":
+        return "ph_fmax({a}, {b})" if f else "(({a} > {b}) ? {a} : {b})"
+    if opname == "pow":
+        return "ph_pow({a}, {b})"
+    if opname == "neg":
+        return "(-{a})"
+    if opname == "abs":
+        return "fabsf({a})" if f else "abs({a})"
+    if opname == "sign":
+        return "(({a} > 0.0f) ? 1.0f : (({a} < 0.0f) ? -1.0f : {a}))" if f else "(({a} > 0) - ({a} < 0))"
+    unary_f = {
+        "exp": "expf({a})",
+        "exp2": "exp2f({a})",
+        "log": "logf({a})",
+        "log1p": "log1pf({a})",
+        "expm1": "expm1f({a})",
+        "sin": "sinf({a})",
+        "cos": "cosf({a})",
+        "tan": "tanf({a})",
+        "tanh": "tanhf({a})",
+        "sqrt": "sqrtf({a})",
+        "rsqrt": "(1.0f / sqrtf({a}))",
+        "floor": "floorf({a})",
+        "ceil": "ceilf({a})",
+        "round": "roundf({a})",
+        "logistic": "(1.0f / (1.0f + expf(-{a})))",
+        "atan2": "atan2f({a}, {b})",
+    }
+    if opname in unary_f:
+        return unary_f[opname]
+    cmp = {"lt": "<", "le": "<=", "gt": ">", "ge": ">=", "eq": "==", "ne": "!="}
+    if opname in cmp:
+        return "({a} %s {b})" % cmp[opname]
+    if opname in ("and", "or", "xor"):
+        op = {"and": "&", "or": "|", "xor": "^"}[opname]
+        return "({a} %s {b})" % op
+    if opname == "not":
+        return "(!{a})" if ops[0].ctype == "bool" else "(~{a})"
+    if opname == "shift_right_logical":
+        if ops[0].ctype == "int":
+            return "((int)(((unsigned int){b} < 32u) ? ((unsigned int){a} >> {b}) : 0u))"
+        return "((((unsigned int){b}) < 32u) ? ({a} >> {b}) : 0u)"
+    if opname == "shift_right_arithmetic":
+        return "({a} >> (((unsigned int){b} < 32u) ? {b} : 31))"
+    if opname == "shift_left":
+        return "((((unsigned int){b}) < 32u) ? ({a} << {b}) : (%s)0)" % ops[0].ctype
+    if opname == "clamp":
+        # lax.clamp(min, x, max) = min(max(x, lo), hi)
+        if f:
+            return "ph_fmin(ph_fmax({b}, {a}), {c})"
+        return "((({b} > {a}) ? {b} : {a}) < {c} ? (({b} > {a}) ? {b} : {a}) : {c})"
+    raise EmitError(f"no element-wise template for {opname}")
+
+
+# The elementwise subset, for discoverability and rule registration.
+ELEMENTWISE = (
+    "add sub mul div rem min max pow neg abs sign exp exp2 log log1p expm1 sin cos "
+    "tan tanh sqrt rsqrt floor ceil round logistic atan2 lt le gt ge eq ne and or xor "
+    "not shift_right_logical shift_right_arithmetic shift_left clamp"
+).split()
+
+
+def _op_index(op: CVal, dst_shape: tuple[int, ...], idx_vars: list[str]) -> str:
+    """NumPy right-aligned broadcast of `op` against `dst_shape`."""
+    if op.size == 1:
+        return "0"
+    rank = len(dst_shape)
+    diff = rank - len(op.shape)
+    strides = element_strides(op.shape)
+    return flat_index([(idx_vars[d + diff], strides[d]) for d, s in enumerate(op.shape) if s != 1])
+
+
+def _emit_elementwise_loops(cursor: Cursor, dst: CVal, body: Callable[[list[str], str], None]) -> None:
+    rank = len(dst.shape)
+    if dst.size == 1:
+        body(["0"] * rank, "0")
+        return
+    strides = element_strides(dst.shape)
+    idx_vars: list[str] = []
+
+    def go(d: int) -> None:
+        if d == rank:
+            body(idx_vars, flat_index(list(zip(idx_vars, strides))))
+            return
+        with cursor.loop(dst.shape[d], f"_e{d}_") as i:
+            idx_vars.append(i)
+            go(d + 1)
+            idx_vars.pop()
+
+    go(0)
+
+
+def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """All pure element-wise primitives (reference: `_rule_elementwise`,
+    `src/palladium/emit/rules.py:274-351`). integer_pow expands to repeated
+    multiplication; convert/bitcast cast; operands broadcast NumPy-style."""
+    ops = [env.val(v) for v in eqn.invars]
+    opname = eqn.primitive.name
+    out = eqn.outvars[0]
+    dst_ctype = ctype_of(out.aval.dtype)
+    if opname == "integer_pow":
+        y = int(eqn.params["y"])
+        if y == 0:
+            template = "(%s)1" % dst_ctype
+        else:
+            body = " * ".join(["{a}"] * abs(y))
+            template = f"({body})" if y > 0 else f"(1.0f / ({body}))"
+    elif opname == "convert_element_type":
+        template = f"(({dst_ctype}){{a}})"
+        if dst_ctype == "bool":
+            template = "({a} != 0)"
+    elif opname == "bitcast_convert_type":
+        template = f"__builtin_bit_cast({dst_ctype}, {{a}})"
+    elif opname == "select_n":
+        if len(ops) == 3 and ops[0].ctype == "bool":
+            template = "({a} ? {c} : {b})"
+        else:
+            if ops[0].ctype == "bool" and len(ops) != 3:
+                raise EmitError("select_n with a bool predicate takes exactly two cases")
+            # Integer selector: case k for k, clamped like lax.select_n.
+            n = len(ops) - 1
+            fields = PRIMITIVE_INVARS[1 : 1 + n]
+            if n > len(PRIMITIVE_INVARS) - 1:
+                raise EmitError(f"select_n with {n} cases exceeds the supported arity")
+            expr = "{%s}" % fields[-1]
+            for k in reversed(range(n - 1)):
+                expr = "(({a} <= %d) ? {%s} : %s)" % (k, fields[k], expr)
+            template = expr
+    else:
+        template = _tmpl(opname, ops, dst_ctype)
+
+    n_fields = len({f for f in PRIMITIVE_INVARS if "{" + f + "}" in template})
+    if n_fields != len(ops):
+        raise EmitError(f"{opname} requires {n_fields} operands, got {len(ops)}")
+
+    dst_shape = tuple(int(d) for d in out.aval.shape)
+    if math.prod(dst_shape) == 1:
+        expr = template.format(**{n: o.at("0") for n, o in zip(PRIMITIVE_INVARS, ops)})
+        declare(env, cursor, out, init=expr)
+        return
+    dst = declare(env, cursor, out)
+
+    def body(idx_vars: list[str], flat: str) -> None:
+        vals = {n: o.at(_op_index(o, dst_shape, idx_vars)) for n, o in zip(PRIMITIVE_INVARS, ops)}
+        cursor.emit(f"{dst.at(flat)} = {template.format(**vals)};")
+
+    _emit_elementwise_loops(cursor, dst, body)
+
+
+for _name in [*ELEMENTWISE, "integer_pow", "convert_element_type", "bitcast_convert_type", "select_n"]:
+    RULES[_name] = _rule_elementwise
+
+
+# ---------------------------------------------------------------------------
+# memory
+
+
+def _indexer(eqn: JaxprEqn, start: int):
+    tree = eqn.params["tree"]
+    args = tree.unflatten(eqn.invars[start:])
+    return args[0] if args else None
+
+
+@rule("get")
+def _rule_get(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """Load from a Ref (reference: `src/palladium/emit/rules.py:38-69`).
+
+    Small blocks are loaded into registers once; read-only blocks larger
+    than REGISTER_BLOCK_LIMIT elements are aliased (pointer view), which is
+    safe because nothing writes through an input ref.
+    """
+    src = env.val(eqn.invars[0])
+    indexer = _indexer(eqn, 1)
+    view = ref_view(env, src, indexer) if indexer is not None else src
+    out = eqn.outvars[0]
+    out_shape = tuple(int(d) for d in out.aval.shape)
+    size = math.prod(out_shape)
+    if size == 1:
+        declare(env, cursor, out, init=view.at("0"))
+        return
+    if view.readonly and size > REGISTER_BLOCK_LIMIT:
+        env.bind(out, dataclasses.replace(view, shape=out_shape))
+        return
+    dst = declare(env, cursor, out)
+    cursor.copy(dst, view, size)
+
+
+@rule("swap")
+def _rule_swap(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """Store to a Ref (reference: `src/palladium/emit/rules.py:72-88`).
+    The outvar (the value the ref held before) is loaded only if used."""
+    ref = env.val(eqn.invars[0])
+    value = env.val(eqn.invars[1])
+    indexer = _indexer(eqn, 2)
+    dst = ref_view(env, ref, indexer) if indexer is not None else ref
+    if dst.readonly:
+        raise EmitError("cannot store into an input ref")
+    out = eqn.outvars[0]
+    size = math.prod(tuple(int(d) for d in out.aval.shape))
+    if env.used(out):
+        old = declare(env, cursor, out, init=dst.at("0")) if size == 1 else declare(env, cursor, out)
+        if size != 1:
+            cursor.copy(old, dst, size)
+    if value.size == 1 and size > 1:
+        with cursor.loop(size) as i:
+            cursor.emit(f"{dst.at(i)} = {value.at('0')};")
+    else:
+        cursor.copy(dst, value, size)
+
+
+# ---------------------------------------------------------------------------
+# structural
+
+
+@rule("broadcast_in_dim")
+def _rule_broadcast_in_dim(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """Size-preserving broadcasts alias; others materialise (reference:
+    `src/palladium/emit/rules.py:364-405`)."""
+    src = env.val(eqn.invars[0])
+    out = eqn.outvars[0]
+    shape = tuple(int(d) for d in eqn.params["shape"])
+    if src.size == math.prod(shape):
+        if src.scalar or src.space == "local" and src.size > 1 or src.space == "global":
+            env.bind(out, dataclasses.replace(src, shape=shape))
+            return
+        # A literal or expression: keep it as a scalar value.
+        env.bind(out, dataclasses.replace(src, shape=shape))
+        return
+    dst = declare(env, cursor, out)
+    bdims = tuple(eqn.params["broadcast_dimensions"])
+    s_strides = element_strides(src.shape)
+
+    def body(idx_vars: list[str], flat: str) -> None:
+        if src.size == 1:
+            cursor.emit(f"{dst.at(flat)} = {src.at('0')};")
+            return
+        sidx = flat_index([(idx_vars[od], s_strides[sd]) for sd, od in enumerate(bdims) if src.shape[sd] != 1])
+        cursor.emit(f"{dst.at(flat)} = {src.at(sidx)};")
+
+    _emit_elementwise_loops(cursor, dst, body)
+
+
+@rule("reshape", "squeeze", "expand_dims")
+def _rule_reshape(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """Row-major reinterpretation, no data movement (reference:
+    `src/palladium/emit/rules.py:204-219`)."""
+    if eqn.params.get("dimensions") is not None:
+        raise EmitError("reshape with a dimensions permutation is unimplemented")
+    src = env.val(eqn.invars[0])
+    shape = tuple(int(d) for d in eqn.outvars[0].aval.shape)
+    env.bind(eqn.outvars[0], dataclasses.replace(src, shape=shape))
+
+
+@rule("transpose")
+def _rule_transpose(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """Materialised permuted copy (reference: `src/palladium/emit/rules.py:222-271`)."""
+    src = env.val(eqn.invars[0])
+    perm = tuple(eqn.params["permutation"])
+    out = eqn.outvars[0]
+    if src.size == 1:
+        env.bind(out, dataclasses.replace(src, shape=tuple(int(d) for d in out.aval.shape)))
+        return
+    dst = declare(env, cursor, out)
+    s_strides = element_strides(src.shape)
+
+    def body(idx_vars: list[str], flat: str) -> None:
+        sidx = flat_index([(idx_vars[d], s_strides[perm[d]]) for d in range(len(perm))])
+        cursor.emit(f"{dst.at(flat)} = {src.at(sidx)};")
+
+    _emit_elementwise_loops(cursor, dst, body)
+
+
+@rule("program_id")
+def _rule_program_id(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """`pl.program_id(axis)` binds the decoded grid coordinate (reference:
+    `src/palladium/emit/rules.py:668-676`)."""
+    axis = int(eqn.params["axis"])
+    pids = getattr(env, "pids", None)
+    if pids is None or axis >= len(pids):
+        raise EmitError(f"program_id({axis}) outside a grid of rank {0 if pids is None else len(pids)}")
+    env.bind(eqn.outvars[0], pids[axis])
+
+
+@rule("num_programs")
+def _rule_num_programs(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    grid = getattr(env, "grid", None)
+    axis = int(eqn.params["axis"])
+    if grid is None:
+        raise EmitError("num_programs outside a kernel")
+    env.bind(eqn.outvars[0], literal_cval(grid[axis], np.int32))
+
+
+@rule("pjit", "jit", "closed_call", "core_call", "custom_jvp_call", "custom_vjp_call", "remat", "checkpoint")
+def _inline_call(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """Inline a nested call by walking its body (reference:
+    `src/palladium/emit/rules.py:91-103`)."""
+    inner = eqn.params.get("jaxpr") or eqn.params.get("call_jaxpr") or eqn.params.get("fun_jaxpr")
+    body = getattr(inner, "jaxpr", inner)
+    if getattr(inner, "consts", None):
+        raise EmitError(f"{eqn.primitive.name} with consts is unsupported")
+    invals = [env.val(v) for v in eqn.invars]
+    n = len(body.invars)
+    outs = emit_jaxpr(env, cursor, body, invals[-n:] if n < len(invals) else invals)
+    for ov, val in zip(eqn.outvars, outs):
+        env.bind(ov, val)
+
+
+# ---------------------------------------------------------------------------
+# random
+
+
+@rule("random_wrap", "random_unwrap")
+def _rule_random_alias(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """Key wrap/unwrap are type-level only (reference:
+    `src/palladium/emit/rules.py:106-118`)."""
+    src = env.val(eqn.invars[0])
+    if src.size != 2:
+        raise EmitError("only unbatched keys (uint32[2] key data) are supported")
+    env.bind(eqn.outvars[0], dataclasses.replace(src, shape=(2,)))
+
+
+def _key_words(cursor: Cursor, key: CVal) -> tuple[str, str]:
+    return key.at("0"), key.at("1")
+
+
+@rule("random_fold_in")
+def _rule_random_fold_in(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """New key = threefry(key, (0, data)) (reference: `src/palladium/emit/rules.py:188-201`)."""
+    key = env.val(eqn.invars[0])
+    data = env.val(eqn.invars[1])
+    k0, k1 = _key_words(cursor, key)
+    name = cursor.fresh("_key")
+    cursor.emit(f"unsigned int {name}[2];")
+    cursor.emit(f"ph_threefry2x32({k0}, {k1}, 0u, (unsigned int)({data.at('0')}), &{name}[0], &{name}[1]);")
+    env.bind(eqn.outvars[0], CVal(name, (2,), "unsigned int"))
+
+
+@rule("random_bits")
+def _rule_random_bits(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """bits[i] = x0 ^ x1 of threefry(key, (0, i)), i the flat row-major
+    index (reference: `src/palladium/emit/rules.py:168-185`)."""
+    if int(eqn.params.get("bit_width", 32)) != 32:
+        raise EmitError("random_bits: only bit_width=32 is implemented")
+    key = env.val(eqn.invars[0])
+    k0, k1 = _key_words(cursor, key)
+    out = eqn.outvars[0]
+    size = math.prod(tuple(int(d) for d in out.aval.shape))
+    a, b = cursor.fresh("_r"), cursor.fresh("_r")
+    if size == 1:
+        cursor.emit(f"unsigned int {a}, {b};")
+        cursor.emit(f"ph_threefry2x32({k0}, {k1}, 0u, 0u, &{a}, &{b});")
+        declare(env, cursor, out, init=f"{a} ^ {b}")
+        return
+    dst = declare(env, cursor, out)
+    with cursor.loop(size) as i:
+        cursor.emit(f"unsigned int {a}, {b};")
+        cursor.emit(f"ph_threefry2x32({k0}, {k1}, 0u, (unsigned int){i}, &{a}, &{b});")
+        cursor.emit(f"{dst.at(i)} = {a} ^ {b};")
+
+
+@rule("threefry2x32")
+def _rule_threefry2x32(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """Raw Threefry-2x32-20 block over broadcast uint32 operands
+    (k0, k1, x0, x1) -> (y0, y1)."""
+    ops = [env.val(v) for v in eqn.invars]
+    o0v, o1v = eqn.outvars
+    shape = tuple(int(d) for d in o0v.aval.shape)
+    if math.prod(shape) == 1:
+        a, b = cursor.fresh("_r"), cursor.fresh("_r")
+        cursor.emit(f"unsigned int {a}, {b};")
+        args = ", ".join(o.at("0") for o in ops)
+        cursor.emit(f"ph_threefry2x32({args}, &{a}, &{b});")
+        declare(env, cursor, o0v, init=a)
+        declare(env, cursor, o1v, init=b)
+        return
+    d0 = declare(env, cursor, o0v)
+    d1 = declare(env, cursor, o1v)
+
+    def body(idx_vars: list[str], flat: str) -> None:
+        args = ", ".join(o.at(_op_index(o, shape, idx_vars)) for o in ops)
+        cursor.emit(f"ph_threefry2x32({args}, &{d0.at(flat)}, &{d1.at(flat)});")
+
+    _emit_elementwise_loops(cursor, d0, body)
+
+
+# ---------------------------------------------------------------------------
+# reductions
+
+
+def _emit_reduce(env: Environment, cursor: Cursor, eqn: JaxprEqn, init: str, combine: Callable[[str, str], str]) -> None:
+    """Nested loops: kept dims outside, reduced dims accumulating inside
+    (reference: `_emit_reduce`, `src/palladium/emit/rules.py:595-642`)."""
+    axes = set(int(a) for a in eqn.params["axes"])
+    src = env.val(eqn.invars[0])
+    rank = len(src.shape)
+    kept = [d for d in range(rank) if d not in axes]
+    red = [d for d in range(rank) if d in axes]
+    out = eqn.outvars[0]
+    ctype = ctype_of(out.aval.dtype)
+    s_strides = element_strides(src.shape)
+    out_shape = tuple(int(d) for d in out.aval.shape)
+    d_strides = element_strides(out_shape)
+    scalar_out = math.prod(out_shape) == 1
+    dst = None if scalar_out else declare(env, cursor, out)
+    idx: dict[int, str] = {}
+
+    def loops(dims: list[int], body: Callable[[], None]) -> None:
+        if not dims:
+            body()
+            return
+        d = dims[0]
+        if src.shape[d] == 1:
+            idx[d] = "0"
+            loops(dims[1:], body)
+            return
+        with cursor.loop(src.shape[d], f"_d{d}_") as i:
+            idx[d] = i
+            loops(dims[1:], body)
+
+    result = {}
+
+    def accumulate() -> None:
+        acc = cursor.fresh("_acc")
+        cursor.emit(f"{ctype} {acc} = {init};")
+
+        def inner() -> None:
+            sidx = flat_index([(idx[d], s_strides[d]) for d in range(rank)])
+            cursor.emit(f"{acc} = {combine(acc, src.at(sidx))};")
+
+        loops(red, inner)
+        if scalar_out:
+            result["acc"] = acc
+        else:
+            didx = flat_index([(idx[d], d_strides[i]) for i, d in enumerate(kept)])
+            cursor.emit(f"{dst.at(didx)} = {acc};")
+
+    loops(kept, accumulate)
+    if scalar_out:
+        env.bind(out, CVal(result["acc"], out_shape, ctype))
+
+
+def _reduce_init(eqn: JaxprEqn, kind: str) -> str:
+    ct = ctype_of(eqn.outvars[0].aval.dtype)
+    if kind == "sum":
+        return "0.0f" if ct == "float" else "0"
+    if kind == "max":
+        return {"float": "(-__builtin_inff())", "int": "(-2147483647 - 1)", "unsigned int": "0u", "bool": "false"}[ct]
+    if kind == "min":
+        return {"float": "__builtin_inff()", "int": "2147483647", "unsigned int": "0xFFFFFFFFu", "bool": "true"}[ct]
+    return {"or": "false", "and": "true"}[kind]
+
+
+@rule("reduce_sum")
+def _rule_reduce_sum(env, cursor, eqn):
+    _emit_reduce(env, cursor, eqn, _reduce_init(eqn, "sum"), lambda a, x: f"{a} + {x}")
+
+
+@rule("reduce_max")
+def _rule_reduce_max(env, cursor, eqn):
+    f = ctype_of(eqn.outvars[0].aval.dtype) == "float"
+    _emit_reduce(env, cursor, eqn, _reduce_init(eqn, "max"),
+                 (lambda a, x: f"ph_fmax({a}, {x})") if f else (lambda a, x: f"(({x} > {a}) ? {x} : {a})"))
+
+
+@rule("reduce_min")
+def _rule_reduce_min(env, cursor, eqn):
+    f = ctype_of(eqn.outvars[0].aval.dtype) == "float"
+    _emit_reduce(env, cursor, eqn, _reduce_init(eqn, "min"),
+                 (lambda a, x: f"ph_fmin({a}, {x})") if f else (lambda a, x: f"(({x} < {a}) ? {x} : {a})"))
+
+
+@rule("reduce_or")
+def _rule_reduce_or(env, cursor, eqn):
+    _emit_reduce(env, cursor, eqn, "false", lambda a, x: f"({a} || {x})")
+
+
+@rule("reduce_and")
+def _rule_reduce_and(env, cursor, eqn):
+    _emit_reduce(env, cursor, eqn, "true", lambda a, x: f"({a} && {x})")
+
+
+# ---------------------------------------------------------------------------
+# control flow
+
+
+def _declare_carries(env: Environment, cursor: Cursor, invars: list[Any], outvars: list[Var]) -> list[CVal]:
+    carries = []
+    for iv, ov in zip(invars, outvars):
+        src = env.val(iv)
+        if isinstance(ov.aval, KeyAval) or src.size != 1 or math.prod(ov.aval.shape) != 1:
+            dst = declare(env, cursor, ov)
+            cursor.copy(dst, src, dst.size)
+        else:
+            dst = declare(env, cursor, ov, init=src.at("0"))
+        carries.append(dst)
+    return carries
+
+
+def copy_back_carries(cursor: Cursor, outs: list[CVal], carries: list[CVal]) -> None:
+    """Simultaneous carry update: read every new value into a temporary,
+    then write all carries (reference: `src/palladium/emit/rules.py:741-809`;
+    the Metal `volatile` workaround is not needed here)."""
+    updates = [(o, c) for o, c in zip(outs, carries) if o.expr != c.expr]
+    staged = []
+    for out, carry in updates:
+        if carry.size == 1:
+            t = cursor.fresh("_cb")
+            cursor.emit(f"const {carry.ctype} {t} = {out.at('0')};")
+            staged.append((carry, t, None))
+        else:
+            t = cursor.fresh("_cb")
+            cursor.emit(f"{carry.ctype} {t}[{carry.size}];")
+            tv = CVal(t, carry.shape, carry.ctype)
+            cursor.copy(tv, out, carry.size)
+            staged.append((carry, t, tv))
+    for carry, t, tv in staged:
+        if tv is None:
+            cursor.emit(f"{carry.at('0')} = {t};")
+        else:
+            cursor.copy(carry, tv, carry.size)
+
+
+@rule("scan")
+def _rule_scan(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """`fori_loop` / pure-carry `scan` -> a counted for-loop; consts pass
+    through, carries become mutable locals (reference:
+    `src/palladium/emit/rules.py:679-714`)."""
+    length = int(eqn.params["length"])
+    body = eqn.params["jaxpr"]
+    body_j = getattr(body, "jaxpr", body)
+    if eqn.params.get("reverse", False):
+        raise EmitError("no reverse-mode scan support, use lax.fori_loop")
+    num_carry = len(eqn.outvars)
+    num_consts = len(eqn.invars) - num_carry
+    if len(body_j.outvars) != num_carry:
+        raise EmitError("lax.scan with stacked ys not supported, use lax.fori_loop")
+    for ov, bv in zip(eqn.outvars, body_j.outvars):
+        if tuple(ov.aval.shape) != tuple(getattr(bv, "aval").shape):
+            raise EmitError("lax.scan with stacked ys not supported, use lax.fori_loop")
+    for iv, bv in zip(eqn.invars, body_j.invars):
+        if tuple(getattr(iv.aval, "shape", ())) != tuple(getattr(bv.aval, "shape", ())):
+            raise EmitError("lax.scan with scanned xs not supported, use lax.fori_loop")
+    consts = [env.val(v) for v in eqn.invars[:num_consts]]
+    carries = _declare_carries(env, cursor, eqn.invars[num_consts:], eqn.outvars)
+    unroll = eqn.params.get("unroll", 1)
+    if isinstance(unroll, bool):
+        unroll = length if unroll else 1
+    idx = cursor.fresh("_s")
+    if int(unroll) > 1:
+        cursor.emit(f"#pragma unroll {int(unroll)}")
+    with cursor.block(f"for (int {idx} = 0; {idx} < {length}; ++{idx})"):
+        outs = emit_jaxpr(env, cursor, body_j, consts + carries)
+        copy_back_carries(cursor, outs, carries)
+
+
+@rule("while")
+def _rule_while(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """`while_loop` -> `while (true) { cond; if (!p) break; body; }`. Each
+    lane iterates independently; the wavefront retires when its last lane
+    exits (reference: `src/palladium/emit/rules.py:812-844`)."""
+    cn = int(eqn.params["cond_nconsts"])
+    bn = int(eqn.params["body_nconsts"])
+    cj = eqn.params["cond_jaxpr"]
+    bj = eqn.params["body_jaxpr"]
+    if getattr(cj, "consts", None) or getattr(bj, "consts", None):
+        raise EmitError("while with jaxpr consts is unsupported")
+    cond_consts = [env.val(v) for v in eqn.invars[:cn]]
+    body_consts = [env.val(v) for v in eqn.invars[cn : cn + bn]]
+    carries = _declare_carries(env, cursor, eqn.invars[cn + bn :], eqn.outvars)
+    with cursor.block("while (true)"):
+        (pred,) = emit_jaxpr(env, cursor, getattr(cj, "jaxpr", cj), cond_consts + carries)
+        with cursor.block(f"if (!({pred.at('0')}))"):
+            cursor.emit("break;")
+        outs = emit_jaxpr(env, cursor, getattr(bj, "jaxpr", bj), body_consts + carries)
+        copy_back_carries(cursor, outs, carries)
+
+
+@rule("cond")
+def _rule_cond(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """`cond`/`switch` -> if / else-if / else over the clamped index
+    (reference: `src/palladium/emit/rules.py:847-878`)."""
+    branches = eqn.params["branches"]
+    index = env.val(eqn.invars[0])
+    ops = [env.val(v) for v in eqn.invars[1:]]
+    outs = [declare(env, cursor, ov) for ov in eqn.outvars]
+    n = len(branches)
+    for i, br in enumerate(branches):
+        if getattr(br, "consts", None):
+            raise EmitError("cond with jaxpr consts is unsupported")
+        if n == 1:
+            header = "if (true)"
+        elif i == 0:
+            header = f"if ({index.at('0')} <= 0)"
+        elif i < n - 1:
+            header = f"else if ({index.at('0')} == {i})"
+        else:
+            header = "else"
+        with cursor.block(header):
+            vals = emit_jaxpr(env, cursor, getattr(br, "jaxpr", br), list(ops))
+            for o, v in zip(outs, vals):
+                cursor.copy(o, v, o.size)

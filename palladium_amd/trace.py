@@ -1,0 +1,176 @@
+"""Step 1 of the pipeline: a pallas_call to a KernelSpec.
+
+Same contract as the reference tracer (`src/palladium/trace.py:26-177`):
+a KernelSpec carries the kernel jaxpr over Refs, the grid (`(1,)` when
+gridless), and per-operand BlockInfo (kernel-visible block shape,
+full array shape, dtype, index-map jaxpr in units of blocks).
+
+Two sources are accepted:
+- a `palladium_amd.frontend.pl.PallasCall` (the JAX-free frontend);
+- with JAX importable, any callable that invokes exactly one
+  `jax.experimental.pallas.pallas_call` (see `palladium_amd.jax_adapter`).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Any, Callable
+
+import numpy as np
+
+from palladium_amd.errors import TraceError
+from palladium_amd.frontend import pl as _pl
+from palladium_amd.frontend.core import Builder, building, check_dtype
+from palladium_amd.ir import ClosedJaxpr, Jaxpr, RefAval
+
+__all__ = ["BlockInfo", "KernelSpec", "trace"]
+
+
+@dataclasses.dataclass(frozen=True)
+class BlockInfo:
+    """One kernel operand: the block a single program instance sees.
+
+    Attributes
+    ----------
+    block_shape : tuple of int
+        Kernel-visible block shape, squeezed dims removed.
+    array_shape : tuple of int
+        Full array shape.
+    dtype : numpy.dtype
+        Element type, shared by block and array.
+    index_map_jaxpr : ClosedJaxpr
+        Staged BlockSpec index map: grid indices to block index, in
+        units of blocks.
+    full_block_shape : tuple of int
+        Block shape with squeezed dims restored as 1 (rank of the array).
+    """
+
+    block_shape: tuple[int, ...]
+    array_shape: tuple[int, ...]
+    dtype: np.dtype
+    index_map_jaxpr: ClosedJaxpr
+    full_block_shape: tuple[int, ...] | None = None
+
+    def full_block(self) -> tuple[int, ...]:
+        if self.full_block_shape is not None:
+            return self.full_block_shape
+        missing = len(self.array_shape) - len(self.block_shape)
+        return (1,) * missing + tuple(self.block_shape)
+
+
+@dataclasses.dataclass(frozen=True)
+class KernelSpec:
+    """Everything the emitter needs.
+
+    Attributes
+    ----------
+    name : str
+        Kernel name, used as the HIP entry point name.
+    jaxpr : Jaxpr
+        The kernel body: a stateful jaxpr over Refs (inputs then outputs).
+    grid : tuple of int
+        Pallas grid; `(1,)` for gridless calls.
+    inputs, outputs : tuple of BlockInfo
+        Operand descriptions in jaxpr order.
+    raw_params : dict
+        Extra pallas_call parameters.
+    """
+
+    name: str
+    jaxpr: Jaxpr
+    grid: tuple[int, ...]
+    inputs: tuple[BlockInfo, ...]
+    outputs: tuple[BlockInfo, ...]
+    raw_params: dict[str, Any]
+
+    @property
+    def num_programs(self) -> int:
+        """Total number of program instances (one GPU thread each)."""
+        return math.prod(self.grid)
+
+
+def _shape_dtype(a: Any) -> tuple[tuple[int, ...], np.dtype]:
+    shape = tuple(int(s) for s in getattr(a, "shape", np.shape(a)))
+    dtype = getattr(a, "dtype", None)
+    if dtype is None:
+        dtype = np.asarray(a).dtype
+    return shape, np.dtype(dtype)
+
+
+def _trace_frontend(call: "_pl.PallasCall", example_args: tuple) -> KernelSpec:
+    grid = call.grid or (1,)
+    in_sd = [_shape_dtype(a) for a in example_args]
+    for i, (_, dt) in enumerate(in_sd):
+        try:
+            check_dtype(dt)
+        except TraceError as e:
+            raise TraceError(f"argument {i}: {e}") from None
+    out_sd = [(s.shape, s.dtype) for s in call.out_shapes]
+    in_specs = call._spec_list(call.in_specs, len(in_sd), "in_specs")
+    out_specs = call._spec_list(call.out_specs, len(out_sd), "out_specs")
+
+    def infos(specs, sds) -> tuple[BlockInfo, ...]:
+        out = []
+        for spec, (shape, dtype) in zip(specs, sds):
+            dims = _pl.block_dims(spec.block_shape if spec is not None else None, shape)
+            block = tuple(d for d in dims if d is not None)
+            full = tuple(1 if d is None else d for d in dims)
+            imj = _pl.trace_index_map(spec, grid if call.grid else (), len(shape))
+            out.append(BlockInfo(block, shape, dtype, imj, full))
+        return tuple(out)
+
+    inputs = infos(in_specs, in_sd)
+    outputs = infos(out_specs, out_sd)
+    b = Builder(None)
+    prev = _pl._grid_state.grid
+    _pl._grid_state.grid = grid
+    try:
+        with building(b):
+            refs = _pl.kernel_refs(b, [RefAval(i.block_shape, i.dtype) for i in (*inputs, *outputs)])
+            call.kernel(*refs)
+    finally:
+        _pl._grid_state.grid = prev
+    jaxpr = Jaxpr([], b.invars, [], b.eqns)
+    name = call.name or getattr(call.kernel, "__name__", None) or "palladium_kernel"
+    if not name.isidentifier() or name == "<lambda>":
+        name = "palladium_kernel"
+    return KernelSpec(
+        name=name,
+        jaxpr=jaxpr,
+        grid=tuple(grid),
+        inputs=inputs,
+        outputs=outputs,
+        raw_params={"grid": call.grid},
+    )
+
+
+def trace(pallas_fn: Callable, *example_args: Any) -> KernelSpec:
+    """Extract a KernelSpec from a staged pallas_call.
+
+    Parameters
+    ----------
+    pallas_fn : PallasCall or callable
+        `palladium_amd.frontend.pl.pallas_call(...)`, or (with JAX
+        importable) any function invoking exactly one JAX pallas_call.
+    *example_args
+        Arrays or ShapeDtypeStructs fixing shapes and dtypes; no data is read.
+
+    Raises
+    ------
+    TraceError
+        Zero or several pallas_calls, scalar prefetch, unsupported block
+        dims or dtypes.
+    """
+    if isinstance(pallas_fn, _pl.PallasCall):
+        return _trace_frontend(pallas_fn, example_args)
+    try:
+        import jax  # noqa: F401
+    except ImportError:
+        raise TraceError(
+            "no pallas_call found: pass palladium_amd.frontend.pl.pallas_call(...) "
+            "(JAX is not importable here, so JAX pallas_calls cannot be traced)"
+        ) from None
+    from palladium_amd.jax_adapter import trace_jax
+
+    return trace_jax(pallas_fn, *example_args)
