@@ -367,8 +367,8 @@ def _xcd_remap(nblocks: int) -> list[str]:
         return ["const unsigned int _blk = blockIdx.x;"]
     per, rem = divmod(nblocks, NUM_XCDS)
     return [
-        "const unsigned int _xcd = blockIdx.x % %du;" % NUM_XCDS,
-        "const unsigned int _slot = blockIdx.x / %du;" % NUM_XCDS,
+        f"const unsigned int _xcd = blockIdx.x % {NUM_XCDS}u;",
+        f"const unsigned int _slot = blockIdx.x / {NUM_XCDS}u;",
         f"const unsigned int _blk = (_xcd < {rem}u) ? _xcd * {per + 1}u + _slot"
         f" : {rem * (per + 1)}u + (_xcd - {rem}u) * {per}u + _slot;",
     ]

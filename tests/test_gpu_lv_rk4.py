@@ -1,0 +1,47 @@
+"""RK4 Lotka-Volterra on the GPU against the C oracle.
+
+SAFE math keeps IEEE op order with no contraction, so the emitted kernel
+must reproduce oracle/oracle.c bit for bit; FAST contracts and reassociates,
+so it is held to a relative tolerance instead (the reference's honest bar
+for FAST is rtol=1e-3, tests/test_06_capstone_rk4.py:66-76; ours is 1e-4).
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+import palladium_amd as pa
+from palladium_amd.workloads import LV_CFG0, lv_inputs, lv_rk4_call
+
+pytestmark = pytest.mark.gpu
+
+
+def test_safe_bit_exact_vs_oracle_cfg0_sample():
+    n = 4096
+    args = lv_inputs(n, LV_CFG0.seed)
+    f = lv_rk4_call(n, LV_CFG0.dt, LV_CFG0.steps, math_mode=pa.MathMode.SAFE)
+    gx, gy = f(*args)
+    wx, wy = oracle.lv_rk4(*args, LV_CFG0.dt, LV_CFG0.steps)
+    np.testing.assert_array_equal(gx, wx)
+    np.testing.assert_array_equal(gy, wy)
+
+
+def test_safe_max_abs_y_bit_exact():
+    n = 1000  # ragged against the 256-lane workgroup
+    args = lv_inputs(n, 1)
+    f = lv_rk4_call(n, 0.005, 400, track_max=True, math_mode="safe")
+    gx, gy, gm = f(*args)
+    wx, wy, wm = oracle.lv_rk4(*args, 0.005, 400, track_max=True)
+    np.testing.assert_array_equal(gx, wx)
+    np.testing.assert_array_equal(gy, wy)
+    np.testing.assert_array_equal(gm, wm)
+
+
+def test_fast_within_tolerance():
+    n = 8192
+    args = lv_inputs(n, 0)
+    f = lv_rk4_call(n, 0.01, 1000)
+    gx, gy = f(*args)
+    wx, wy = oracle.lv_rk4(*args, 0.01, 1000)
+    np.testing.assert_allclose(gx, wx, rtol=1e-4, atol=1e-6)
+    np.testing.assert_allclose(gy, wy, rtol=1e-4, atol=1e-6)
