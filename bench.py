@@ -128,6 +128,125 @@ def bench_lv(steps: int, warmup: int, cpu: bool) -> dict:
     return result
 
 
+def _timed_launches(bound, ops, steps: int, warmup: int):
+    from palladium_amd import runtime as rt
+
+    stream = bound.stream
+    for _ in range(warmup):
+        bound.launch_device(*ops, stream=stream)
+    stream.synchronize()
+    evs = [rt.Event() for _ in range(steps + 1)]
+    evs[0].record(stream)
+    for k in range(steps):
+        bound.launch_device(*ops, stream=stream)
+        evs[k + 1].record(stream)
+    stream.synchronize()
+    per = [evs[k].elapsed_ms(evs[k + 1]) for k in range(steps)]
+    return evs[0].elapsed_ms(evs[-1]) / steps, float(np.mean(per))
+
+
+def _base(metric: str, value: float, unit: str, steps: int, warmup: int, ms: float, config: dict) -> dict:
+    return {
+        "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded)", "config": config,
+    }
+
+
+def bench_gbm(steps: int, warmup: int, cpu: bool) -> dict:
+    from palladium_amd import runtime as rt
+    from palladium_amd.frontend import random
+    from palladium_amd.workloads import GBM_CFG, gbm_call
+
+    cfg = GBM_CFG
+    key = random.key(cfg.seed)
+    bound = gbm_call(cfg).bound(key)
+    ops = [rt.Buffer.from_numpy(key), rt.Buffer.empty((cfg.n_paths,), np.float32)]
+    ms, avg = _timed_launches(bound, ops, steps, warmup)
+    ps = cfg.n_paths * cfg.n_steps
+    res = _base("GBM path-steps/s (4,194,304 paths x 252 steps, Threefry + Box-Muller, fp32)", ps / (ms / 1e3),
+                "path-steps/s", steps, warmup, ms,
+                {"workload": "GBM Monte Carlo, config 3", "paths": cfg.n_paths, "steps": cfg.n_steps, "math_mode": "fast"})
+    res["roofline"] = {"bound": "valu", "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None,
+                       "avg_launch_ms": avg}
+    if cpu:
+        import oracle
+
+        n_cpu = 65536
+        oracle.gbm(cfg, 64)
+        t0 = time.perf_counter()
+        oracle.gbm(cfg, n_cpu)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": n_cpu * cfg.n_steps / dt, "unit": "path-steps/s", "cores": _cpu_cores(),
+                               "kind": "port", "sample": f"{n_cpu} paths x {cfg.n_steps} steps, C oracle, {dt:.2f} s"}
+    return res
+
+
+def bench_gs(steps: int, warmup: int, cpu: bool) -> dict:
+    from palladium_amd.workloads import GS_BYTES_PER_CELL_STEP, GS_CFG, gray_scott_call, gray_scott_initial, gray_scott_run
+
+    cfg = GS_CFG
+    u0, v0 = gray_scott_initial(cfg.size)
+    call = gray_scott_call(cfg)
+    gray_scott_run(call, u0, v0, 10)  # compile + warm
+    n_steps = cfg.steps
+    _, v, gpu_s = gray_scott_run(call, u0, v0, n_steps, graph=True)
+    cells = cfg.size * cfg.size
+    ms = gpu_s * 1e3 / n_steps
+    achieved = GS_BYTES_PER_CELL_STEP * cells / (ms / 1e3)
+    res = _base("Gray-Scott cell-steps/s (4096^2, 2,000 steps, fp32)", cells / (ms / 1e3), "cell-steps/s",
+                n_steps, 10, ms, {"workload": "Gray-Scott 4096x4096, 2000 steps as one HIP graph, config 4",
+                                  "size": cfg.size, "math_mode": "fast"})
+    res["roofline"] = {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                       "frac": achieved / HBM_PEAK, "traffic": None, "bytes_per_cell_step": GS_BYTES_PER_CELL_STEP,
+                       "avg_launch_ms": ms}
+    res["pattern_energy"] = float(np.sum(v, dtype=np.float64))
+    if cpu:
+        import oracle
+
+        size = 1024
+        su, sv = gray_scott_initial(size)
+        t0 = time.perf_counter()
+        oracle.gray_scott(su, sv, cfg, 20)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": size * size * 20 / dt, "unit": "cell-steps/s", "cores": _cpu_cores(),
+                               "kind": "port", "sample": f"{size}^2 grid x 20 steps, C oracle, {dt:.2f} s"}
+    return res
+
+
+def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
+    from palladium_amd import runtime as rt
+    from palladium_amd.workloads import BS3_CFG, bs3_inputs, bs3_vdp_call
+
+    cfg = BS3_CFG
+    host = bs3_inputs(cfg.n)
+    bound = bs3_vdp_call(cfg.n).bound(*host)
+    ins = [rt.Buffer.from_numpy(a) for a in host]
+    outs = [rt.Buffer.empty((cfg.n,), np.float32) for _ in range(3)] + [rt.Buffer.empty((cfg.n,), np.int32) for _ in range(2)]
+    ms, avg = _timed_launches(bound, ins + outs, steps, warmup)
+    acc = outs[3].to_numpy().astype(np.int64)
+    rej = outs[4].to_numpy().astype(np.int64)
+    attempts = acc + rej
+    waves = attempts[: (cfg.n // 64) * 64].reshape(-1, 64)
+    active = float(waves.sum() / (waves.max(axis=1).sum() * 64))
+    total = int(attempts.sum())
+    res = _base("BS3(2)+PI attempted steps/s (Van der Pol, N=262,144, fp32)", total / (ms / 1e3), "attempts/s",
+                steps, warmup, ms, {"workload": "adaptive BS3(2) Van der Pol, config 2", "n": cfg.n, "math_mode": "fast"})
+    res["roofline"] = {"bound": "valu", "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None,
+                       "avg_launch_ms": avg, "active_lane_fraction": active, "total_attempts": total,
+                       "accepted": int(acc.sum()), "rejected": int(rej.sum())}
+    if cpu:
+        import oracle
+
+        n_cpu = 16384
+        t0 = time.perf_counter()
+        a2 = oracle.bs3_vdp(*(h[:n_cpu] for h in host), cfg)
+        dt = time.perf_counter() - t0
+        res["cpu_baseline"] = {"value": float((a2[3].astype(np.int64) + a2[4]).sum() / dt), "unit": "attempts/s",
+                               "cores": _cpu_cores(), "kind": "port", "sample": f"first {n_cpu} trajectories, C oracle, {dt:.2f} s"}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -144,10 +263,10 @@ def main() -> int:
         )
         return 2
     rank = int(os.environ.get("RANK", "0"))
-    if a.workload == "lv":
-        res = bench_lv(a.steps, a.warmup, cpu=not a.no_cpu and rank == 0)
-    else:
-        raise SystemExit(f"unknown workload {a.workload}")
+    fns = {"lv": bench_lv, "gbm": bench_gbm, "gs": bench_gs, "bs3": bench_bs3}
+    if a.workload not in fns:
+        raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")
+    res = fns[a.workload](a.steps, a.warmup, cpu=not a.no_cpu and rank == 0)
     if rank == 0:
         print(json.dumps(res), flush=True)
     return 0

@@ -81,3 +81,89 @@ def fold_in(key, data: int) -> np.ndarray:
 
 def bits_to_uniform(bits: int, lo: float = 0.0, hi: float = 1.0) -> np.float32:
     return np.float32(lib().oracle_bits_to_uniform(int(bits), lo, hi))
+
+
+_I = ctypes.POINTER(ctypes.c_int32)
+
+
+def _declare_more(L):
+    f, l, u = ctypes.c_float, ctypes.c_long, ctypes.c_uint32
+    L.oracle_gbm.argtypes = [l, l, l, u, u, f, f, f, f, f, _F]
+    L.oracle_pow.argtypes = [f, f]
+    L.oracle_pow.restype = f
+    L.oracle_bs3_vdp.argtypes = [l, _F, _F, _F, f, f, f, f, l, _F, _F, _F, _I, _I]
+    L.oracle_gray_scott_step.argtypes = [l, _F, _F, f, f, f, f, f, _F, _F]
+    L.oracle_gray_scott.argtypes = [l, l, _F, _F, _F, _F, f, f, f, f, f]
+    L.oracle_df32_add.argtypes = [l] + [_F] * 6
+    L.oracle_df32_mul.argtypes = [l] + [_F] * 6
+    L.oracle_lv_rk4_df32.argtypes = [l] + [_F] * 6 + [f, l] + [_F] * 4
+
+
+def _lib2():
+    L = lib()
+    if not getattr(L, "_more", False):
+        _declare_more(L)
+        L._more = True
+    return L
+
+
+def gbm(cfg, n_paths: int, first_path: int = 0) -> np.ndarray:
+    """Per-path undiscounted call payoff for paths [first, first+n)."""
+    out = np.empty(n_paths, np.float32)
+    key = (0, cfg.seed)
+    two_pi = float(np.float32(2.0 * np.pi))
+    _lib2().oracle_gbm(n_paths, first_path, cfg.n_steps, key[0], key[1], float(np.float32(cfg.s0)),
+                       float(np.float32(cfg.strike)), float(np.float32(cfg.drift_dt)),
+                       float(np.float32(cfg.vol_sqdt)), two_pi, _fp(out))
+    return out
+
+
+def pow32(x: float, y: float) -> np.float32:
+    return np.float32(_lib2().oracle_pow(float(x), float(y)))
+
+
+def bs3_vdp(x0, v0, mu, cfg):
+    n = x0.size
+    outs = [np.empty(n, np.float32) for _ in range(3)] + [np.empty(n, np.int32) for _ in range(2)]
+    a = [np.ascontiguousarray(v, np.float32) for v in (x0, v0, mu)]
+    f32 = lambda v: float(np.float32(v))  # noqa: E731
+    _lib2().oracle_bs3_vdp(n, *[_fp(v) for v in a], f32(cfg.t1), f32(cfg.dt0), f32(cfg.rtol), f32(cfg.atol),
+                           int(cfg.max_attempts), _fp(outs[0]), _fp(outs[1]), _fp(outs[2]),
+                           outs[3].ctypes.data_as(_I), outs[4].ctypes.data_as(_I))
+    return tuple(outs)
+
+
+def _gs_consts(cfg):
+    f32 = lambda v: float(np.float32(v))  # noqa: E731
+    return f32(cfg.du), f32(cfg.dv), f32(cfg.f), f32(cfg.f + cfg.k), f32(cfg.dt)
+
+
+def gray_scott(u0, v0, cfg, steps: int):
+    n = u0.shape[0]
+    u = np.ascontiguousarray(u0, np.float32).copy()
+    v = np.ascontiguousarray(v0, np.float32).copy()
+    tu, tv = np.empty_like(u), np.empty_like(v)
+    _lib2().oracle_gray_scott(n, steps, _fp(u), _fp(v), _fp(tu), _fp(tv), *_gs_consts(cfg))
+    return u, v
+
+
+def df32_add(ah, al, bh, bl):
+    n = ah.size
+    oh, ol = np.empty(n, np.float32), np.empty(n, np.float32)
+    _lib2().oracle_df32_add(n, *[_fp(np.ascontiguousarray(x, np.float32)) for x in (ah, al, bh, bl)], _fp(oh), _fp(ol))
+    return oh, ol
+
+
+def df32_mul(ah, al, bh, bl):
+    n = ah.size
+    oh, ol = np.empty(n, np.float32), np.empty(n, np.float32)
+    _lib2().oracle_df32_mul(n, *[_fp(np.ascontiguousarray(x, np.float32)) for x in (ah, al, bh, bl)], _fp(oh), _fp(ol))
+    return oh, ol
+
+
+def lv_rk4_df32(x0, y0, a, b, c, d, dt: float, steps: int):
+    n = x0.size
+    arrs = [np.ascontiguousarray(v, np.float32) for v in (x0, y0, a, b, c, d)]
+    outs = [np.empty(n, np.float32) for _ in range(4)]
+    _lib2().oracle_lv_rk4_df32(n, *[_fp(v) for v in arrs], float(np.float32(dt)), int(steps), *[_fp(o) for o in outs])
+    return tuple(outs)

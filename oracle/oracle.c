@@ -122,3 +122,345 @@ float oracle_bits_to_uniform(uint32_t bits, float lo, float hi) {
   f = f + lo;
   return fmaxf(lo, f);
 }
+
+/* ------------------------------------------------------------------------
+ * GBM Monte Carlo, one path per call index (examples/03_sde_montecarlo.py:
+ * 97-119 restated with the configured counter layout): per step one
+ * Threefry block over counter (path, step) gives two uint32; each becomes
+ * a uniform through JAX's conversion; u1 is floored at 1e-7; Box-Muller
+ * z = sqrt(-2 ln u1) cos(2 pi u2); s <- s * exp(drift + vol z).
+ * Op order matches palladium_amd.workloads.gbm_kernel.
+ * ---------------------------------------------------------------------- */
+void oracle_gbm(long n_paths, long first_path, long n_steps, uint32_t k0, uint32_t k1,
+                float s0, float strike, float drift, float vol, float two_pi,
+                float *payoff) {
+#pragma omp parallel for schedule(static)
+  for (long p = 0; p < n_paths; ++p) {
+    uint32_t path = (uint32_t)(first_path + p);
+    float s = s0;
+    for (long i = 0; i < n_steps; ++i) {
+      uint32_t b0, b1;
+      oracle_threefry2x32(k0, k1, path, (uint32_t)i, &b0, &b1);
+      float u1 = oracle_bits_to_uniform(b0, 0.0f, 1.0f);
+      u1 = fmaxf(u1, 1e-7f);
+      float u2 = oracle_bits_to_uniform(b1, 0.0f, 1.0f);
+      float l = logf(u1);
+      float r = sqrtf(-2.0f * l);
+      float c = cosf(two_pi * u2);
+      float z = r * c;
+      float e = expf(drift + vol * z);
+      s = s * e;
+    }
+    float d = s - strike;
+    payoff[p] = fmaxf(d, 0.0f);
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * Deterministic pow, the same sequence as the SAFE-mode device ph_pow
+ * (palladium_amd/emit/prelude.py): double-precision ln via the atanh series
+ * and exp via k ln2 + r reduction and a degree-13 Taylor polynomial, all in
+ * IEEE double with explicit fma. Pinned against libm pow in tests.
+ * ---------------------------------------------------------------------- */
+static double ph_ln_pos(double x) {
+  int e;
+  double m = frexp(x, &e);
+  if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
+  double t = (m - 1.0) / (m + 1.0);
+  double t2 = t * t;
+  double p = 1.0 / 23.0;
+  p = fma(p, t2, 1.0 / 21.0);
+  p = fma(p, t2, 1.0 / 19.0);
+  p = fma(p, t2, 1.0 / 17.0);
+  p = fma(p, t2, 1.0 / 15.0);
+  p = fma(p, t2, 1.0 / 13.0);
+  p = fma(p, t2, 1.0 / 11.0);
+  p = fma(p, t2, 1.0 / 9.0);
+  p = fma(p, t2, 1.0 / 7.0);
+  p = fma(p, t2, 1.0 / 5.0);
+  p = fma(p, t2, 1.0 / 3.0);
+  p = fma(p, t2, 1.0);
+  double lnm = 2.0 * t * p;
+  const double ln2_hi = 6.93147180369123816490e-01;
+  const double ln2_lo = 1.90821492927058770002e-10;
+  double de = (double)e;
+  return fma(de, ln2_hi, fma(de, ln2_lo, lnm));
+}
+
+static double ph_exp_dbl(double z) {
+  const double inv_ln2 = 1.44269504088896338700e+00;
+  const double ln2_hi = 6.93147180369123816490e-01;
+  const double ln2_lo = 1.90821492927058770002e-10;
+  double kd = rint(z * inv_ln2);
+  double r = fma(-kd, ln2_hi, z);
+  r = fma(-kd, ln2_lo, r);
+  double p = 1.0 / 6227020800.0;
+  p = fma(p, r, 1.0 / 479001600.0);
+  p = fma(p, r, 1.0 / 39916800.0);
+  p = fma(p, r, 1.0 / 3628800.0);
+  p = fma(p, r, 1.0 / 362880.0);
+  p = fma(p, r, 1.0 / 40320.0);
+  p = fma(p, r, 1.0 / 5040.0);
+  p = fma(p, r, 1.0 / 720.0);
+  p = fma(p, r, 1.0 / 120.0);
+  p = fma(p, r, 1.0 / 24.0);
+  p = fma(p, r, 1.0 / 6.0);
+  p = fma(p, r, 0.5);
+  p = fma(p, r, 1.0);
+  p = fma(p, r, 1.0);
+  return ldexp(p, (int)kd);
+}
+
+float oracle_pow(float x, float y) {
+  if (y == 0.0f || x == 1.0f) return 1.0f;
+  if (x != x || y != y) return x + y;
+  float ax = fabsf(x);
+  float ay = fabsf(y);
+  int y_int = (ay < 16777216.0f) ? (truncf(y) == y) : 1;
+  int y_odd = y_int && (ay < 16777216.0f) && (fmodf(ay, 2.0f) == 1.0f);
+  if (x < 0.0f && !y_int && ax != INFINITY) return NAN;
+  if (ay == INFINITY) {
+    if (ax == 1.0f) return 1.0f;
+    return ((ax > 1.0f) == (y > 0.0f)) ? INFINITY : 0.0f;
+  }
+  float sign = (x < 0.0f && y_odd) ? -1.0f : 1.0f;
+  if (ax == 0.0f) return (y < 0.0f) ? sign * INFINITY : sign * 0.0f;
+  if (ax == INFINITY) return (y < 0.0f) ? sign * 0.0f : sign * INFINITY;
+  double z = (double)y * ph_ln_pos((double)ax);
+  if (z > 89.0) return sign * INFINITY;
+  if (z < -104.0) return sign * 0.0f;
+  return sign * (float)ph_exp_dbl(z);
+}
+
+/* ------------------------------------------------------------------------
+ * Adaptive Bogacki-Shampine 3(2) with FSAL and a PI step controller on Van
+ * der Pol, one trajectory per index, as tests/test_08_adaptive.py:76-122
+ * (tableau, error norm, controller, dt clamp) but iterating while t < T1
+ * (bounded by max_attempts). Op order matches
+ * palladium_amd.workloads.bs3_vdp_kernel, statement for statement.
+ * ---------------------------------------------------------------------- */
+static inline void vdp_rhs(float mu, float x, float v, float *fx, float *fv) {
+  float x2 = x * x;
+  float a = 1.0f - x2;
+  float b = mu * a;
+  float c = b * v;
+  *fx = v;
+  *fv = c - x;
+}
+
+void oracle_bs3_vdp(long n, const float *x0, const float *v0, const float *mu_in,
+                    float t1, float dt0, float rtol, float atol, long max_attempts,
+                    float *to, float *xo, float *vo, int32_t *acc_out,
+                    int32_t *rej_out) {
+  const float coeff1 = (float)((0.3 + 0.4) / 3.0);
+  const float coeff2 = (float)(-0.4 / 3.0);
+  const float b1 = (float)(2.0 / 9.0), b2 = (float)(1.0 / 3.0), b3 = (float)(4.0 / 9.0);
+  const float e1 = (float)(7.0 / 24.0), e2 = 0.25f, e3 = (float)(1.0 / 3.0), e4 = 0.125f;
+#pragma omp parallel for schedule(dynamic, 64)
+  for (long i = 0; i < n; ++i) {
+    const float mu = mu_in[i];
+    float x = x0[i], v = v0[i];
+    float t = 0.0f, dt = dt0, prev = 1.0f;
+    float k1x, k1v;
+    vdp_rhs(mu, x, v, &k1x, &k1v);
+    int32_t acc = 0, rej = 0, it = 0;
+    while (t < t1 && it < max_attempts) {
+      float rem = t1 - t;
+      dt = fminf(dt, rem);
+      float h = 0.5f * dt;
+      float xa = x + h * k1x, va = v + h * k1v;
+      float k2x, k2v;
+      vdp_rhs(mu, xa, va, &k2x, &k2v);
+      h = 0.75f * dt;
+      xa = x + h * k2x; va = v + h * k2v;
+      float k3x, k3v;
+      vdp_rhs(mu, xa, va, &k3x, &k3v);
+      float sx = b1 * k1x; sx = sx + b2 * k2x; sx = sx + b3 * k3x;
+      float x3 = x + dt * sx;
+      float sv = b1 * k1v; sv = sv + b2 * k2v; sv = sv + b3 * k3v;
+      float v3 = v + dt * sv;
+      float k4x, k4v;
+      vdp_rhs(mu, x3, v3, &k4x, &k4v);
+      float qx = e1 * k1x; qx = qx + e2 * k2x; qx = qx + e3 * k3x; qx = qx + e4 * k4x;
+      float x2 = x + dt * qx;
+      float qv = e1 * k1v; qv = qv + e2 * k2v; qv = qv + e3 * k3v; qv = qv + e4 * k4v;
+      float v2 = v + dt * qv;
+      float ex = x3 - x2, ev = v3 - v2;
+      float nx = fabsf(ex) / (atol + rtol * fabsf(x3));
+      float nv = fabsf(ev) / (atol + rtol * fabsf(v3));
+      float err = fmaxf(nx, nv);
+      int accept = err <= 1.0f;
+      float tn = t + dt;
+      float t2 = accept ? tn : t;
+      float xn = accept ? x3 : x;
+      float vn = accept ? v3 : v;
+      float kx = accept ? k4x : k1x;
+      float kv = accept ? k4v : k1v;
+      err = fmaxf(err, 1e-9f);
+      float inv = 1.0f / err;
+      float f = 0.9f * oracle_pow(inv, coeff1);
+      f = f * oracle_pow(prev, coeff2);
+      float pn = accept ? inv : prev;
+      float cl = fminf(10.0f, fmaxf(0.2f, f));
+      dt = dt * cl;
+      acc = acc + (accept ? 1 : 0);
+      rej = rej + (accept ? 0 : 1);
+      it = it + 1;
+      t = t2; x = xn; v = vn; k1x = kx; k1v = kv; prev = pn;
+    }
+    to[i] = t; xo[i] = x; vo[i] = v; acc_out[i] = acc; rej_out[i] = rej;
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * One Gray-Scott explicit Euler step on an n x n periodic grid, one cell per
+ * index, as examples/04_reaction_diffusion.py:61-74: five-point Laplacian
+ * ((((u[ip,j] + u[im,j]) + u[i,jp]) + u[i,jm]) - 4u), uvv = (u v) v,
+ * u' = u + dt((Du lap_u - uvv) + F(1-u)), v' = v + dt((Dv lap_v + uvv) - (F+k) v).
+ * ---------------------------------------------------------------------- */
+void oracle_gray_scott_step(long n, const float *u, const float *v, float du, float dv,
+                            float f, float fk, float dt, float *uo, float *vo) {
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) {
+    long ip = (i == n - 1) ? 0 : i + 1;
+    long im = (i == 0) ? n - 1 : i - 1;
+    for (long j = 0; j < n; ++j) {
+      long jp = (j == n - 1) ? 0 : j + 1;
+      long jm = (j == 0) ? n - 1 : j - 1;
+      float uc = u[i * n + j], vc = v[i * n + j];
+      float lu = u[ip * n + j] + u[im * n + j];
+      lu = lu + u[i * n + jp];
+      lu = lu + u[i * n + jm];
+      lu = lu - 4.0f * uc;
+      float lv = v[ip * n + j] + v[im * n + j];
+      lv = lv + v[i * n + jp];
+      lv = lv + v[i * n + jm];
+      lv = lv - 4.0f * vc;
+      float uv = uc * vc;
+      float uvv = uv * vc;
+      float a = du * lu;
+      a = a - uvv;
+      float b = 1.0f - uc;
+      b = f * b;
+      a = a + b;
+      uo[i * n + j] = uc + dt * a;
+      float c = dv * lv;
+      c = c + uvv;
+      float d = fk * vc;
+      c = c - d;
+      vo[i * n + j] = vc + dt * c;
+    }
+  }
+}
+
+void oracle_gray_scott(long n, long steps, float *u, float *v, float *tmp_u, float *tmp_v,
+                       float du, float dv, float f, float fk, float dt) {
+  for (long s = 0; s < steps; ++s) {
+    oracle_gray_scott_step(n, u, v, du, dv, f, fk, dt, tmp_u, tmp_v);
+    memcpy(u, tmp_u, sizeof(float) * n * n);
+    memcpy(v, tmp_v, sizeof(float) * n * n);
+  }
+}
+
+/* ------------------------------------------------------------------------
+ * df32 (double-float) arithmetic: a value is hi + lo with |lo| <= ulp(hi)/2.
+ * Algorithms: TwoSum (Knuth), Fast2Sum (Dekker), TwoProd via FMA, and the
+ * double-word operations of Joldes, Muller & Popescu, "Tight and rigorous
+ * error bounds for basic building blocks of double-word arithmetic",
+ * ACM TOMS 44(2), 2017: DWPlusDW (Alg. 6, "AccurateDWPlusDW") and
+ * DWTimesDW (Alg. 12, FMA-based). The device prelude
+ * (palladium_amd/df32.py) performs the same sequence.
+ * Used by the df32 RK4 LV kernel (examples/05_df32_precision.py:27-80).
+ * ---------------------------------------------------------------------- */
+typedef struct { float hi, lo; } df32;
+
+static inline df32 df_fast2sum(float a, float b) {
+  float s = a + b;
+  float z = s - a;
+  df32 r = {s, b - z};
+  return r;
+}
+static inline df32 df_twosum(float a, float b) {
+  float s = a + b;
+  float ap = s - b;
+  float bp = s - ap;
+  float da = a - ap;
+  float db = b - bp;
+  df32 r = {s, da + db};
+  return r;
+}
+static inline df32 df_from_float(float a) { df32 r = {a, 0.0f}; return r; }
+static inline float df_to_float(df32 a) { return a.hi + a.lo; }
+static inline df32 df_add(df32 x, df32 y) {
+  df32 s = df_twosum(x.hi, y.hi);
+  df32 t = df_twosum(x.lo, y.lo);
+  float c = s.lo + t.hi;
+  df32 v = df_fast2sum(s.hi, c);
+  float w = t.lo + v.lo;
+  return df_fast2sum(v.hi, w);
+}
+static inline df32 df_neg(df32 a) { df32 r = {-a.hi, -a.lo}; return r; }
+static inline df32 df_sub(df32 x, df32 y) { return df_add(x, df_neg(y)); }
+static inline df32 df_mul(df32 x, df32 y) {
+  float ch = x.hi * y.hi;
+  float cl1 = fmaf(x.hi, y.hi, -ch);
+  float tl0 = x.lo * y.lo;
+  float tl1 = fmaf(x.hi, y.lo, tl0);
+  float cl2 = fmaf(x.lo, y.hi, tl1);
+  float cl3 = cl1 + cl2;
+  return df_fast2sum(ch, cl3);
+}
+
+void oracle_df32_add(long n, const float *ah, const float *al, const float *bh, const float *bl,
+                     float *oh, float *ol) {
+  for (long i = 0; i < n; ++i) {
+    df32 a = {ah[i], al[i]}, b = {bh[i], bl[i]};
+    df32 r = df_add(a, b);
+    oh[i] = r.hi; ol[i] = r.lo;
+  }
+}
+
+void oracle_df32_mul(long n, const float *ah, const float *al, const float *bh, const float *bl,
+                     float *oh, float *ol) {
+  for (long i = 0; i < n; ++i) {
+    df32 a = {ah[i], al[i]}, b = {bh[i], bl[i]};
+    df32 r = df_mul(a, b);
+    oh[i] = r.hi; ol[i] = r.lo;
+  }
+}
+
+static inline void df_lv_rhs(df32 a, df32 b, df32 c, df32 d, df32 x, df32 y, df32 *fx, df32 *fy) {
+  df32 xy = df_mul(x, y);
+  *fx = df_sub(df_mul(a, x), df_mul(b, xy));
+  *fy = df_sub(df_mul(c, xy), df_mul(d, y));
+}
+
+static inline df32 df_adv(df32 s, df32 k, df32 h) { return df_add(s, df_mul(h, k)); }
+
+/* RK4 LV in df32, as examples/05_df32_precision.py:27-80 (the rhs groups
+ * x*y once; stage constants 0.5*dt, dt, dt/6 and 2 enter as df32 of their
+ * fp32 values). Outputs both words. */
+void oracle_lv_rk4_df32(long n, const float *x0, const float *y0, const float *a_,
+                        const float *b_, const float *c_, const float *d_, float dt,
+                        long steps, float *xo_hi, float *xo_lo, float *yo_hi, float *yo_lo) {
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) {
+    df32 a = df_from_float(a_[i]), b = df_from_float(b_[i]);
+    df32 c = df_from_float(c_[i]), d = df_from_float(d_[i]);
+    df32 half = df_from_float(0.5f * dt), full = df_from_float(dt);
+    df32 sixth = df_from_float(dt / 6.0f), two = df_from_float(2.0f);
+    df32 x = df_from_float(x0[i]), y = df_from_float(y0[i]);
+    for (long s = 0; s < steps; ++s) {
+      df32 k1x, k1y, k2x, k2y, k3x, k3y, k4x, k4y;
+      df_lv_rhs(a, b, c, d, x, y, &k1x, &k1y);
+      df_lv_rhs(a, b, c, d, df_adv(x, k1x, half), df_adv(y, k1y, half), &k2x, &k2y);
+      df_lv_rhs(a, b, c, d, df_adv(x, k2x, half), df_adv(y, k2y, half), &k3x, &k3y);
+      df_lv_rhs(a, b, c, d, df_adv(x, k3x, full), df_adv(y, k3y, full), &k4x, &k4y);
+      df32 sx = df_add(df_add(df_add(k1x, df_mul(two, k2x)), df_mul(two, k3x)), k4x);
+      df32 sy = df_add(df_add(df_add(k1y, df_mul(two, k2y)), df_mul(two, k3y)), k4y);
+      x = df_adv(x, sx, sixth);
+      y = df_adv(y, sy, sixth);
+    }
+    xo_hi[i] = x.hi; xo_lo[i] = x.lo; yo_hi[i] = y.hi; yo_lo[i] = y.lo;
+  }
+}

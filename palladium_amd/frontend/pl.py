@@ -179,14 +179,14 @@ class Ref:
             elif isinstance(i, Slice):
                 st = i.start
                 if isinstance(st, Tracer):
-                    leaves.append(b.atom(_as_i32(st)))
+                    leaves.append(_as_i32(st))
                     st = _Leaf(len(leaves) - 1)
                 out.append(Slice(st, i.size, i.stride))
             else:
                 if isinstance(i, Tracer):
                     if i.shape != ():
                         raise TraceError("ref indices must be scalars")
-                    leaves.append(b.atom(_as_i32(i)))
+                    leaves.append(_as_i32(i))
                 else:
                     v = int(i)
                     if v < 0:

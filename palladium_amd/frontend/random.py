@@ -87,7 +87,11 @@ def uniform(k: Any, shape: Sequence[int] = (), dtype: Any = np.float32, minval: 
     in [1, 2); subtract 1, scale, shift, then clamp below by minval."""
     if np.dtype(dtype) != F32:
         raise TraceError("uniform: only float32 is supported")
-    b = bits(k, shape)
+    return bits_to_uniform(bits(k, shape), minval, maxval)
+
+
+def bits_to_uniform(b: Tracer, minval: float = 0.0, maxval: float = 1.0) -> Tracer:
+    """JAX's uint32 -> float32 uniform conversion, staged op for op."""
     shifted = jnp.right_shift(b, np.uint32(9))
     fb = jnp.bitwise_or(shifted, np.uint32(0x3F800000))
     floats = jnp.bitcast_convert_type(fb, F32) - np.float32(1.0)
