@@ -24,6 +24,9 @@ import numpy as np
 
 FP32_PEAK = 157.3e12
 HBM_PEAK = 8.0e12
+# rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 for one config-1 launch.
+LV_MEASURED_TRAFFIC_BYTES = int((23467.5 + 11718.75) * 1024)
+GS_MEASURED_TRAFFIC_BYTES = int((131612.4 + 131072.0) * 1024)
 
 
 def _cpu_cores() -> int:
@@ -102,7 +105,10 @@ def bench_lv(steps: int, warmup: int, cpu: bool) -> dict:
             "peak": FP32_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": achieved / FP32_PEAK,
-            "traffic": None,
+            # HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE passes,
+            # scaled by the copy-kernel calibration (profiles/hbm_traffic_lv_rk4_n1e6.md).
+            "traffic": LV_MEASURED_TRAFFIC_BYTES,
+            "traffic_algorithmic": 36 * n,
             "flop_per_traj_step": LV_FLOP_PER_STEP,
             "avg_launch_ms": avg_launch_s * 1e3,
         },
@@ -172,13 +178,87 @@ def bench_gbm(steps: int, warmup: int, cpu: bool) -> dict:
     if cpu:
         import oracle
 
-        n_cpu = 65536
+        n_cpu = cfg.n_paths
         oracle.gbm(cfg, 64)
         t0 = time.perf_counter()
         oracle.gbm(cfg, n_cpu)
         dt = time.perf_counter() - t0
         res["cpu_baseline"] = {"value": n_cpu * cfg.n_steps / dt, "unit": "path-steps/s", "cores": _cpu_cores(),
-                               "kind": "port", "sample": f"{n_cpu} paths x {cfg.n_steps} steps, C oracle, {dt:.2f} s"}
+                               "kind": "port", "sample": f"all {n_cpu} paths x {cfg.n_steps} steps of config 3, C oracle, {dt:.2f} s"}
+    return res
+
+
+def bench_copy(steps: int, warmup: int, cpu: bool) -> dict:
+    """Calibration: an emitted copy of two 4096x4096 fp32 fields (the
+    Gray-Scott working set: read 2 fields, write 2), one element per lane."""
+    import palladium_amd as pa
+    from palladium_amd import runtime as rt
+    from palladium_amd.frontend import pl
+
+    n = 4096 * 4096
+
+    def copy2(u_ref, v_ref, uo_ref, vo_ref):
+        uo_ref[...] = u_ref[...]
+        vo_ref[...] = v_ref[...]
+
+    spec = pl.BlockSpec((1,), lambda i: (i,))
+    call = pa.hip_call(copy2, grid=(n,), in_specs=[spec, spec], out_specs=(spec, spec),
+                       out_shape=(pl.ShapeDtypeStruct((n,), np.float32),) * 2, name="copy2")
+    host = np.zeros(n, np.float32)
+    bound = call.bound(host, host)
+    ops = [rt.Buffer.from_numpy(host), rt.Buffer.from_numpy(host), rt.Buffer.empty((n,), np.float32),
+           rt.Buffer.empty((n,), np.float32)]
+    ms, avg = _timed_launches(bound, ops, steps, warmup)
+    nbytes = 16 * n
+    res = _base("emitted copy GB/s (2 x 64 MiB in, 2 x 64 MiB out)", nbytes / (ms / 1e3) / 1e9, "GB/s", steps,
+                warmup, ms, {"workload": "copy calibration", "bytes_per_launch": nbytes})
+    res["roofline"] = {"bound": "hbm", "achieved": nbytes / (avg / 1e3) / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                       "frac": nbytes / (avg / 1e3) / HBM_PEAK, "traffic": None, "avg_launch_ms": avg}
+    return res
+
+
+def bench_df32(steps: int, warmup: int, cpu: bool) -> dict:
+    """RK4 LV, N=1e6, every operation in df32 (config 4b: SAFE math,
+    config-1 inputs/dt/steps); accuracy against the float64 restatement on
+    a sample is reported beside the fp32 error."""
+    from palladium_amd import df32
+    from palladium_amd import runtime as rt
+    from palladium_amd.workloads import LV_CFG1, lv_inputs
+
+    cfg = LV_CFG1
+    host = lv_inputs(cfg.n, cfg.seed)
+    ins = [rt.Buffer.from_numpy(a) for a in host]
+    outs = [rt.Buffer.empty((cfg.n,), np.float32) for _ in range(4)]
+    stream = rt.Stream()
+    for _ in range(warmup):
+        df32.lv_rk4_df32_device(ins, outs, cfg.dt, cfg.steps, cfg.n, stream)
+    stream.synchronize()
+    evs = [rt.Event() for _ in range(steps + 1)]
+    evs[0].record(stream)
+    for k in range(steps):
+        df32.lv_rk4_df32_device(ins, outs, cfg.dt, cfg.steps, cfg.n, stream)
+        evs[k + 1].record(stream)
+    stream.synchronize()
+    ms = evs[0].elapsed_ms(evs[-1]) / steps
+    ts = cfg.n * cfg.steps
+    res = _base("df32 RK4 LV trajectory-steps/s (N=1e6, SAFE, compensated fp32 pairs)", ts / (ms / 1e3),
+                "trajectory-steps/s", steps, warmup, ms,
+                {"workload": "RK4 LV df32, config 4b (config-1 inputs, dt=0.005, 4000 steps)", "math_mode": "safe"})
+    res["dtype"] = "df32"
+    res["roofline"] = {"bound": "valu", "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None,
+                       "avg_launch_ms": ms, "df_ops_per_traj_step": 58}
+    if cpu:
+        import oracle
+
+        n_cpu = 2048
+        sample = tuple(a[:n_cpu] for a in host)
+        t0 = time.perf_counter()
+        want = oracle.lv_rk4_df32(*sample, cfg.dt, cfg.steps)
+        dt = time.perf_counter() - t0
+        got = [o.to_numpy(stream)[:n_cpu] for o in outs]
+        res["parity_sample_max_abs_diff"] = float(max(np.max(np.abs(g - w)) for g, w in zip(got, want)))
+        res["cpu_baseline"] = {"value": n_cpu * cfg.steps / dt, "unit": "trajectory-steps/s", "cores": _cpu_cores(),
+                               "kind": "port", "sample": f"first {n_cpu} trajectories, C oracle df32, {dt:.2f} s"}
     return res
 
 
@@ -189,8 +269,9 @@ def bench_gs(steps: int, warmup: int, cpu: bool) -> dict:
     u0, v0 = gray_scott_initial(cfg.size)
     call = gray_scott_call(cfg)
     gray_scott_run(call, u0, v0, 10)  # compile + warm
-    n_steps = cfg.steps
-    _, v, gpu_s = gray_scott_run(call, u0, v0, n_steps, graph=True)
+    n_steps = int(os.environ.get("PALLADIUM_GS_STEPS", cfg.steps))
+    graph = os.environ.get("PALLADIUM_GS_GRAPH", "1") != "0"
+    _, v, gpu_s = gray_scott_run(call, u0, v0, n_steps, graph=graph)
     cells = cfg.size * cfg.size
     ms = gpu_s * 1e3 / n_steps
     achieved = GS_BYTES_PER_CELL_STEP * cells / (ms / 1e3)
@@ -198,19 +279,18 @@ def bench_gs(steps: int, warmup: int, cpu: bool) -> dict:
                 n_steps, 10, ms, {"workload": "Gray-Scott 4096x4096, 2000 steps as one HIP graph, config 4",
                                   "size": cfg.size, "math_mode": "fast"})
     res["roofline"] = {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                       "frac": achieved / HBM_PEAK, "traffic": None, "bytes_per_cell_step": GS_BYTES_PER_CELL_STEP,
+                       "frac": achieved / HBM_PEAK, "traffic": GS_MEASURED_TRAFFIC_BYTES, "bytes_per_cell_step": GS_BYTES_PER_CELL_STEP,
                        "avg_launch_ms": ms}
     res["pattern_energy"] = float(np.sum(v, dtype=np.float64))
     if cpu:
         import oracle
 
-        size = 1024
-        su, sv = gray_scott_initial(size)
+        size, cs = cfg.size, 40
         t0 = time.perf_counter()
-        oracle.gray_scott(su, sv, cfg, 20)
+        oracle.gray_scott(u0, v0, cfg, cs)
         dt = time.perf_counter() - t0
-        res["cpu_baseline"] = {"value": size * size * 20 / dt, "unit": "cell-steps/s", "cores": _cpu_cores(),
-                               "kind": "port", "sample": f"{size}^2 grid x 20 steps, C oracle, {dt:.2f} s"}
+        res["cpu_baseline"] = {"value": size * size * cs / dt, "unit": "cell-steps/s", "cores": _cpu_cores(),
+                               "kind": "port", "sample": f"config-4 grid ({size}^2) x first {cs} of {cfg.steps} steps, C oracle, {dt:.2f} s"}
     return res
 
 
@@ -238,7 +318,7 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     if cpu:
         import oracle
 
-        n_cpu = 16384
+        n_cpu = 131072
         t0 = time.perf_counter()
         a2 = oracle.bs3_vdp(*(h[:n_cpu] for h in host), cfg)
         dt = time.perf_counter() - t0
@@ -263,7 +343,7 @@ def main() -> int:
         )
         return 2
     rank = int(os.environ.get("RANK", "0"))
-    fns = {"lv": bench_lv, "gbm": bench_gbm, "gs": bench_gs, "bs3": bench_bs3}
+    fns = {"lv": bench_lv, "gbm": bench_gbm, "gs": bench_gs, "bs3": bench_bs3, "copy": bench_copy, "df32": bench_df32}
     if a.workload not in fns:
         raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")
     res = fns[a.workload](a.steps, a.warmup, cpu=not a.no_cpu and rank == 0)

@@ -34,6 +34,7 @@ from palladium_amd.errors import (
     UnsupportedPrimitiveError,
 )
 from palladium_amd.ffi import FfiCallable, hip_call_jit
+from palladium_amd.interpret import check_block_bounds
 from palladium_amd.runtime import MathMode
 from palladium_amd.trace import BlockInfo, KernelSpec, trace
 
@@ -152,6 +153,7 @@ class HipCallable:
                 if b is None:
                     _check_dtypes(tuple(args))
                     spec = trace(self._staged, *args)
+                    check_block_bounds(spec)
                     log_compile(spec, self._threadgroup, self._math_mode)
                     from palladium_amd.dispatch import _block_of
 

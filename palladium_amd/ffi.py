@@ -109,7 +109,10 @@ class FfiCallable:
                 if entry is None:
                     from palladium_amd.dispatch import _block_of
 
+                    from palladium_amd.interpret import check_block_bounds
+
                     spec = trace(self._staged, *args)
+                    check_block_bounds(spec)
                     log_compile(spec, self._threadgroup, self._math_mode)
                     entry = (spec, emit_hip(spec, block=_block_of(self._threadgroup)))
                     self._cache[key] = entry

@@ -1,0 +1,141 @@
+"""Public API contract on the CPU: explain(), PALLADIUM_EXPLAIN, the error
+taxonomy, call-boundary validation, and compile-once under concurrency
+(reference: tests/test_16_diagnostics.py, tests/test_17_robustness.py)."""
+
+import threading
+
+import numpy as np
+import pytest
+
+import palladium_amd as pa
+from palladium_amd import DispatchError, EmitError, PalladiumError, TraceError, UnsupportedPrimitiveError
+from palladium_amd.frontend import pl
+
+F = np.float32
+
+
+def _double(n=64, **kw):
+    def kernel(x_ref, o_ref):
+        o_ref[...] = x_ref[...] * 2.0
+
+    spec = pl.BlockSpec((1,), lambda i: (i,))
+    return pa.hip_call(kernel, grid=(n,), in_specs=[spec], out_specs=spec, out_shape=pl.ShapeDtypeStruct((n,), F), **kw)
+
+
+def test_all_exports_present():
+    for name in pa.__all__:
+        assert hasattr(pa, name), name
+
+
+def test_error_hierarchy():
+    assert issubclass(TraceError, ValueError) and issubclass(TraceError, PalladiumError)
+    assert issubclass(DispatchError, TypeError) and issubclass(DispatchError, PalladiumError)
+    assert issubclass(UnsupportedPrimitiveError, EmitError) and issubclass(UnsupportedPrimitiveError, NotImplementedError)
+
+
+def test_explain_reports_geometry_and_resources():
+    diag = _double(1000).explain(np.zeros(1000, F))
+    assert diag.grid == (1000,)
+    assert diag.threadgroup is None
+    assert diag.block == 256 and diag.blocks == 4
+    assert diag.hip_lines > 0 and diag.msl_lines == diag.hip_lines
+    assert diag.resources.vgprs > 0 and diag.resources.scratch_bytes == 0
+    assert f"palladium kernel {diag.name}" in str(diag)
+
+
+def test_explain_explicit_threadgroup():
+    diag = _double(128, threadgroup=64).explain(np.zeros(128, F), compile=False)
+    assert diag.threadgroup == (64,)
+    assert diag.blocks == 2
+    assert "threadgroup=(64,)" in str(diag)
+
+
+def test_explain_env_logs_once_per_compile(monkeypatch, capsys):
+    monkeypatch.setenv("PALLADIUM_EXPLAIN", "1")
+    call = _double(64)
+    x = np.zeros(64, F)
+    call.bound(x)
+    call.bound(x)
+    assert capsys.readouterr().err.count("palladium kernel") == 1
+
+
+def test_dump_hip_env(monkeypatch, tmp_path):
+    monkeypatch.setenv("PALLADIUM_DUMP_HIP", str(tmp_path))
+    _double(64).bound(np.zeros(64, F))
+    files = list(tmp_path.glob("*.hip"))
+    assert len(files) == 1 and "__global__" in files[0].read_text()
+
+
+def test_dtype_gate_before_tracing():
+    with pytest.raises(DispatchError, match="float64"):
+        _double(4)(np.zeros(4, np.float64))
+
+
+def test_arity_shape_dtype_checks():
+    call = _double(64)
+    x = np.zeros(64, F)
+    bound = call.bound(x)
+    with pytest.raises(DispatchError, match="kernel takes 1 arrays, got 2"):
+        bound(x, x)
+    with pytest.raises(DispatchError, match="dtype int32 does not match the traced float32; cast explicitly"):
+        bound(np.zeros(64, np.int32))
+    with pytest.raises(DispatchError, match=r"expected shape \(64,\), got \(32,\)"):
+        bound(np.zeros(32, F))
+
+
+def test_concurrent_first_calls_compile_once(monkeypatch):
+    import palladium_amd
+
+    calls = []
+    real_bind = palladium_amd.bind
+
+    def counting_bind(*a, **k):
+        calls.append(1)
+        return real_bind(*a, **k)
+
+    monkeypatch.setattr(palladium_amd, "bind", counting_bind)
+    call = _double(256)
+    x = np.zeros(256, F)
+    barrier = threading.Barrier(16)
+    errors = []
+
+    def worker():
+        try:
+            barrier.wait()
+            call.bound(x)
+        except Exception as e:  # pragma: no cover
+            errors.append(e)
+
+    ts = [threading.Thread(target=worker) for _ in range(16)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors
+    assert len(calls) == 1
+    assert len(call.cache) == 1
+
+
+def test_debug_hip_returns_source():
+    src = pa.debug_hip(lambda x_ref, o_ref: None, np.zeros(4, F), out_shape=pl.ShapeDtypeStruct((4,), F))
+    assert 'extern "C" __global__' in src
+
+
+def test_hip_call_jit_rejects_whole_batch_vmap():
+    with pytest.raises(ValueError, match="sequential"):
+        pa.hip_call_jit(lambda x, o: None, out_shape=pl.ShapeDtypeStruct((1,), F), vmap_method="expand_dims")
+
+
+def test_hip_call_jit_ffi_attributes():
+    call = pa.hip_call_jit(lambda x_ref, o_ref: None, out_shape=pl.ShapeDtypeStruct((4,), F), math_mode="safe")
+    attrs = call.ffi_attributes((np.zeros(4, F),))
+    assert attrs["function_name"] == "<lambda>" or attrs["function_name"] == "palladium_kernel"
+    assert (attrs["grid_x"], attrs["grid_y"], attrs["grid_z"]) == (1, 1, 1)
+    assert attrs["block_x"] == 256 and attrs["math_mode"] == 0
+    assert "__global__" in attrs["hip_source"]
+
+
+def test_math_mode_values():
+    assert pa.MathMode("safe").ordinal == 0 and pa.MathMode.FAST.ordinal == 2
+    with pytest.raises(ValueError):
+        _double(4, math_mode="turbo")

@@ -1,0 +1,177 @@
+"""Emitter unit tests (CPU): source shape, hiprtc compilation of every rule,
+and the error taxonomy."""
+
+import numpy as np
+import pytest
+
+import palladium_amd as pa
+from palladium_amd import runtime as rt
+from palladium_amd.emit import emit_hip, rule
+from palladium_amd.errors import EmitError, UnsupportedPrimitiveError
+from palladium_amd.frontend import jnp, lax, pl, random
+from palladium_amd.trace import trace
+
+
+def _spec(kernel, out_shape, *args, **kw):
+    return trace(pl.pallas_call(kernel, out_shape=out_shape, **kw), *args)
+
+
+def _compile(spec, mode="fast"):
+    src = emit_hip(spec)
+    return src, rt.compile_code_object(src, spec.name, mode)
+
+
+F = np.float32
+
+
+def test_scalar_values_are_registers_not_arrays():
+    s1 = pl.BlockSpec((1,), lambda i: (i,))
+
+    def k(x_ref, o_ref):
+        x = x_ref[...]
+        o_ref[...] = lax.fori_loop(0, 10, lambda i, v: v * 1.5 + 1.0, x)
+
+    src, _ = _compile(_spec(k, pl.ShapeDtypeStruct((64,), F), np.zeros(64, F), grid=(64,), in_specs=[s1], out_specs=s1))
+    body = src.split("__launch_bounds__")[1]
+    assert "[1]" not in body
+    assert "float t" in body
+
+
+def test_all_elementwise_rules_compile():
+    def k(x_ref, y_ref, i_ref, o_ref, oi_ref, ob_ref):
+        x, y, i = x_ref[...], y_ref[...], i_ref[...]
+        f = [x + y, x - y, x * y, x / y, jnp.minimum(x, y), jnp.maximum(x, y), x ** y, -x, jnp.abs(x),
+             jnp.exp(x), jnp.log(x), jnp.sin(x), jnp.cos(x), jnp.sqrt(x), jnp.tanh(x), x ** 3, x ** -2,
+             jnp.clamp(0.1, x, 0.9), jnp.where(x < y, x, y), jnp.floor(x), jnp.rsqrt(x), jnp.exp2(x),
+             jnp.sign(x), jnp.remainder(x, y), i.astype(jnp.float32)]
+        acc = f[0]
+        for v in f[1:]:
+            acc = acc + v
+        o_ref[...] = acc
+        u = i.astype(jnp.uint32)
+        ii = [i + 1, i * 3, i // 2, i % 5, jnp.minimum(i, 4), i >> 1, i << 2, ~i, i & 7, i | 8, i ^ 3,
+              (u >> np.uint32(3)).astype(jnp.int32), lax.bitcast_convert_type(x, jnp.int32)]
+        acc_i = ii[0]
+        for v in ii[1:]:
+            acc_i = acc_i + v
+        oi_ref[...] = acc_i
+        ob_ref[...] = jnp.logical_and(x <= y, jnp.logical_not(x == y)) | (x >= y) ^ (x != y) | (x > y)
+
+    args = (np.ones(8, F), np.ones(8, F), np.ones(8, np.int32))
+    outs = (pl.ShapeDtypeStruct((8,), F), pl.ShapeDtypeStruct((8,), np.int32), pl.ShapeDtypeStruct((8,), np.bool_))
+    spec = _spec(k, outs, *args)
+    for mode in ("safe", "relaxed", "fast"):
+        _compile(spec, mode)
+
+
+def test_control_flow_and_reductions_compile():
+    def k(x_ref, o_ref, m_ref):
+        x = x_ref[...]
+
+        def body(c):
+            i, v = c
+            v = lax.cond(jnp.sum(v) > 1.0, lambda v: v * 0.5, lambda v: v + 1.0, v)
+            return i + 1, v
+
+        _, v = lax.while_loop(lambda c: c[0] < 10, body, (0, x))
+        v = lax.switch(jnp.argmax if False else 1, [lambda v: v, lambda v: v * 2.0, lambda v: v * 3.0], v)
+        o_ref[...] = v
+        m_ref[0] = jnp.max(v) + jnp.min(v) + jnp.any(v > 0).astype(jnp.float32) + jnp.all(v > 0).astype(jnp.float32)
+
+    spec = _spec(k, (pl.ShapeDtypeStruct((4,), F), pl.ShapeDtypeStruct((1,), F)), np.ones(4, F))
+    src, _ = _compile(spec)
+    assert "while (true)" in src
+
+
+def test_traced_switch_index_compiles():
+    def k(x_ref, i_ref, o_ref):
+        o_ref[...] = lax.switch(i_ref[0], [lambda v: v, lambda v: v * 2.0, lambda v: -v], x_ref[...])
+
+    spec = _spec(k, pl.ShapeDtypeStruct((4,), F), np.ones(4, F), np.zeros(1, np.int32))
+    src, _ = _compile(spec)
+    assert "else if" in src
+
+
+def test_random_rules_compile():
+    def k(k_ref, o_ref, f_ref):
+        key = random.wrap_key_data(k_ref[...])
+        o_ref[...] = random.bits(random.fold_in(key, pl.program_id(0)), (4,))
+        f_ref[...] = random.key_data(key)
+
+    spec = _spec(k, (pl.ShapeDtypeStruct((16,), np.uint32), pl.ShapeDtypeStruct((2,), np.uint32)), np.zeros(2, np.uint32),
+                 grid=(4,), in_specs=[pl.BlockSpec((2,), lambda i: (0,))],
+                 out_specs=(pl.BlockSpec((4,), lambda i: (i,)), pl.BlockSpec((2,), lambda i: (0,))))
+    _compile(spec)
+
+
+def test_noncontiguous_block_rejected():
+    call = pl.pallas_call(lambda x, o: None, grid=(2, 2), in_specs=[pl.BlockSpec((4, 4), lambda i, j: (i, j))],
+                          out_specs=pl.BlockSpec((4, 4), lambda i, j: (i, j)), out_shape=pl.ShapeDtypeStruct((8, 8), F))
+    with pytest.raises(EmitError, match="not contiguous"):
+        emit_hip(trace(call, np.zeros((8, 8), F)))
+
+
+def test_unknown_primitive_raises_and_rule_extends():
+    from palladium_amd.frontend.jnp import _stage
+
+    def k(x_ref, o_ref):
+        x = x_ref[...]
+        o_ref[...] = _stage("my_cube", [x], x.shape, x.dtype)
+
+    spec = _spec(k, pl.ShapeDtypeStruct((1,), F), np.ones(1, F))
+    with pytest.raises(UnsupportedPrimitiveError, match="my_cube"):
+        emit_hip(spec)
+
+    from palladium_amd.emit import RULES, declare
+
+    @rule("my_cube")
+    def _cube(env, cursor, eqn):
+        a = env.val(eqn.invars[0])
+        declare(env, cursor, eqn.outvars[0], init=f"({a.at('0')} * {a.at('0')} * {a.at('0')})")
+
+    try:
+        src = emit_hip(spec)
+        assert "* " in src
+        rt.compile_code_object(src, spec.name, "fast")
+    finally:
+        RULES.pop("my_cube", None)
+
+
+def test_store_into_input_ref_rejected():
+    def k(x_ref, o_ref):
+        x_ref[...] = o_ref[...]
+
+    spec = _spec(k, pl.ShapeDtypeStruct((1,), F), np.ones(1, F))
+    with pytest.raises(EmitError, match="input ref"):
+        emit_hip(spec)
+
+
+def test_block_size_validation():
+    spec = _spec(lambda x, o: None, pl.ShapeDtypeStruct((1,), F), np.ones(1, F))
+    with pytest.raises(EmitError, match="multiple of 64"):
+        emit_hip(spec, block=100)
+    assert "__launch_bounds__(512)" in emit_hip(spec, block=512)
+
+
+def test_ragged_blocks_rejected_before_launch():
+    from palladium_amd.interpret import check_block_bounds
+
+    spec_ok = pl.BlockSpec((256,), lambda i: (i,))
+    call = pl.pallas_call(lambda x, o: None, grid=(391,), in_specs=[spec_ok], out_specs=spec_ok,
+                          out_shape=pl.ShapeDtypeStruct((100_000,), F))
+    spec = trace(call, np.zeros(100_000, F))
+    with pytest.raises(EmitError, match="past the array extent"):
+        check_block_bounds(spec)
+
+
+def test_xcd_remap_is_a_bijection():
+    from palladium_amd.emit.core import NUM_XCDS
+
+    for nb in (16, 17, 391, 3907, 65536):
+        per, rem = divmod(nb, NUM_XCDS)
+        seen = set()
+        for b in range(nb):
+            xcd, slot = b % NUM_XCDS, b // NUM_XCDS
+            blk = xcd * (per + 1) + slot if xcd < rem else rem * (per + 1) + (xcd - rem) * per + slot
+            seen.add(blk)
+        assert seen == set(range(nb))

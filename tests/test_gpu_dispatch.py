@@ -1,0 +1,153 @@
+"""Launch semantics on the GPU (reference: tests/test_dispatch_launch.py,
+tests/test_11_ffi.py, tests/test_17_robustness.py)."""
+
+import ctypes
+import threading
+
+import numpy as np
+import pytest
+
+import palladium_amd as pa
+from palladium_amd import runtime as rt
+from palladium_amd.emit import emit_hip
+from palladium_amd.frontend import pl
+
+pytestmark = pytest.mark.gpu
+
+F = np.float32
+
+
+def _inc(n):
+    def kernel(x_ref, o_ref):
+        o_ref[...] = x_ref[...] + 1.0
+
+    spec = pl.BlockSpec((1,), lambda i: (i,))
+    return pa.hip_call(kernel, grid=(n,), in_specs=[spec], out_specs=spec, out_shape=pl.ShapeDtypeStruct((n,), F))
+
+
+def test_launch_wait_matches_call(rng):
+    f = _inc(256)
+    x = rng.standard_normal(256).astype(F)
+    np.testing.assert_array_equal(f.launch(x).wait(), f(x))
+    np.testing.assert_array_equal(f(x), x + 1.0)
+
+
+def test_stepping_loop_via_launch(rng):
+    f, g = _inc(64), _inc(64)
+    x0 = rng.standard_normal(64).astype(F)
+    x = x0.copy()
+    for _ in range(5):
+        x = f(x)
+    pending = g.launch(x0)
+    for _ in range(4):
+        pending = g.launch(pending.wait())
+    np.testing.assert_array_equal(pending.wait(), x)
+
+
+def test_second_launch_before_wait_does_not_corrupt_first(rng):
+    n = 1 << 20
+    f = _inc(n)
+    x0 = rng.standard_normal(n).astype(F)
+    x1 = rng.standard_normal(n).astype(F)
+    first = f.launch(x0)
+    second = f.launch(x1)
+    np.testing.assert_array_equal(first.wait(), x0 + 1.0)
+    np.testing.assert_array_equal(second.wait(), x1 + 1.0)
+
+
+def test_pin_redispatches_without_upload(rng):
+    f = _inc(128)
+    x = rng.standard_normal(128).astype(F)
+    call = f.pin(x)
+    x[:] = 0  # later mutation is not observed
+    a, b = call(), call()
+    np.testing.assert_array_equal(a, b)
+    assert not np.array_equal(a, np.ones(128, F))
+
+
+def test_concurrent_launches_on_one_kernel(rng):
+    f = _inc(4096)
+    xs = [rng.standard_normal(4096).astype(F) for _ in range(8)]
+    results = [None] * 8
+
+    def worker(i):
+        results[i] = f(xs[i])
+
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(8)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    for x, r in zip(xs, results):
+        np.testing.assert_array_equal(r, x + 1.0)
+
+
+def test_launch_device_with_runtime_buffers(rng):
+    f = _inc(1000)
+    x = rng.standard_normal(1000).astype(F)
+    bound = f.bound(x)
+    xb = rt.Buffer.from_numpy(x)
+    ob = rt.Buffer.empty((1000,), F)
+    bound.launch_device(xb, ob)
+    np.testing.assert_array_equal(ob.to_numpy(bound.stream), x + 1.0)
+    with pytest.raises(pa.DispatchError):
+        bound.launch_device(xb, rt.Buffer.empty((999,), F))
+
+
+def test_ph_dispatch_c_abi_host_buffers(rng):
+    """The FFI-handler entry point: source + name + grid + block + math mode,
+    host inputs then outputs, synchronous."""
+    n = 777
+    f = _inc(n)
+    x = rng.standard_normal(n).astype(F)
+    spec = pa.trace(f._staged, x)
+    src = emit_hip(spec).encode()
+    out = np.empty(n, F)
+    ins = (ctypes.c_void_p * 1)(x.ctypes.data)
+    in_b = (ctypes.c_size_t * 1)(x.nbytes)
+    outs = (ctypes.c_void_p * 1)(out.ctypes.data)
+    out_b = (ctypes.c_size_t * 1)(out.nbytes)
+    err = ctypes.c_void_p()
+    rc = rt.lib().ph_dispatch(src, len(src), spec.name.encode(), n, 1, 1, 256, 0, ins, in_b, 1, outs, out_b, 1,
+                              ctypes.byref(err))
+    assert rc == 0
+    np.testing.assert_array_equal(out, x + 1.0)
+    rc = rt.lib().ph_dispatch(src, len(src), spec.name.encode(), n, 1, 1, 256, 5, ins, in_b, 1, outs, out_b, 1,
+                              ctypes.byref(err))
+    assert rc == rt.PH_ERR_INVALID
+    assert b"math_mode out of range" in ctypes.cast(err, ctypes.c_char_p).value
+    rt.lib().ph_free_error(err)
+
+
+def test_kernel_cache_compiles_each_source_once():
+    before = rt.lib().ph_kernel_cache_size()
+    f = _inc(32)
+    f(np.zeros(32, F))
+    mid = rt.lib().ph_kernel_cache_size()
+    k = rt.Kernel(f.cache[next(iter(f.cache))].hip_source, f.cache[next(iter(f.cache))].spec.name, "fast")
+    k.load()
+    assert rt.lib().ph_kernel_cache_size() == mid >= before + 1
+
+
+def test_safe_mode_propagates_nan_and_inf():
+    def kernel(x_ref, o_ref):
+        x = x_ref[...]
+        o_ref[...] = x * 0.0 + x / 0.0
+
+    f = pa.hip_call(kernel, out_shape=pl.ShapeDtypeStruct((3,), F), math_mode="safe")
+    out = f(np.array([1.0, -1.0, 0.0], F))
+    assert np.isnan(out[2]) and np.isinf(out[0]) and out[1] < 0
+
+
+def test_torch_device_tensors_zero_copy():
+    torch = pytest.importorskip("torch")
+    if not torch.cuda.is_available():
+        pytest.skip("torch has no GPU here")
+    f = _inc(512)
+    x = torch.arange(512, dtype=torch.float32, device="cuda")
+    o = torch.empty_like(x)
+    bound = f.bound(np.zeros(512, F))
+    torch.cuda.synchronize()
+    bound.launch_device(x, o)
+    bound.stream.synchronize()
+    assert torch.equal(o, x + 1.0)
