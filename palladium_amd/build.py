@@ -33,10 +33,30 @@ def build_launcher(verbose: bool = False) -> Path:
     return LIB
 
 
-def build_all(verbose: bool = False) -> list[Path]:
-    return [build_launcher(verbose)]
+def build_ffi(verbose: bool = False) -> Path:
+    """The jax.ffi handler (csrc/xla_ffi_handler.cc) over the C ABI; needs
+    jax for the XLA FFI headers."""
+    import jax
+
+    out = PKG / "libpalladium_hip_ffi.so"
+    cmd = [
+        HIPCC, "--offload-arch=gfx950", *NO_PACKED, "-O2", "-fPIC", "-shared", "-std=c++17",
+        f"-I{ROOT / 'include'}", f"-I{jax.ffi.include_dir()}", str(PKG / "csrc" / "xla_ffi_handler.cc"),
+        str(PKG / "csrc" / "palladium_hip.cpp"), "-o", str(out), "-lhiprtc",
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    return out
+
+
+def build_all(verbose: bool = False, ffi: bool = False) -> list[Path]:
+    out = [build_launcher(verbose)]
+    if ffi:
+        out.append(build_ffi(verbose))
+    return out
 
 
 if __name__ == "__main__":
-    for p in build_all(verbose="-v" in sys.argv):
+    for p in build_all(verbose="-v" in sys.argv, ffi="--ffi" in sys.argv):
         print(p)
