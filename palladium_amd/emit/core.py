@@ -376,24 +376,33 @@ def _xcd_remap(nblocks: int) -> list[str]:
 
 @dataclasses.dataclass(frozen=True)
 class LaunchGeometry:
-    """How a KernelSpec maps to a HIP launch: 1-D grid of `blocks`
-    workgroups of `block` lanes, one lane per program instance."""
+    """How a KernelSpec maps to a HIP launch: a 1-D grid of `blocks`
+    workgroups of `block` lanes. `lanes` is 1 when each program instance
+    is one lane, or B when an instance's B-row block is spread over B lanes
+    (lane-parallel lowering)."""
 
     block: int
     blocks: int
     num_programs: int
+    lanes: int = 1
 
 
-def launch_geometry(spec: KernelSpec, block: int | None = None) -> LaunchGeometry:
+def launch_geometry(spec: KernelSpec, block: int | None = None, lanes: int | None = None) -> LaunchGeometry:
+    from palladium_amd.emit.lanes import lanes_of, workgroup_for
+
     n = spec.num_programs
     b = int(block) if block else DEFAULT_BLOCK
     if b <= 0 or b > 1024 or b % 64:
         raise EmitError(f"block size {b} must be a positive multiple of 64 and at most 1024")
     if n <= 0:
         raise EmitError(f"grid {spec.grid} has no program instances")
-    if n >= 2**31:
-        raise EmitError(f"grid {spec.grid} has more than 2**31 program instances")
-    return LaunchGeometry(b, (n + b - 1) // b, n)
+    lanes = lanes if lanes is not None else lanes_of(spec)
+    if lanes > 1:
+        b = workgroup_for(lanes, block)
+    threads = n * lanes
+    if threads >= 2**31:
+        raise EmitError(f"grid {spec.grid} needs more than 2**31 lanes")
+    return LaunchGeometry(b, (threads + b - 1) // b, n, lanes)
 
 
 def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None = None) -> str:
@@ -413,8 +422,12 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
     """
     from palladium_amd.emit.prelude import PRELUDE
 
+    from palladium_amd.emit.lanes import lane_transform
+
     name = kernel_name or spec.name
-    geo = launch_geometry(spec, block)
+    plan = lane_transform(spec)
+    lanes = plan.lanes if plan else 1
+    geo = launch_geometry(spec, block, lanes)
     operands = list(spec.inputs) + list(spec.outputs)
     n_in = len(spec.inputs)
     if len(spec.jaxpr.invars) != len(operands):
@@ -435,9 +448,14 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
     for line in _xcd_remap(geo.blocks):
         cursor.emit(line)
     cursor.emit(f"const unsigned int _flat = _blk * {geo.block}u + threadIdx.x;")
-    cursor.emit(f"if (_flat >= {geo.num_programs}u) return;")
+    cursor.emit(f"if (_flat >= {geo.num_programs * lanes}u) return;")
+    if lanes > 1:
+        cursor.emit(f"const unsigned int _inst = _flat / {lanes}u;")
+        cursor.emit(f"const int _lane = (int)(_flat % {lanes}u);")
+    env.lanes = lanes  # type: ignore[attr-defined]
+    env.grid = tuple(spec.grid)  # type: ignore[attr-defined]
     pid_vals = []
-    rem = "_flat"
+    rem = "_inst" if lanes > 1 else "_flat"
     grid = tuple(spec.grid)
     for axis in reversed(range(len(grid))):
         g = grid[axis]
@@ -463,7 +481,7 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         cursor.emit(f"{ptr} = arg{k}_base + {offset};" if offset != "0" else f"{ptr} = arg{k}_base;")
         ref_vals.append(CVal(f"arg{k}", info.block_shape or (1,), ct, "global", k < n_in))
 
-    emit_jaxpr(env, cursor, spec.jaxpr, ref_vals)
+    emit_jaxpr(env, cursor, plan.jaxpr if plan else spec.jaxpr, ref_vals)
 
     head = (
         f'extern "C" __global__ void __launch_bounds__({geo.block})\n{name}(\n    '
@@ -472,7 +490,7 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
     )
     return "\n".join(
         [
-            f"// palladium_amd kernel {name}: grid={grid} block={geo.block} blocks={geo.blocks}",
+            f"// palladium_amd kernel {name}: grid={grid} block={geo.block} blocks={geo.blocks} lanes={lanes}",
             PRELUDE,
             head,
             *cursor.lines,

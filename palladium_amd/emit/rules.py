@@ -263,11 +263,18 @@ def _rule_swap(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
         old = declare(env, cursor, out, init=dst.at("0")) if size == 1 else declare(env, cursor, out)
         if size != 1:
             cursor.copy(old, dst, size)
+    guard = eqn.params.get("lane0_only") and getattr(env, "lanes", 1) > 1
+    if guard:
+        cursor.emit("if (_lane == 0) {")
+        cursor.indent += 1
     if value.size == 1 and size > 1:
         with cursor.loop(size) as i:
             cursor.emit(f"{dst.at(i)} = {value.at('0')};")
     else:
         cursor.copy(dst, value, size)
+    if guard:
+        cursor.indent -= 1
+        cursor.emit("}")
 
 
 # ---------------------------------------------------------------------------
@@ -661,3 +668,72 @@ def _rule_cond(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
             vals = emit_jaxpr(env, cursor, getattr(br, "jaxpr", br), list(ops))
             for o, v in zip(outs, vals):
                 cursor.copy(o, v, o.size)
+
+
+# ---------------------------------------------------------------------------
+# iota and the lane-parallel primitives
+
+
+@rule("iota")
+def _rule_iota(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """`lax.broadcasted_iota`: index along `dimension` as the value."""
+    out = eqn.outvars[0]
+    shape = tuple(int(d) for d in out.aval.shape)
+    dim = int(eqn.params["dimension"])
+    ct = ctype_of(out.aval.dtype)
+    if math.prod(shape) == 1:
+        declare(env, cursor, out, init=f"({ct})0")
+        return
+    dst = declare(env, cursor, out)
+
+    def body(idx_vars: list[str], flat: str) -> None:
+        cursor.emit(f"{dst.at(flat)} = ({ct}){idx_vars[dim]};")
+
+    _emit_elementwise_loops(cursor, dst, body)
+
+
+@rule("lane_index")
+def _rule_lane_index(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """This lane's row within its instance's block (lane-parallel mode)."""
+    env.bind(eqn.outvars[0], CVal("_lane", (), "int"))
+
+
+_WAVE = 64
+
+
+@rule("lane_reduce")
+def _rule_lane_reduce(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """Reduce one scalar per lane over the instance's lanes; every lane gets
+    the result. Wavefront butterfly with `__shfl_xor`, then (instances wider
+    than one wavefront) partials through LDS, combined in a fixed order."""
+    kind = eqn.params["kind"]
+    lanes = int(eqn.params["lanes"])
+    src = env.val(eqn.invars[0])
+    out = eqn.outvars[0]
+    ct = ctype_of(out.aval.dtype)
+    is_bool = ct == "bool"
+    wt = "int" if is_bool else ct
+    comb = {
+        "sum": lambda a, b: f"({a} + {b})",
+        "max": (lambda a, b: f"ph_fmax({a}, {b})") if ct == "float" else (lambda a, b: f"(({a} > {b}) ? {a} : {b})"),
+        "min": (lambda a, b: f"ph_fmin({a}, {b})") if ct == "float" else (lambda a, b: f"(({a} < {b}) ? {a} : {b})"),
+        "or": lambda a, b: f"({a} | {b})",
+        "and": lambda a, b: f"({a} & {b})",
+    }[kind]
+    acc = cursor.fresh("_lr")
+    cursor.emit(f"{wt} {acc} = ({wt})({src.at('0')});")
+    off = _WAVE // 2
+    while off >= 1:
+        cursor.emit(f"{acc} = {comb(acc, f'__shfl_xor({acc}, {off}, {_WAVE})')};")
+        off //= 2
+    if lanes > _WAVE:
+        nw = lanes // _WAVE
+        sh = cursor.fresh("_lds")
+        cursor.emit(f"__shared__ {wt} {sh}[{nw}];")
+        cursor.emit(f"if ((_lane & {_WAVE - 1}) == 0) {sh}[_lane / {_WAVE}] = {acc};")
+        cursor.emit("__syncthreads();")
+        cursor.emit(f"{acc} = {sh}[0];")
+        for w in range(1, nw):
+            cursor.emit(f"{acc} = {comb(acc, f'{sh}[{w}]')};")
+        cursor.emit("__syncthreads();")
+    declare(env, cursor, out, init=f"({ct})({acc})" if not is_bool else f"({acc} != 0)")

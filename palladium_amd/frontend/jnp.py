@@ -474,3 +474,14 @@ def _value_getitem(x: Tracer, idx: Any) -> Tracer:
 
 def _is_key(x: Any) -> bool:
     return isinstance(x, Tracer) and isinstance(x.aval, KeyAval)
+
+
+def broadcasted_iota(dtype: Any, shape: Sequence[int], dimension: int) -> Tracer:
+    """`lax.broadcasted_iota`: the index along `dimension`, as `dtype`."""
+    dt = check_dtype(dtype)
+    shape = tuple(int(s) for s in shape)
+    return _stage("iota", [], shape, dt, dtype=dt, shape=shape, dimension=int(dimension), sharding=None)
+
+
+def arange(n: int, dtype: Any = np.int32) -> Tracer:
+    return broadcasted_iota(dtype, (int(n),), 0)

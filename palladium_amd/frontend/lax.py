@@ -68,6 +68,13 @@ eq = jnp.equal
 ne = jnp.not_equal
 
 
+broadcasted_iota = jnp.broadcasted_iota
+
+
+def iota(dtype: Any, size: int) -> Tracer:
+    return jnp.broadcasted_iota(dtype, (int(size),), 0)
+
+
 def shift_right_logical(a: Any, b: Any) -> Tracer:
     return jnp._nary("shift_right_logical", a, b)
 

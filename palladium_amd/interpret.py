@@ -266,6 +266,11 @@ def _eval(jaxpr: Jaxpr, env: _Env, invals: list[Any], mask: np.ndarray) -> list[
             old = ref.flat[np.where(m, idx, 0)].reshape(shape)
             ref.flat[sel] = vals.reshape(idx.shape)[m]
             env.write(eqn.outvars[0], old)
+        elif name == "iota":
+            shape = tuple(eqn.params["shape"])
+            dim = int(eqn.params["dimension"])
+            r = np.arange(shape[dim], dtype=eqn.outvars[0].aval.dtype).reshape([-1 if k == dim else 1 for k in range(len(shape))])
+            env.write(eqn.outvars[0], np.broadcast_to(r, (n,) + shape).copy())
         elif name == "program_id":
             env.write(eqn.outvars[0], env.pids[int(eqn.params["axis"])])
         elif name == "num_programs":

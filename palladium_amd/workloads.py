@@ -440,3 +440,47 @@ def gray_scott_run(call, u0: np.ndarray, v0: np.ndarray, steps: int, graph: bool
     batch.commit(graph=graph)
     batch.wait()
     return bufs[src][0].to_numpy(bound.stream), bufs[src][1].to_numpy(bound.stream), batch.gpu_time
+
+
+def gbm_block_kernel(cfg: GBMConfig, block: int):
+    """Kernel: refs (key u32[2]) -> one discounted-payoff *sum* per block of
+    `block` paths ("reduced per block"). The block's paths are the rows of
+    a (block,) value, which the emitter spreads across `block` lanes; the
+    closing `jnp.sum` is a cross-lane reduction."""
+    drift, vol = cfg.drift_dt, cfg.vol_sqdt
+    disc = math.exp(-cfg.r * cfg.t)
+
+    def kernel(key_ref, o_ref):
+        k0, k1 = key_ref[0], key_ref[1]
+        first = pl.program_id(0) * block
+        path = (first + lax.iota(jnp.int32, block)).astype(jnp.uint32)
+
+        def step(i, s):
+            b0, b1 = random.threefry2x32_p(k0, k1, path, i.astype(jnp.uint32))
+            u1 = jnp.maximum(random.bits_to_uniform(b0), 1e-7)
+            u2 = random.bits_to_uniform(b1)
+            z = jnp.sqrt(-2.0 * jnp.log(u1)) * jnp.cos(2.0 * jnp.pi * u2)
+            return s * jnp.exp(drift + vol * z)
+
+        s = lax.fori_loop(0, cfg.n_steps, step, jnp.full((block,), cfg.s0, jnp.float32))
+        o_ref[0] = jnp.sum(disc * jnp.maximum(s - cfg.strike, 0.0))
+
+    kernel.__name__ = "gbm_block_sums"
+    return kernel
+
+
+def gbm_block_call(cfg: GBMConfig = GBM_CFG, block: int = 256, n_paths: int | None = None, **kw: Any):
+    import palladium_amd as pa
+
+    n = n_paths or cfg.n_paths
+    if n % block:
+        raise ValueError(f"n_paths={n} is not a multiple of block={block}")
+    return pa.hip_call(
+        gbm_block_kernel(cfg, block),
+        grid=(n // block,),
+        in_specs=[pl.BlockSpec((2,), lambda i: (0,))],
+        out_specs=pl.BlockSpec((1,), lambda i: (i,)),
+        out_shape=pl.ShapeDtypeStruct((n // block,), F32),
+        name="gbm_block_sums",
+        **kw,
+    )

@@ -1,0 +1,77 @@
+"""Lane-parallel kernels on the GPU against the oracle and the interpreter."""
+
+import numpy as np
+import pytest
+
+import oracle
+import palladium_amd as pa
+from palladium_amd.frontend import jnp, lax, pl, random
+from palladium_amd.workloads import GBMConfig, gbm_block_call, lv_inputs, lv_rk4_call
+
+pytestmark = pytest.mark.gpu
+
+F = np.float32
+
+
+def test_lv_cfg0_layout_blocks_of_256_bit_exact():
+    # Config 0's layout: grid=(N/256,), blocks of 256 trajectories.
+    n = 256 * 40
+    args = lv_inputs(n, 0)
+    got = lv_rk4_call(n, 0.01, 1000, block=256, math_mode="safe")(*args)
+    want = oracle.lv_rk4(*args, 0.01, 1000)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
+
+
+def test_gbm_block_sums_match_oracle_paths():
+    cfg = GBMConfig(n_steps=32)
+    n = 256 * 64
+    sums = gbm_block_call(cfg, n_paths=n, math_mode="safe")(random.key(cfg.seed))
+    paths = oracle.gbm(cfg, n).astype(np.float64)
+    want = np.exp(-cfg.r * cfg.t) * paths.reshape(-1, 256).sum(axis=1)
+    np.testing.assert_allclose(sums, want, rtol=2e-5, atol=1e-3)
+
+
+def _lockstep_kernel(x_ref, o_ref, n_ref, m_ref):
+    x = x_ref[...]
+
+    def cond(c):
+        return jnp.any(c[0] > 1.0)
+
+    def body(c):
+        v, k = c
+        active = v > 1.0
+        return jnp.where(active, v * 0.5, v), k + jnp.where(active, 1, 0)
+
+    v, k = lax.while_loop(cond, body, (x, jnp.zeros(x.shape, jnp.int32)))
+    o_ref[...] = v
+    n_ref[...] = k
+    m_ref[0] = jnp.max(v) + jnp.min(v) + jnp.all(v <= 1.0).astype(jnp.float32)
+
+
+@pytest.mark.parametrize("lanes", [64, 256])
+def test_lockstep_while_any_matches_interpreter(lanes):
+    n = lanes * 12
+    blk = pl.BlockSpec((lanes,), lambda i: (i,))
+    one = pl.BlockSpec((1,), lambda i: (i,))
+    call = pa.hip_call(_lockstep_kernel, grid=(12,), in_specs=[blk], out_specs=(blk, blk, one),
+                       out_shape=(pl.ShapeDtypeStruct((n,), F), pl.ShapeDtypeStruct((n,), np.int32),
+                                  pl.ShapeDtypeStruct((12,), F)), math_mode="safe")
+    x = (10.0 ** np.random.default_rng(lanes).uniform(-1, 4, n)).astype(F)
+    got = call(x)
+    want = call.interpret(x)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
+
+
+def test_two_d_blocks_column_stores():
+    def kernel(x_ref, o_ref):
+        x = x_ref[...]
+        o_ref[:, 0] = x * 2.0
+        o_ref[:, 1] = x + 1.0
+
+    call = pa.hip_call(kernel, grid=(4,), in_specs=[pl.BlockSpec((128,), lambda i: (i,))],
+                       out_specs=pl.BlockSpec((128, 2), lambda i: (i, 0)),
+                       out_shape=pl.ShapeDtypeStruct((512, 2), F))
+    x = np.arange(512, dtype=F)
+    np.testing.assert_array_equal(call(x), np.stack([x * 2.0, x + 1.0], axis=1))
