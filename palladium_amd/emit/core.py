@@ -297,11 +297,22 @@ def flat_index(terms: list[tuple[str, int]]) -> str:
 
 
 def check_contiguous(info: BlockInfo, what: str) -> None:
+    """A block is one contiguous run of memory iff, scanning from the
+    innermost dim, every dim is full up to the first partial one, and every
+    dim outside that has block size 1. (The reference accepts the narrower
+    "only the leading dim may be partial", `src/palladium/emit/core.py:336-344`;
+    leading size-1 dims, e.g. squeezed row blocks of a 3-D array, are
+    contiguous too.)"""
     full = info.full_block()
-    if any(b != a for b, a in zip(full[1:], info.array_shape[1:])):
+    arr = info.array_shape
+    d = len(full) - 1
+    while d >= 0 and full[d] == arr[d]:
+        d -= 1
+    # dims 0..d-1 must be size 1 (dim d may be partial)
+    if any(full[k] != 1 for k in range(0, max(d, 0))):
         raise EmitError(
             f"{what}: block {info.block_shape} of array {info.array_shape} is "
-            "not contiguous; only the leading block dim may be partial"
+            "not contiguous; only the leading non-unit block dim may be partial"
         )
 
 

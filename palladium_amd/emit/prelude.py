@@ -14,6 +14,8 @@
   t = (m-1)/(m+1), as an odd series in t; exp by reduction z = k ln2 + r,
   |r| <= ln2/2, and a degree-13 Taylor polynomial; both carried in double,
   so the float result is the correctly rounded double value rounded once.
+- `ph_sin`/`ph_cos`: under FAST the hardware sine/cosine (the reference's
+  FAST contract allows approximate transcendentals); libm-accurate otherwise.
 - `ph_fmin`/`ph_fmax`: NaN-suppressing min/max (C fminf/fmaxf), the
   reference's lowering of `min`/`max` (`src/palladium/emit/core.py:574-575`).
 """
@@ -48,6 +50,16 @@ __device__ __forceinline__ void ph_threefry2x32(unsigned int k0, unsigned int k1
     *o0 = x0;
     *o1 = x1;
 }
+
+#if PH_MATH_MODE == 2
+/* FAST: hardware sine/cosine (v_sin_f32/v_cos_f32 take revolutions, so
+   cos(2*pi*u) needs no range reduction after reassociation). */
+__device__ __forceinline__ float ph_sin(float x) { return __sinf(x); }
+__device__ __forceinline__ float ph_cos(float x) { return __cosf(x); }
+#else
+__device__ __forceinline__ float ph_sin(float x) { return sinf(x); }
+__device__ __forceinline__ float ph_cos(float x) { return cosf(x); }
+#endif
 
 __device__ __forceinline__ float ph_fmin(float a, float b) { return fminf(a, b); }
 __device__ __forceinline__ float ph_fmax(float a, float b) { return fmaxf(a, b); }

@@ -76,8 +76,8 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
         "log": "logf({a})",
         "log1p": "log1pf({a})",
         "expm1": "expm1f({a})",
-        "sin": "sinf({a})",
-        "cos": "cosf({a})",
+        "sin": "ph_sin({a})",
+        "cos": "ph_cos({a})",
         "tan": "tanf({a})",
         "tanh": "tanhf({a})",
         "sqrt": "sqrtf({a})",
