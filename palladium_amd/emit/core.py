@@ -385,6 +385,20 @@ def _xcd_remap(nblocks: int) -> list[str]:
     ]
 
 
+def _tile2d(grid: tuple[int, ...], block: int) -> tuple[int, int] | None:
+    """(rows, cols) of the instance tile one workgroup covers on a 2-D grid,
+    or None to keep the row-major order. Disabled with PALLADIUM_TILE2D=0."""
+    import os
+
+    if os.environ.get("PALLADIUM_TILE2D", "1") == "0" or len(grid) != 2:
+        return None
+    tj = int(os.environ.get("PALLADIUM_TILE_COLS", "64"))
+    ti = block // tj
+    if ti < 2 or grid[1] % tj or grid[0] % ti:
+        return None
+    return ti, tj
+
+
 @dataclasses.dataclass(frozen=True)
 class LaunchGeometry:
     """How a KernelSpec maps to a HIP launch: a 1-D grid of `blocks`
@@ -468,17 +482,30 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
     pid_vals = []
     rem = "_inst" if lanes > 1 else "_flat"
     grid = tuple(spec.grid)
-    for axis in reversed(range(len(grid))):
-        g = grid[axis]
-        if axis == 0:
-            expr = rem
-        else:
-            expr = f"{rem} % {g}u" if g != 1 else "0u"
-        cursor.emit(f"const int _pid{axis} = (int)({expr});")
-        if axis > 0:
-            nxt = cursor.fresh("_q")
-            cursor.emit(f"const unsigned int {nxt} = {rem} / {g}u;")
-            rem = nxt
+    tile = _tile2d(grid, geo.block) if lanes == 1 else None
+    if tile is not None:
+        # 2-D grids: a workgroup covers a (block/64) x 64 tile of instances,
+        # each wavefront one 64-wide row segment, so vertical neighbours of
+        # a stencil are in the same workgroup (and L1) instead of in other
+        # workgroups.
+        ti, tj = tile
+        tiles_j = grid[1] // tj
+        cursor.emit(f"const unsigned int _tw = _blk % {tiles_j}u;")
+        cursor.emit(f"const unsigned int _th = _blk / {tiles_j}u;")
+        cursor.emit(f"const int _pid0 = (int)(_th * {ti}u + threadIdx.x / {tj}u);")
+        cursor.emit(f"const int _pid1 = (int)(_tw * {tj}u + threadIdx.x % {tj}u);")
+    else:
+        for axis in reversed(range(len(grid))):
+            g = grid[axis]
+            if axis == 0:
+                expr = rem
+            else:
+                expr = f"{rem} % {g}u" if g != 1 else "0u"
+            cursor.emit(f"const int _pid{axis} = (int)({expr});")
+            if axis > 0:
+                nxt = cursor.fresh("_q")
+                cursor.emit(f"const unsigned int {nxt} = {rem} / {g}u;")
+                rem = nxt
     for axis in range(len(grid)):
         pid_vals.append(CVal(f"_pid{axis}", (), "int"))
     env.pids = pid_vals  # type: ignore[attr-defined]
