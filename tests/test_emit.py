@@ -175,3 +175,30 @@ def test_xcd_remap_is_a_bijection():
             blk = xcd * (per + 1) + slot if xcd < rem else rem * (per + 1) + (xcd - rem) * per + slot
             seen.add(blk)
         assert seen == set(range(nb))
+
+
+def test_two_d_tile_order_is_a_bijection():
+    from palladium_amd.emit.core import _tile2d
+
+    for grid, block in (((64, 128), 256), ((4096, 4096), 256), ((8, 64), 512)):
+        tile = _tile2d(grid, block)
+        assert tile is not None
+        ti, tj = tile
+        tiles_j = grid[1] // tj
+        nblk = grid[0] * grid[1] // block
+        if nblk > 4096:
+            continue
+        seen = set()
+        for blk in range(nblk):
+            tw, th = blk % tiles_j, blk // tiles_j
+            for t in range(block):
+                seen.add((th * ti + t // tj, tw * tj + t % tj))
+        assert seen == {(i, j) for i in range(grid[0]) for j in range(grid[1])}
+
+
+def test_two_d_tile_only_when_it_divides():
+    from palladium_amd.emit.core import _tile2d
+
+    assert _tile2d((3, 128), 256) is None  # rows not a multiple of 4
+    assert _tile2d((8, 100), 256) is None  # cols not a multiple of 64
+    assert _tile2d((8,), 256) is None
