@@ -334,6 +334,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="lv")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true", help="skip the Gray-Scott line in the default run")
     a = ap.parse_args()
     if a.gpus != 1:
         print(
@@ -347,6 +348,12 @@ def main() -> int:
     if a.workload not in fns:
         raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")
     res = fns[a.workload](a.steps, a.warmup, cpu=not a.no_cpu and rank == 0)
+    if a.workload == "lv" and not a.no_secondary:
+        # The headline metric names two rooflines: RK4 LV against FP32 VALU
+        # (above) and the Gray-Scott stencil against HBM; report the second
+        # beside the first.
+        gs = bench_gs(a.steps, a.warmup, cpu=False)
+        res["secondary"] = {"gray_scott_4096": {k: gs[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline")}}
     if rank == 0:
         print(json.dumps(res), flush=True)
     return 0
