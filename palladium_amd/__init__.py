@@ -157,7 +157,7 @@ class HipCallable:
                     log_compile(spec, self._threadgroup, self._math_mode)
                     from palladium_amd.dispatch import _block_of
 
-                    b = bind(spec, emit_hip(spec, block=_block_of(self._threadgroup)),
+                    b = bind(spec, emit_hip(spec, block=_block_of(self._threadgroup), math_mode=self._math_mode),
                              math_mode=self._math_mode, threadgroup=self._threadgroup)
                     self.cache[key] = b
         return b

@@ -155,7 +155,7 @@ def explain_spec(spec: KernelSpec, threadgroup: Any = None, math_mode: Any = Non
     from palladium_amd.dispatch import _block_of
 
     block = _block_of(threadgroup)
-    src = emit_hip(spec, block=block)
+    src = emit_hip(spec, block=block, math_mode=math_mode)
     geo = launch_geometry(spec, block)
     res = None
     if compile:

@@ -34,6 +34,7 @@ import numpy as np
 
 from palladium_amd.errors import EmitError, UnsupportedPrimitiveError
 from palladium_amd.ir import Jaxpr, JaxprEqn, KeyAval, Literal, NDIndexer, Slice, Var
+from palladium_amd.runtime import math_mode_ordinal
 from palladium_amd.trace import BlockInfo, KernelSpec
 
 __all__ = [
@@ -430,13 +431,16 @@ def launch_geometry(spec: KernelSpec, block: int | None = None, lanes: int | Non
     return LaunchGeometry(b, (threads + b - 1) // b, n, lanes)
 
 
-def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None = None) -> str:
+def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None = None,
+             math_mode: Any = None) -> str:
     """Assemble the complete HIP source for a KernelSpec.
 
     Signature convention (relied on by the launcher): one pointer per
     operand in jaxpr order, inputs (`const T* __restrict__`) then outputs
     (`T* __restrict__`), and nothing else; the grid and block shapes are
-    compile-time constants of the source.
+    compile-time constants of the source. With `math_mode` FAST the jaxpr
+    first goes through the FAST-only algebraic rewrites of
+    `palladium_amd.emit.optimize`.
 
     Raises
     ------
@@ -519,7 +523,12 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         cursor.emit(f"{ptr} = arg{k}_base + {offset};" if offset != "0" else f"{ptr} = arg{k}_base;")
         ref_vals.append(CVal(f"arg{k}", info.block_shape or (1,), ct, "global", k < n_in))
 
-    emit_jaxpr(env, cursor, plan.jaxpr if plan else spec.jaxpr, ref_vals)
+    body = plan.jaxpr if plan else spec.jaxpr
+    if math_mode is not None and math_mode_ordinal(math_mode) == 2:
+        from palladium_amd.emit.optimize import factor_common_products
+
+        body = factor_common_products(body)
+    emit_jaxpr(env, cursor, body, ref_vals)
 
     head = (
         f'extern "C" __global__ void __launch_bounds__({geo.block})\n{name}(\n    '

@@ -114,7 +114,7 @@ class FfiCallable:
                     spec = trace(self._staged, *args)
                     check_block_bounds(spec)
                     log_compile(spec, self._threadgroup, self._math_mode)
-                    entry = (spec, emit_hip(spec, block=_block_of(self._threadgroup)))
+                    entry = (spec, emit_hip(spec, block=_block_of(self._threadgroup), math_mode=self._math_mode))
                     self._cache[key] = entry
         return entry
 

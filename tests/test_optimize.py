@@ -1,0 +1,116 @@
+"""FAST-only jaxpr rewrite `factor_common_products` (CPU, interpreter)."""
+
+import dataclasses
+
+import numpy as np
+
+from palladium_amd.emit import emit_hip
+from palladium_amd.emit.optimize import factor_common_products
+from palladium_amd.frontend import jnp, pl
+from palladium_amd.interpret import interpret_spec
+from palladium_amd.trace import trace
+from palladium_amd.workloads import (
+    BS3Config,
+    bs3_inputs,
+    bs3_vdp_call,
+    gray_scott_call,
+    gray_scott_initial,
+    lv_inputs,
+    lv_rk4_call,
+)
+
+
+def _count(jaxpr, name):
+    n = 0
+    for e in jaxpr.eqns:
+        n += e.primitive.name == name
+        for v in e.params.values():
+            sub = getattr(v, "jaxpr", v)
+            if hasattr(sub, "eqns"):
+                n += _count(sub, name)
+    return n
+
+
+def _rewritten(spec):
+    return dataclasses.replace(spec, jaxpr=factor_common_products(spec.jaxpr))
+
+
+def test_lv_rhs_is_factored_and_agrees_within_rounding():
+    args = lv_inputs(2000, 3)
+    spec = trace(lv_rk4_call(2000, 0.01, 100, track_max=True)._staged, *args)
+    opt = _rewritten(spec)
+    # Two products per rhs component and four rhs evaluations: one mul saved
+    # per component per stage.
+    assert _count(opt.jaxpr, "mul") == _count(spec.jaxpr, "mul") - 8
+    want = interpret_spec(spec, *args)
+    got = interpret_spec(opt, *args)
+    for g, w in zip(got, want):
+        np.testing.assert_allclose(g, w, rtol=2e-5)
+
+
+def test_rewrite_keeps_multi_use_products():
+    def kernel(a_ref, x_ref, o_ref, p_ref):
+        a = a_ref[...]
+        x = x_ref[...]
+        ax = a * x
+        o_ref[...] = ax - x * x
+        p_ref[...] = ax  # second use: ax must survive
+
+    a = np.linspace(1, 2, 64, dtype=np.float32)
+    x = np.linspace(-1, 3, 64, dtype=np.float32)
+    call = pl.pallas_call(kernel, out_shape=(pl.ShapeDtypeStruct((64,), np.float32),) * 2)
+    spec = trace(call, a, x)
+    opt = _rewritten(spec)
+    assert _count(opt.jaxpr, "mul") == _count(spec.jaxpr, "mul")
+    for g, w in zip(interpret_spec(opt, a, x), interpret_spec(spec, a, x)):
+        np.testing.assert_array_equal(g, w)
+
+
+def test_rewrite_factors_literal_and_var_chains():
+    def kernel(x_ref, y_ref, o_ref):
+        x = x_ref[...]
+        y = y_ref[...]
+        o_ref[...] = (2.0 * x) * y + (3.0 * y) * x
+
+    x = np.linspace(1, 2, 64, dtype=np.float32)
+    y = np.linspace(-1, 3, 64, dtype=np.float32)
+    call = pl.pallas_call(kernel, out_shape=pl.ShapeDtypeStruct((64,), np.float32))
+    spec = trace(call, x, y)
+    opt = _rewritten(spec)
+    assert _count(opt.jaxpr, "mul") == _count(spec.jaxpr, "mul") - 1
+    np.testing.assert_allclose(interpret_spec(opt, x, y)[0], 5 * x * y, rtol=1e-6)
+
+
+def test_integer_arithmetic_is_untouched():
+    def kernel(x_ref, o_ref):
+        x = x_ref[...]
+        o_ref[...] = x * 3 - x * 5
+
+    x = np.arange(64, dtype=np.int32)
+    call = pl.pallas_call(kernel, out_shape=pl.ShapeDtypeStruct((64,), np.int32))
+    spec = trace(call, x)
+    assert _count(_rewritten(spec).jaxpr, "mul") == _count(spec.jaxpr, "mul")
+
+
+def test_gray_scott_and_bs3_agree_after_rewrite():
+    u0, v0 = gray_scott_initial(32)
+    spec = trace(gray_scott_call(size=32)._staged, u0, v0)
+    opt = _rewritten(spec)
+    for g, w in zip(interpret_spec(opt, u0, v0), interpret_spec(spec, u0, v0)):
+        np.testing.assert_allclose(g, w, rtol=1e-5, atol=1e-6)
+    cfg = dataclasses.replace(BS3Config(), n=128, t1=2.0)
+    args = bs3_inputs(128)
+    spec = trace(bs3_vdp_call(128, cfg)._staged, *args)
+    opt = _rewritten(spec)
+    got = interpret_spec(opt, *args)
+    want = interpret_spec(spec, *args)
+    np.testing.assert_allclose(got[0], want[0], rtol=1e-3, atol=1e-4)
+
+
+def test_emitter_applies_rewrite_only_under_fast():
+    args = lv_inputs(256, 0)
+    spec = trace(lv_rk4_call(256, 0.01, 10)._staged, *args)
+    safe = emit_hip(spec, math_mode="safe")
+    fast = emit_hip(spec, math_mode="fast")
+    assert safe == emit_hip(spec)
+    assert fast.count(" * ") < safe.count(" * ")
