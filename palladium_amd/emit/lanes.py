@@ -293,6 +293,18 @@ class _Pass:
                 return
             out(U)
             return
+        if name == "dot_general":
+            (lc, rc), (lb, rb) = e.params["dimension_numbers"]
+            if ins_st[1] == L or tuple(lb) or tuple(rb):
+                raise _Bail("dot_general with a lane rhs or batch dims")
+            if ins_st[0] == U:
+                out(U)
+                return
+            lcd = [int(d) for d in lc]
+            if 0 in lcd:
+                raise _Bail("dot_general contracts over the lane dim")
+            out(L, params={**e.params, "dimension_numbers": ((tuple(d - 1 for d in lcd), tuple(rc)), ((), ()))})
+            return
         if name in _REDUCE:
             axes = tuple(int(x) for x in e.params["axes"])
             if ins_st[0] == U:

@@ -339,6 +339,93 @@ def _rule_transpose(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     _emit_elementwise_loops(cursor, dst, body)
 
 
+# Contractions up to this length are fully unrolled; longer ones stay loops.
+DOT_UNROLL_LIMIT = 32
+
+
+@rule("dot_general")
+def _rule_dot_general(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
+    """Per-instance contraction of rank-1/rank-2 operands over one dim
+    (reference: `src/palladium/emit/rules.py:408-499`).
+
+    Any single contracting dim on either side is accepted (the reference
+    takes only lhs dim 1 with rhs dim 0 and materialises transposes first);
+    the operand strides absorb the layout, so `a.T @ b` reads `a` in place.
+    Output dims are the lhs free dim then the rhs free dim, as in JAX.
+    Accumulation runs in the output ctype (`preferred_element_type`), each
+    product formed after converting its operands to it, in k order from
+    zero: under SAFE math this is the exact sequence `acc = acc + a*b`. In
+    the lane-parallel lowering the lhs rows are spread across lanes, so a
+    block matmul `(B, K) @ (K, N)` becomes one `(K,) @ (K, N)` row per lane
+    with the rhs read uniformly by the whole wavefront.
+    """
+    (lc, rc), (lb, rb) = eqn.params["dimension_numbers"]
+    if tuple(lb) or tuple(rb):
+        raise EmitError("dot_general: batch dims are unimplemented")
+    if len(lc) != 1 or len(rc) != 1:
+        raise EmitError("dot_general: exactly one contracting dim per operand is implemented")
+    lhs = env.val(eqn.invars[0])
+    rhs = env.val(eqn.invars[1])
+    if len(lhs.shape) not in (1, 2) or len(rhs.shape) not in (1, 2):
+        raise EmitError("dot_general: only rank-1/rank-2 operands are implemented")
+    lcd, rcd = int(lc[0]), int(rc[0])
+    k = lhs.shape[lcd]
+    if rhs.shape[rcd] != k:
+        raise EmitError(f"dot_general: inner dims disagree ({k} vs {rhs.shape[rcd]})")
+    ls, rs = element_strides(lhs.shape), element_strides(rhs.shape)
+    lfree = [d for d in range(len(lhs.shape)) if d != lcd]
+    rfree = [d for d in range(len(rhs.shape)) if d != rcd]
+    m = lhs.shape[lfree[0]] if lfree else 1
+    n = rhs.shape[rfree[0]] if rfree else 1
+    out = eqn.outvars[0]
+    ctype = ctype_of(out.aval.dtype)
+    scalar_out = m * n == 1
+    dst = None if scalar_out else declare(env, cursor, out)
+
+    def conv(expr: str, src: CVal) -> str:
+        return expr if src.ctype == ctype else f"(({ctype}){expr})"
+
+    def term(idx: list[tuple[str, int]]) -> str:
+        return flat_index([(v, st) for v, st in idx if v != "0"])
+
+    def contraction(i: str, j: str) -> str:
+        acc = cursor.fresh("_acc")
+        cursor.emit(f"{ctype} {acc} = ({ctype})0;")
+
+        def step(kk: str) -> None:
+            li = term(([(i, ls[lfree[0]])] if lfree else []) + [(kk, ls[lcd])])
+            ri = term([(kk, rs[rcd])] + ([(j, rs[rfree[0]])] if rfree else []))
+            cursor.emit(f"{acc} = {acc} + {conv(lhs.at(li), lhs)} * {conv(rhs.at(ri), rhs)};")
+
+        if k <= DOT_UNROLL_LIMIT:
+            with cursor.loop(k, "_k") as kk:
+                step(kk)
+        else:
+            kk = cursor.fresh("_k")
+            with cursor.block(f"for (int {kk} = 0; {kk} < {k}; ++{kk})"):
+                step(kk)
+        return acc
+
+    if scalar_out:
+        env.bind(out, CVal(contraction("0", "0"), tuple(int(d) for d in out.aval.shape), ctype))
+        return
+
+    def rows(i: str) -> None:
+        if n == 1:
+            acc = contraction(i, "0")
+            cursor.emit(f"{dst.at(term([(i, 1)]) if m > 1 else '0')} = {acc};")
+            return
+        with cursor.loop(n, "_n") as j:
+            acc = contraction(i, j)
+            cursor.emit(f"{dst.at(term([(i, n), (j, 1)]))} = {acc};")
+
+    if m == 1:
+        rows("0")
+    else:
+        with cursor.loop(m, "_m") as i:
+            rows(i)
+
+
 @rule("program_id")
 def _rule_program_id(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     """`pl.program_id(axis)` binds the decoded grid coordinate (reference:

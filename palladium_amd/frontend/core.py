@@ -203,6 +203,8 @@ class Tracer:
     def __rtruediv__(self, o): return _jnp().divide(o, self)
     def __pow__(self, o): return _jnp().power(self, o)
     def __rpow__(self, o): return _jnp().power(o, self)
+    def __matmul__(self, o): return _jnp().matmul(self, o)
+    def __rmatmul__(self, o): return _jnp().matmul(o, self)
     def __neg__(self): return _jnp().negative(self)
     def __pos__(self): return self
     def __abs__(self): return _jnp().abs(self)

@@ -205,6 +205,56 @@ def reshape(x: Tracer, new_sizes: Sequence[int]) -> Tracer:
     return _stage("reshape", [x], new_t, x.dtype, x.weak_type, new_sizes=new_t, dimensions=None, sharding=None)
 
 
+def dot_general(lhs: Any, rhs: Any, dimension_numbers: Any, precision: Any = None,
+                preferred_element_type: Any = None) -> Tracer:
+    """Stage `dot_general` as JAX does: output dims are the lhs free dims,
+    then the rhs free dims (batch dims are not supported)."""
+    (lc, rc), (lb, rb) = dimension_numbers
+    lc, rc, lb, rb = (tuple(int(d) for d in t) for t in (lc, rc, lb, rb))
+    if lb or rb:
+        raise TraceError("dot_general: batch dimensions are not supported")
+    if not isinstance(lhs, Tracer):
+        lhs = asarray(lhs)
+    if not isinstance(rhs, Tracer):
+        rhs = asarray(rhs)
+    if len(lc) != len(rc) or builtins.any(lhs.shape[a] != rhs.shape[b] for a, b in zip(lc, rc)):
+        raise TraceError(f"dot_general: contracting dims disagree ({lhs.shape} vs {rhs.shape})")
+    dt = _result_dtype([lhs, rhs])
+    if lhs.dtype != dt:
+        lhs = convert_element_type(lhs, dt)
+    if rhs.dtype != dt:
+        rhs = convert_element_type(rhs, dt)
+    out_dt = np.dtype(preferred_element_type) if preferred_element_type is not None else dt
+    shape = tuple(d for k, d in enumerate(lhs.shape) if k not in lc) + tuple(
+        d for k, d in enumerate(rhs.shape) if k not in rc)
+    return _stage("dot_general", [lhs, rhs], shape, out_dt, False,
+                  dimension_numbers=((lc, rc), ((), ())), precision=precision,
+                  preferred_element_type=out_dt, out_sharding=None)
+
+
+def dot(a: Any, b: Any, *, precision: Any = None, preferred_element_type: Any = None) -> Tracer:
+    """`jnp.dot` for rank <= 2: contracts a's last dim with b's first
+    (b's only dim when b is a vector)."""
+    a_nd = len(_shape_of(a))
+    b_nd = len(_shape_of(b))
+    if a_nd == 0 or b_nd == 0:
+        return multiply(a, b)
+    if a_nd > 2 or b_nd > 2:
+        raise TraceError("dot: operands of rank > 2 are not supported")
+    rc = 0 if b_nd == 1 else b_nd - 2
+    return dot_general(a, b, (((a_nd - 1,), (rc,)), ((), ())), precision, preferred_element_type)
+
+
+def matmul(a: Any, b: Any, *, precision: Any = None, preferred_element_type: Any = None) -> Tracer:
+    if len(_shape_of(a)) == 0 or len(_shape_of(b)) == 0:
+        raise TraceError("matmul: operands must have rank >= 1")
+    return dot(a, b, precision=precision, preferred_element_type=preferred_element_type)
+
+
+def vdot(a: Tracer, b: Tracer) -> Tracer:
+    return dot(reshape(a, (math.prod(a.shape),)), reshape(b, (math.prod(b.shape),)))
+
+
 def transpose(x: Tracer, axes: Sequence[int] | None = None) -> Tracer:
     perm = tuple(axes) if axes is not None else tuple(reversed(range(x.ndim)))
     shape = tuple(x.shape[p] for p in perm)

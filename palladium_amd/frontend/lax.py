@@ -69,6 +69,12 @@ ne = jnp.not_equal
 
 
 broadcasted_iota = jnp.broadcasted_iota
+dot_general = jnp.dot_general
+transpose = jnp.transpose
+
+
+def dot(lhs: Any, rhs: Any, precision: Any = None, preferred_element_type: Any = None) -> Tracer:
+    return jnp.dot(lhs, rhs, precision=precision, preferred_element_type=preferred_element_type)
 
 
 def iota(dtype: Any, size: int) -> Tracer:

@@ -295,6 +295,8 @@ def _eval(jaxpr: Jaxpr, env: _Env, invals: list[Any], mask: np.ndarray) -> list[
             src = env.read(eqn.invars[0])
             perm = tuple(eqn.params["permutation"])
             env.write(eqn.outvars[0], np.transpose(src, (0,) + tuple(p + 1 for p in perm)).copy())
+        elif name == "dot_general":
+            env.write(eqn.outvars[0], _dot_general(eqn, env.read(eqn.invars[0]), env.read(eqn.invars[1]), n))
         elif name in ("reduce_sum", "reduce_max", "reduce_min", "reduce_or", "reduce_and"):
             src = np.asarray(env.read(eqn.invars[0]))
             axes = tuple(int(a) + 1 for a in eqn.params["axes"])
@@ -344,6 +346,27 @@ def _eval(jaxpr: Jaxpr, env: _Env, invals: list[Any], mask: np.ndarray) -> list[
         else:
             raise UnsupportedPrimitiveError(f"interpreter has no rule for primitive '{name}'")
     return [env.read(v) for v in jaxpr.outvars]
+
+
+def _dot_general(eqn: JaxprEqn, lhs: Any, rhs: Any, n: int) -> np.ndarray:
+    """Contraction accumulated in k order from zero in the output dtype,
+    `acc = acc + a*b`, the operation sequence the emitter produces."""
+    (lc, rc), _ = eqn.params["dimension_numbers"]
+    out_dt = np.dtype(eqn.outvars[0].aval.dtype)
+    la, ra = eqn.invars[0].aval, eqn.invars[1].aval
+    lhs = np.broadcast_to(np.asarray(lhs), (n,) + tuple(la.shape)).astype(out_dt)
+    rhs = np.broadcast_to(np.asarray(rhs), (n,) + tuple(ra.shape)).astype(out_dt)
+    # Move the contracting dim last on both sides: (n, m?, k) and (n, n_?, k).
+    lhs = np.moveaxis(lhs, int(lc[0]) + 1, -1)
+    rhs = np.moveaxis(rhs, int(rc[0]) + 1, -1)
+    m_shape, r_shape = lhs.shape[1:-1], rhs.shape[1:-1]
+    a = lhs.reshape(n, -1, 1, lhs.shape[-1])
+    b = rhs.reshape(n, 1, -1, rhs.shape[-1])
+    acc = np.zeros((n, a.shape[1], b.shape[2]), out_dt)
+    with np.errstate(all="ignore"):
+        for kk in range(a.shape[-1]):
+            acc = acc + a[..., kk] * b[..., kk]
+    return acc.reshape((n,) + tuple(m_shape) + tuple(r_shape))
 
 
 def _full(val: Any, aval: Any, n: int) -> np.ndarray:
