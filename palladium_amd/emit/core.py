@@ -55,6 +55,7 @@ PRIMITIVE_INVARS = string.ascii_lowercase[:MAX_PRIMITIVE_ARITY]
 
 CTYPES = {
     "float32": "float",
+    "float16": "_Float16",
     "int32": "int",
     "uint32": "unsigned int",
     "bool": "bool",
@@ -202,7 +203,10 @@ def literal_cval(v: Any, dtype: Any) -> CVal:
     dt = np.dtype(dtype)
     ctype = ctype_of(dt)
     if dt.kind == "f":
-        expr = format_float(v)
+        # Round to the literal's own type first: a float16 literal is emitted
+        # as the float32 spelling of its float16 value (exact), so mixed
+        # expressions round exactly as float16 arithmetic would.
+        expr = format_float(float(np.asarray(v, dt)))
     elif dt.kind == "b":
         expr = "true" if v else "false"
     elif dt.kind == "u":

@@ -36,10 +36,15 @@ from palladium_amd.emit.core import (
 from palladium_amd.ir import JaxprEqn, KeyAval, Literal, Var
 
 F32 = "float"
+F16 = "_Float16"
+FLOAT_CTYPES = (F32, F16)
 
 
 def _is_float(c: CVal) -> bool:
-    return c.ctype == "float"
+    """float32 and float16 share every template: float16 operands promote to
+    float in the float functions, and assigning the result to a float16
+    variable rounds it once."""
+    return c.ctype in FLOAT_CTYPES
 
 
 # ---------------------------------------------------------------------------
@@ -598,11 +603,13 @@ def _emit_reduce(env: Environment, cursor: Cursor, eqn: JaxprEqn, init: str, com
 def _reduce_init(eqn: JaxprEqn, kind: str) -> str:
     ct = ctype_of(eqn.outvars[0].aval.dtype)
     if kind == "sum":
-        return "0.0f" if ct == "float" else "0"
+        return "0.0f" if ct in FLOAT_CTYPES else "0"
     if kind == "max":
-        return {"float": "(-__builtin_inff())", "int": "(-2147483647 - 1)", "unsigned int": "0u", "bool": "false"}[ct]
+        return {"float": "(-__builtin_inff())", F16: "(-__builtin_inff())", "int": "(-2147483647 - 1)",
+                "unsigned int": "0u", "bool": "false"}[ct]
     if kind == "min":
-        return {"float": "__builtin_inff()", "int": "2147483647", "unsigned int": "0xFFFFFFFFu", "bool": "true"}[ct]
+        return {"float": "__builtin_inff()", F16: "__builtin_inff()", "int": "2147483647",
+                "unsigned int": "0xFFFFFFFFu", "bool": "true"}[ct]
     return {"or": "false", "and": "true"}[kind]
 
 
@@ -613,14 +620,14 @@ def _rule_reduce_sum(env, cursor, eqn):
 
 @rule("reduce_max")
 def _rule_reduce_max(env, cursor, eqn):
-    f = ctype_of(eqn.outvars[0].aval.dtype) == "float"
+    f = ctype_of(eqn.outvars[0].aval.dtype) in FLOAT_CTYPES
     _emit_reduce(env, cursor, eqn, _reduce_init(eqn, "max"),
                  (lambda a, x: f"ph_fmax({a}, {x})") if f else (lambda a, x: f"(({x} > {a}) ? {x} : {a})"))
 
 
 @rule("reduce_min")
 def _rule_reduce_min(env, cursor, eqn):
-    f = ctype_of(eqn.outvars[0].aval.dtype) == "float"
+    f = ctype_of(eqn.outvars[0].aval.dtype) in FLOAT_CTYPES
     _emit_reduce(env, cursor, eqn, _reduce_init(eqn, "min"),
                  (lambda a, x: f"ph_fmin({a}, {x})") if f else (lambda a, x: f"(({x} < {a}) ? {x} : {a})"))
 
@@ -799,11 +806,14 @@ def _rule_lane_reduce(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     out = eqn.outvars[0]
     ct = ctype_of(out.aval.dtype)
     is_bool = ct == "bool"
-    wt = "int" if is_bool else ct
+    # Shuffles move 32-bit values: bools travel as int, float16 as float
+    # (a float16 sum is then accumulated in float32 and rounded once).
+    wt = "int" if is_bool else (F32 if ct == F16 else ct)
+    isf = ct in FLOAT_CTYPES
     comb = {
         "sum": lambda a, b: f"({a} + {b})",
-        "max": (lambda a, b: f"ph_fmax({a}, {b})") if ct == "float" else (lambda a, b: f"(({a} > {b}) ? {a} : {b})"),
-        "min": (lambda a, b: f"ph_fmin({a}, {b})") if ct == "float" else (lambda a, b: f"(({a} < {b}) ? {a} : {b})"),
+        "max": (lambda a, b: f"ph_fmax({a}, {b})") if isf else (lambda a, b: f"(({a} > {b}) ? {a} : {b})"),
+        "min": (lambda a, b: f"ph_fmin({a}, {b})") if isf else (lambda a, b: f"(({a} < {b}) ? {a} : {b})"),
         "or": lambda a, b: f"({a} | {b})",
         "and": lambda a, b: f"({a} & {b})",
     }[kind]

@@ -39,7 +39,9 @@ I32 = np.dtype(np.int32)
 U32 = np.dtype(np.uint32)
 BOOL = np.dtype(np.bool_)
 
-SUPPORTED_DTYPES = (F32, I32, U32, BOOL)
+F16 = np.dtype(np.float16)
+
+SUPPORTED_DTYPES = (F32, F16, I32, U32, BOOL)
 
 _state = threading.local()
 

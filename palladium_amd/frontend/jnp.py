@@ -32,6 +32,7 @@ from palladium_amd.frontend.core import (
 from palladium_amd.ir import KeyAval, Literal, ShapedArray
 
 float32 = np.float32
+float16 = np.float16
 int32 = np.int32
 uint32 = np.uint32
 bool_ = np.bool_
@@ -77,8 +78,10 @@ def _result_dtype(args: Sequence[Any]) -> np.dtype:
         dt = strong[0]
         for d in strong[1:]:
             if d != dt:
-                if d.kind == "f" or dt.kind == "f":
-                    dt = F32
+                if d.kind == "f" and dt.kind == "f":
+                    dt = F32  # float16 with float32
+                elif d.kind == "f" or dt.kind == "f":
+                    dt = d if d.kind == "f" else dt
                 elif {d, dt} <= {I32, U32, BOOL}:
                     dt = I32 if BOOL in (d, dt) and U32 not in (d, dt) else (U32 if U32 in (d, dt) and BOOL in (d, dt) else I32)
                 else:
