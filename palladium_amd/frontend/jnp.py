@@ -474,6 +474,8 @@ def _reduce(name: str, x: Tracer, axis: Any, out_dtype: np.dtype | None = None) 
         x = asarray(x)
     if axis is None:
         axes = tuple(range(x.ndim))
+    elif x.ndim == 0:
+        raise TraceError(f"{name}: axis {axis} is out of range for a rank-0 value")
     elif isinstance(axis, int):
         axes = (axis % x.ndim,)
     else:
