@@ -22,6 +22,8 @@ import time
 
 import numpy as np
 
+from palladium_amd.trace import trace
+
 FP32_PEAK = 157.3e12
 HBM_PEAK = 8.0e12
 # rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 for one config-1 launch.
@@ -151,6 +153,36 @@ def _timed_launches(bound, ops, steps: int, warmup: int):
     return evs[0].elapsed_ms(evs[-1]) / steps, float(np.mean(per))
 
 
+# Algorithmic 32-bit integer ops of one Threefry-2x32-20 block: 20 rounds of
+# (add, rotate, xor), five key injections of two adds each, two initial adds.
+THREEFRY_OPS = 20 * 3 + 5 * 2 + 2
+# Data movement and reinterpretation, not arithmetic.
+_NOT_OPS = {"broadcast_in_dim", "bitcast_convert_type", "reshape", "squeeze", "expand_dims", "get", "swap",
+            "program_id", "num_programs", "random_wrap", "random_unwrap"}
+
+
+def loop_ops_per_iteration(spec, loop: str) -> int:
+    """Elementwise ops executed per iteration of the kernel's `loop`
+    (`while`: condition + body; `scan`: body), counted from the IR: one per
+    eqn (pow = 1), THREEFRY_OPS per threefry2x32, nothing for data movement."""
+    def count(j) -> int:
+        n = 0
+        for e in j.eqns:
+            name = e.primitive.name
+            if name == "threefry2x32":
+                n += THREEFRY_OPS
+            elif name not in _NOT_OPS and not any(hasattr(getattr(v, "jaxpr", v), "eqns") for v in e.params.values()):
+                n += 1
+        return n
+
+    for e in spec.jaxpr.eqns:
+        if e.primitive.name == loop:
+            if loop == "while":
+                return count(e.params["cond_jaxpr"].jaxpr) + count(e.params["body_jaxpr"].jaxpr)
+            return count(getattr(e.params["jaxpr"], "jaxpr", e.params["jaxpr"]))
+    raise ValueError(f"no {loop} in the kernel")
+
+
 def _base(metric: str, value: float, unit: str, steps: int, warmup: int, ms: float, config: dict) -> dict:
     return {
         "metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
@@ -166,14 +198,19 @@ def bench_gbm(steps: int, warmup: int, cpu: bool) -> dict:
 
     cfg = GBM_CFG
     key = random.key(cfg.seed)
-    bound = gbm_call(cfg).bound(key)
+    call = gbm_call(cfg)
+    bound = call.bound(key)
     ops = [rt.Buffer.from_numpy(key), rt.Buffer.empty((cfg.n_paths,), np.float32)]
     ms, avg = _timed_launches(bound, ops, steps, warmup)
     ps = cfg.n_paths * cfg.n_steps
     res = _base("GBM path-steps/s (4,194,304 paths x 252 steps, Threefry + Box-Muller, fp32)", ps / (ms / 1e3),
                 "path-steps/s", steps, warmup, ms,
                 {"workload": "GBM Monte Carlo, config 3", "paths": cfg.n_paths, "steps": cfg.n_steps, "math_mode": "fast"})
-    res["roofline"] = {"bound": "valu", "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None,
+    per_step = loop_ops_per_iteration(trace(call._staged, key), "scan")
+    achieved = ps * per_step / (avg / 1e3)
+    res["roofline"] = {"bound": "valu", "achieved": achieved / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TOP/s",
+                       "frac": achieved / FP32_PEAK, "traffic": None, "ops_per_path_step": per_step,
+                       "ops_note": f"staged elementwise ops per step, Threefry-2x32-20 = {THREEFRY_OPS} integer ops",
                        "avg_launch_ms": avg}
     if cpu:
         import oracle
@@ -300,7 +337,8 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
 
     cfg = BS3_CFG
     host = bs3_inputs(cfg.n)
-    bound = bs3_vdp_call(cfg.n).bound(*host)
+    call = bs3_vdp_call(cfg.n)
+    bound = call.bound(*host)
     ins = [rt.Buffer.from_numpy(a) for a in host]
     outs = [rt.Buffer.empty((cfg.n,), np.float32) for _ in range(3)] + [rt.Buffer.empty((cfg.n,), np.int32) for _ in range(2)]
     ms, avg = _timed_launches(bound, ins + outs, steps, warmup)
@@ -312,7 +350,11 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     total = int(attempts.sum())
     res = _base("BS3(2)+PI attempted steps/s (Van der Pol, N=262,144, fp32)", total / (ms / 1e3), "attempts/s",
                 steps, warmup, ms, {"workload": "adaptive BS3(2) Van der Pol, config 2", "n": cfg.n, "math_mode": "fast"})
-    res["roofline"] = {"bound": "valu", "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None,
+    ops = loop_ops_per_iteration(trace(call._staged, *host), "while")
+    achieved = total * ops / (avg / 1e3)
+    res["roofline"] = {"bound": "valu", "achieved": achieved / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TOP/s",
+                       "frac": achieved / FP32_PEAK, "traffic": None, "ops_per_attempt": ops,
+                       "ops_note": "elementwise eqns of the while condition + body per attempt (pow = 1)",
                        "avg_launch_ms": avg, "active_lane_fraction": active, "total_attempts": total,
                        "accepted": int(acc.sum()), "rejected": int(rej.sum())}
     if cpu:

@@ -47,7 +47,7 @@ int hip_fail(char **err, hipError_t e, const char *what) {
 const char *kOptions[3] = {
     "-ffp-contract=off",
     "-ffp-contract=fast",
-    "-ffp-contract=fast -ffast-math -fno-finite-math-only "
+    "-ffp-contract=fast -ffast-math -fno-finite-math-only -fgpu-flush-denormals-to-zero "
     "-fno-hip-fp32-correctly-rounded-divide-sqrt",
 };
 

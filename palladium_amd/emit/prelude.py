@@ -8,8 +8,9 @@
 - `ph_pow`: under SAFE math (`PH_MATH_MODE == 0`) a deterministic power
   function built only from IEEE double add/mul/div/fma, so a host build of
   the same sequence returns bit-identical results; this is what makes
-  adaptive accept/reject decisions reproducible on the CPU. Under
-  RELAXED/FAST it is the device `powf`.
+  adaptive accept/reject decisions reproducible on the CPU. Under RELAXED
+  it is the device `powf`; under FAST, 2^(y log2 x) on the hardware base-2
+  transcendentals for positive normal bases (powf otherwise).
   Method: x = m * 2^e with m in [sqrt(1/2), sqrt(2)); ln m = 2 atanh(t),
   t = (m-1)/(m+1), as an odd series in t; exp by reduction z = k ln2 + r,
   |r| <= ln2/2, and a degree-13 Taylor polynomial; both carried in double,
@@ -133,6 +134,16 @@ __device__ __noinline__ float ph_pow(float x, float y) {
     if (z > 89.0) return sign * __builtin_inff();
     if (z < -104.0) return sign * 0.0f;
     return sign * (float)ph_exp_dbl(z);
+}
+#elif PH_MATH_MODE == 2
+/* FAST: x^y = 2^(y log2 x) on the hardware base-2 logarithm and
+   exponential (v_log_f32, v_exp_f32) for a positive normal finite base and
+   a finite exponent; zero, negative, subnormal and non-finite operands take
+   the full powf. */
+__device__ __forceinline__ float ph_pow(float x, float y) {
+    if (x >= 0x1p-126f && x < __builtin_inff() && __builtin_fabsf(y) < __builtin_inff())
+        return __builtin_amdgcn_exp2f(y * __builtin_amdgcn_logf(x));
+    return powf(x, y);
 }
 #else
 __device__ __forceinline__ float ph_pow(float x, float y) { return powf(x, y); }
