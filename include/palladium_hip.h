@@ -79,17 +79,33 @@ int ph_launch_ptrs(ph_kernel *k, unsigned int blocks, unsigned int block,
                    void *stream, void *const *ptrs, size_t n_ptrs, char **err);
 
 /* One synchronous dispatch of emitted source over host buffers: compile or
- * hit the cache, stage inputs host->device, launch ceil(prod(grid)/block)
- * workgroups of `block` lanes (0 = 256), copy outputs device->host, wait.
- * Attribute-for-attribute the reference's XLA FFI handler on the "cpu"
- * platform (native/ffi/palladium_ffi.cpp:110-209): source, function name,
- * grid, block (threadgroup), math mode, then inputs, then outputs. */
+ * hit the cache, stage inputs host->device, launch
+ * ceil(prod(grid) * lanes / block) workgroups of `block` threads (0 = 256),
+ * copy outputs device->host, wait. Attribute-for-attribute the reference's
+ * XLA FFI handler on the "cpu" platform (native/ffi/palladium_ffi.cpp:
+ * 110-209): source, function name, grid, block (threadgroup), math mode,
+ * then inputs, then outputs; plus `lanes`, the threads per program instance
+ * (1, or the block rows a lane-parallel kernel spreads across lanes), which
+ * Metal's one-thread-per-instance model has no use for. */
 int ph_dispatch(const char *src, size_t src_len, const char *name,
                 int64_t grid_x, int64_t grid_y, int64_t grid_z,
-                int64_t block_x, int64_t math_mode, const void *const *inputs,
-                const size_t *input_bytes, size_t n_inputs,
-                void *const *outputs, const size_t *output_bytes,
-                size_t n_outputs, char **err);
+                int64_t block_x, int64_t lanes, int64_t math_mode,
+                const void *const *inputs, const size_t *input_bytes,
+                size_t n_inputs, void *const *outputs,
+                const size_t *output_bytes, size_t n_outputs, char **err);
+
+/* The same dispatch over device buffers on the caller's stream: no
+ * staging, no allocation beyond the compile cache, no wait (the launch is
+ * ordered on `stream`; NULL = default stream). The body an XLA FFI handler
+ * on the "ROCM" platform needs (device buffers + the XLA stream), which the
+ * reference's Metal-only native/ffi/palladium_ffi.cpp:110-193 has no
+ * counterpart for. */
+int ph_dispatch_device(const char *src, size_t src_len, const char *name,
+                       int64_t grid_x, int64_t grid_y, int64_t grid_z,
+                       int64_t block_x, int64_t lanes, int64_t math_mode,
+                       void *stream, const void *const *inputs,
+                       size_t n_inputs, void *const *outputs,
+                       size_t n_outputs, char **err);
 
 /* Device memory, streams, events and graphs: the role metal-runtime's
  * Buffer/Batch/gpu_time play for the reference

@@ -234,24 +234,66 @@ int ph_launch_ptrs(ph_kernel *k, unsigned int blocks, unsigned int block,
                    n_ptrs ? params.data() : nullptr, err);
 }
 
-int ph_dispatch(const char *src, size_t src_len, const char *name,
-                int64_t grid_x, int64_t grid_y, int64_t grid_z, int64_t block_x,
-                int64_t math_mode, const void *const *inputs,
-                const size_t *input_bytes, size_t n_inputs,
-                void *const *outputs, const size_t *output_bytes,
-                size_t n_outputs, char **err) {
+namespace {
+
+// Validate the dispatch attributes and derive the 1-D launch: `lanes`
+// threads per program instance (1, or the block rows of a lane-parallel
+// kernel), ceil(programs * lanes / block) workgroups. This is the geometry
+// the emitter compiled into the source (its XCD remap and bounds guard).
+int dispatch_geometry(int64_t grid_x, int64_t grid_y, int64_t grid_z, int64_t block_x,
+                      int64_t lanes, int64_t math_mode, unsigned int *blocks,
+                      unsigned int *block, char **err) {
   if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_FAST)
     return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: math_mode out of range");
   if (grid_x <= 0 || grid_y <= 0 || grid_z <= 0)
     return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: grid dims must be positive");
-  int64_t programs = grid_x * grid_y * grid_z;
-  int64_t block = block_x > 0 ? block_x : 256;
-  if (block > 1024 || block % 64)
+  if (lanes <= 0 || lanes > 1024)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: lanes must be in [1, 1024]");
+  int64_t b = block_x > 0 ? block_x : 256;
+  if (b > 1024 || b % 64)
     return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: block must be a multiple of 64, at most 1024");
-  if (programs >= (int64_t(1) << 31))
+  if (grid_x >= (int64_t(1) << 31) || grid_y >= (int64_t(1) << 31) || grid_z >= (int64_t(1) << 31))
     return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: too many program instances");
+  int64_t threads = grid_x * grid_y;
+  if (threads >= (int64_t(1) << 31) || (threads *= grid_z) >= (int64_t(1) << 31) ||
+      (threads *= lanes) >= (int64_t(1) << 31))
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: too many program instances");
+  *block = (unsigned int)b;
+  *blocks = (unsigned int)((threads + b - 1) / b);
+  return PH_OK;
+}
+
+}  // namespace
+
+int ph_dispatch_device(const char *src, size_t src_len, const char *name,
+                       int64_t grid_x, int64_t grid_y, int64_t grid_z, int64_t block_x,
+                       int64_t lanes, int64_t math_mode, void *stream,
+                       const void *const *inputs, size_t n_inputs,
+                       void *const *outputs, size_t n_outputs, char **err) {
+  unsigned int blocks = 0, block = 0;
+  int rc = dispatch_geometry(grid_x, grid_y, grid_z, block_x, lanes, math_mode, &blocks, &block, err);
+  if (rc != PH_OK) return rc;
   ph_kernel *k = nullptr;
-  int rc = ph_get_kernel(src, src_len, name, (int)math_mode, &k, err);
+  rc = ph_get_kernel(src, src_len, name, (int)math_mode, &k, err);
+  if (rc != PH_OK) return rc;
+  std::vector<void *> ptrs;
+  ptrs.reserve(n_inputs + n_outputs);
+  for (size_t i = 0; i < n_inputs; ++i) ptrs.push_back(const_cast<void *>(inputs[i]));
+  for (size_t i = 0; i < n_outputs; ++i) ptrs.push_back(outputs[i]);
+  return ph_launch_ptrs(k, blocks, block, stream, ptrs.data(), ptrs.size(), err);
+}
+
+int ph_dispatch(const char *src, size_t src_len, const char *name,
+                int64_t grid_x, int64_t grid_y, int64_t grid_z, int64_t block_x,
+                int64_t lanes, int64_t math_mode, const void *const *inputs,
+                const size_t *input_bytes, size_t n_inputs,
+                void *const *outputs, const size_t *output_bytes,
+                size_t n_outputs, char **err) {
+  unsigned int blocks = 0, block = 0;
+  int rc = dispatch_geometry(grid_x, grid_y, grid_z, block_x, lanes, math_mode, &blocks, &block, err);
+  if (rc != PH_OK) return rc;
+  ph_kernel *k = nullptr;
+  rc = ph_get_kernel(src, src_len, name, (int)math_mode, &k, err);
   if (rc != PH_OK) return rc;
 
   hipStream_t stream = nullptr;
@@ -279,8 +321,7 @@ int ph_dispatch(const char *src, size_t src_len, const char *name,
       return hip_fail(err, e, "hipMemcpyHtoDAsync");
     }
   }
-  unsigned int blocks = (unsigned int)((programs + block - 1) / block);
-  rc = ph_launch_ptrs(k, blocks, (unsigned int)block, stream, dev.data(), dev.size(), err);
+  rc = ph_launch_ptrs(k, blocks, block, stream, dev.data(), dev.size(), err);
   if (rc != PH_OK) {
     cleanup();
     return rc;

@@ -66,6 +66,11 @@ def _register() -> None:
         handle = ctypes.CDLL(str(_library_path()))
         capsule = jax.ffi.pycapsule(handle.palladium_hip_dispatch)
         jax.ffi.register_ffi_target(_TARGET_NAME, capsule, platform="cpu")
+        # jax on ROCm: arrays already live in HBM, so the same target name
+        # resolves to the device-buffer handler on XLA's own stream.
+        if any(d.platform == "rocm" for d in jax.devices()):
+            rocm = jax.ffi.pycapsule(handle.palladium_hip_dispatch_rocm)
+            jax.ffi.register_ffi_target(_TARGET_NAME, rocm, platform="ROCM")
         _registered = True
 
 
@@ -134,6 +139,7 @@ class FfiCallable:
             grid_y=int(grid[1]),
             grid_z=int(grid[2]),
             block_x=int(geo.block),
+            lanes=int(geo.lanes),
             math_mode=int(self._math_mode),
         )
 

@@ -108,7 +108,10 @@ def _declare(L: ctypes.CDLL) -> None:
         "ph_launch": (c.c_int, [_P, c.c_uint, c.c_uint, c.c_uint, c.c_uint, c.c_uint, c.c_uint, c.c_uint, _P, _PP, _PP]),
         "ph_launch_ptrs": (c.c_int, [_P, c.c_uint, c.c_uint, _P, _PP, c.c_size_t, _PP]),
         "ph_dispatch": (c.c_int, [c.c_char_p, c.c_size_t, c.c_char_p, c.c_int64, c.c_int64, c.c_int64, c.c_int64, c.c_int64,
-                                  _PP, c.POINTER(c.c_size_t), c.c_size_t, _PP, c.POINTER(c.c_size_t), c.c_size_t, _PP]),
+                                  c.c_int64, _PP, c.POINTER(c.c_size_t), c.c_size_t, _PP, c.POINTER(c.c_size_t),
+                                  c.c_size_t, _PP]),
+        "ph_dispatch_device": (c.c_int, [c.c_char_p, c.c_size_t, c.c_char_p, c.c_int64, c.c_int64, c.c_int64, c.c_int64,
+                                         c.c_int64, c.c_int64, _P, _PP, c.c_size_t, _PP, c.c_size_t, _PP]),
         "ph_device_count": (c.c_int, [c.POINTER(c.c_int)]),
         "ph_device_name": (c.c_int, [c.c_char_p, c.c_size_t]),
         "ph_malloc": (c.c_int, [c.c_size_t, _PP, _PP]),
@@ -326,7 +329,12 @@ class Buffer:
     @classmethod
     def wrap(cls, obj: Any) -> "Buffer":
         """Zero-copy view of a device array (torch CUDA/HIP tensor or any
-        object exposing `__cuda_array_interface__`)."""
+        object exposing `__cuda_array_interface__`).
+
+        torch wheels carry their own libamdhip64. Import torch before this
+        module loads its native library, so that the library binds to the
+        runtime torch already holds: a process with two HIP runtimes loaded
+        leaves torch without a device."""
         if hasattr(obj, "data_ptr") and getattr(obj, "is_cuda", False):
             if not obj.is_contiguous():
                 raise ValueError("device tensors must be contiguous")

@@ -9,8 +9,9 @@ from palladium_amd.frontend import jnp, lax, pl
 F32 = np.float32
 
 
-def _call(kernel, grid, in_specs, out_spec, out_shape, **kw):
-    return pa.hip_call(kernel, grid=grid, in_specs=in_specs, out_specs=out_spec, out_shape=out_shape, **kw)
+def _call(kernel, grid, in_specs, out_spec, out_shape, factory=None, **kw):
+    factory = factory or pa.hip_call
+    return factory(kernel, grid=grid, in_specs=in_specs, out_specs=out_spec, out_shape=out_shape, **kw)
 
 
 def lane_rows(rng, b=128, k=8, n=4, rows=1024, **kw):

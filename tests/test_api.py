@@ -131,8 +131,17 @@ def test_hip_call_jit_ffi_attributes():
     attrs = call.ffi_attributes((np.zeros(4, F),))
     assert attrs["function_name"] == "<lambda>" or attrs["function_name"] == "palladium_kernel"
     assert (attrs["grid_x"], attrs["grid_y"], attrs["grid_z"]) == (1, 1, 1)
-    assert attrs["block_x"] == 256 and attrs["math_mode"] == 0
+    assert attrs["block_x"] == 256 and attrs["math_mode"] == 0 and attrs["lanes"] == 1
     assert "__global__" in attrs["hip_source"]
+
+
+def test_ffi_attributes_carry_lanes_of_a_lane_parallel_kernel():
+    from dot_cases import lane_rows
+
+    jit, inputs = lane_rows(np.random.default_rng(0), factory=pa.hip_call_jit)
+    attrs = jit.ffi_attributes(inputs)
+    # 8 programs of 128 rows: one workgroup of 128 lanes per program.
+    assert (attrs["grid_x"], attrs["block_x"], attrs["lanes"]) == (8, 128, 128)
 
 
 def test_math_mode_values():

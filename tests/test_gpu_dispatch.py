@@ -3,6 +3,7 @@ tests/test_11_ffi.py, tests/test_17_robustness.py)."""
 
 import ctypes
 import threading
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -108,14 +109,68 @@ def test_ph_dispatch_c_abi_host_buffers(rng):
     outs = (ctypes.c_void_p * 1)(out.ctypes.data)
     out_b = (ctypes.c_size_t * 1)(out.nbytes)
     err = ctypes.c_void_p()
-    rc = rt.lib().ph_dispatch(src, len(src), spec.name.encode(), n, 1, 1, 256, 0, ins, in_b, 1, outs, out_b, 1,
+    rc = rt.lib().ph_dispatch(src, len(src), spec.name.encode(), n, 1, 1, 256, 1, 0, ins, in_b, 1, outs, out_b, 1,
                               ctypes.byref(err))
     assert rc == 0
     np.testing.assert_array_equal(out, x + 1.0)
-    rc = rt.lib().ph_dispatch(src, len(src), spec.name.encode(), n, 1, 1, 256, 5, ins, in_b, 1, outs, out_b, 1,
+    rc = rt.lib().ph_dispatch(src, len(src), spec.name.encode(), n, 1, 1, 256, 1, 5, ins, in_b, 1, outs, out_b, 1,
                               ctypes.byref(err))
     assert rc == rt.PH_ERR_INVALID
     assert b"math_mode out of range" in ctypes.cast(err, ctypes.c_char_p).value
+    rt.lib().ph_free_error(err)
+
+
+def _lane_kernel_attrs(rng):
+    """A lane-parallel kernel ((128, 8) @ (8, 4) blocks, one row per lane)
+    and the FFI attributes hip_call_jit would bake into the HLO."""
+    from dot_cases import lane_rows
+
+    f, inputs = lane_rows(np.random.default_rng(4), math_mode="safe")
+    jit, _ = lane_rows(np.random.default_rng(4), factory=pa.hip_call_jit, math_mode="safe")
+    attrs = jit.ffi_attributes(inputs)
+    assert attrs["lanes"] == 128
+    return f, inputs, attrs
+
+
+def test_ph_dispatch_lane_parallel_kernel(rng):
+    f, (a, w), attrs = _lane_kernel_attrs(rng)
+    want = f.interpret(a, w)
+    out = np.empty_like(want)
+    src = attrs["hip_source"].encode()
+    ins = (ctypes.c_void_p * 2)(a.ctypes.data, w.ctypes.data)
+    in_b = (ctypes.c_size_t * 2)(a.nbytes, w.nbytes)
+    outs = (ctypes.c_void_p * 1)(out.ctypes.data)
+    out_b = (ctypes.c_size_t * 1)(out.nbytes)
+    err = ctypes.c_void_p()
+    rc = rt.lib().ph_dispatch(src, len(src), attrs["function_name"].encode(), attrs["grid_x"], attrs["grid_y"],
+                              attrs["grid_z"], attrs["block_x"], attrs["lanes"], attrs["math_mode"],
+                              ins, in_b, 2, outs, out_b, 1, ctypes.byref(err))
+    assert rc == 0, ctypes.cast(err, ctypes.c_char_p).value
+    np.testing.assert_array_equal(out, want)
+
+
+def test_ph_dispatch_device_buffers_on_a_stream(rng):
+    """The ROCM-platform handler body: device pointers, the caller's stream,
+    no staging and no wait."""
+    f, (a, w), attrs = _lane_kernel_attrs(rng)
+    want = f.interpret(a, w)
+    da, dw = rt.Buffer.from_numpy(a), rt.Buffer.from_numpy(w)
+    dout = rt.Buffer.empty(want.shape, want.dtype)
+    stream = rt.Stream()
+    src = attrs["hip_source"].encode()
+    ins = (ctypes.c_void_p * 2)(da.ptr, dw.ptr)
+    outs = (ctypes.c_void_p * 1)(dout.ptr)
+    err = ctypes.c_void_p()
+    rc = rt.lib().ph_dispatch_device(src, len(src), attrs["function_name"].encode(), attrs["grid_x"],
+                                     attrs["grid_y"], attrs["grid_z"], attrs["block_x"], attrs["lanes"],
+                                     attrs["math_mode"], ctypes.c_void_p(stream.handle), ins, 2, outs, 1,
+                                     ctypes.byref(err))
+    assert rc == 0, ctypes.cast(err, ctypes.c_char_p).value
+    np.testing.assert_array_equal(dout.to_numpy(stream), want)
+    rc = rt.lib().ph_dispatch_device(src, len(src), attrs["function_name"].encode(), 0, 1, 1, 256, 1, 0,
+                                     ctypes.c_void_p(stream.handle), ins, 2, outs, 1, ctypes.byref(err))
+    assert rc == rt.PH_ERR_INVALID
+    assert b"grid dims must be positive" in ctypes.cast(err, ctypes.c_char_p).value
     rt.lib().ph_free_error(err)
 
 
@@ -139,15 +194,41 @@ def test_safe_mode_propagates_nan_and_inf():
     assert np.isnan(out[2]) and np.isinf(out[0]) and out[1] < 0
 
 
+_TORCH_INTEROP = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import torch  # first: palladium_amd then binds to torch's HIP runtime
+import numpy as np
+import palladium_amd as pa
+from palladium_amd.frontend import pl
+assert torch.cuda.is_available()
+f = pa.hip_call(lambda x_ref, o_ref: o_ref.__setitem__(Ellipsis, x_ref[...] + 1.0),
+                grid=(2,), in_specs=[pl.BlockSpec((256,), lambda i: (i,))],
+                out_specs=pl.BlockSpec((256,), lambda i: (i,)),
+                out_shape=pl.ShapeDtypeStruct((512,), np.float32))
+x = torch.arange(512, dtype=torch.float32, device="cuda")
+o = torch.empty_like(x)
+bound = f.bound(np.zeros(512, np.float32))
+torch.cuda.synchronize()
+bound.launch_device(x, o)
+bound.stream.synchronize()
+assert torch.equal(o, x + 1.0)
+print("torch interop ok")
+"""
+
+
 def test_torch_device_tensors_zero_copy():
-    torch = pytest.importorskip("torch")
-    if not torch.cuda.is_available():
-        pytest.skip("torch has no GPU here")
-    f = _inc(512)
-    x = torch.arange(512, dtype=torch.float32, device="cuda")
-    o = torch.empty_like(x)
-    bound = f.bound(np.zeros(512, F))
-    torch.cuda.synchronize()
-    bound.launch_device(x, o)
-    bound.stream.synchronize()
-    assert torch.equal(o, x + 1.0)
+    """torch tensors in HBM passed straight to a kernel. One process holds
+    one HIP runtime only when torch is imported before palladium_amd (the
+    native library then binds to torch's libamdhip64), so this runs in a
+    fresh child process that does exactly that."""
+    import importlib.util
+    import subprocess
+    import sys
+
+    if importlib.util.find_spec("torch") is None:
+        pytest.skip("torch is not installed")
+    root = str(Path(__file__).resolve().parents[1])
+    r = subprocess.run([sys.executable, "-c", _TORCH_INTEROP, root], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "torch interop ok" in r.stdout
