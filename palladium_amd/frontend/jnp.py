@@ -469,7 +469,7 @@ def clamp(lo: Any, x: Tracer, hi: Any) -> Tracer:
 # reductions
 
 
-def _reduce(name: str, x: Tracer, axis: Any, out_dtype: np.dtype | None = None) -> Tracer:
+def _reduce(name: str, x: Tracer, axis: Any, out_dtype: np.dtype | None = None, keepdims: bool = False) -> Tracer:
     if not isinstance(x, Tracer):
         x = asarray(x)
     if axis is None:
@@ -480,36 +480,48 @@ def _reduce(name: str, x: Tracer, axis: Any, out_dtype: np.dtype | None = None) 
         axes = (axis % x.ndim,)
     else:
         axes = tuple(int(a) % x.ndim for a in axis)
+    axes = tuple(sorted(set(axes)))
     shape = tuple(s for d, s in enumerate(x.shape) if d not in axes)
-    return _stage(name, [x], shape, out_dtype or x.dtype, axes=axes, out_sharding=None)
+    r = _stage(name, [x], shape, out_dtype or x.dtype, axes=axes, out_sharding=None)
+    if keepdims:
+        # JAX stages keepdims as a broadcast_in_dim onto the size-1 axes.
+        kshape = tuple(1 if d in axes else s for d, s in enumerate(x.shape))
+        r = broadcast_in_dim(r, kshape, tuple(d for d in range(x.ndim) if d not in axes))
+    return r
 
 
-def sum(x: Tracer, axis: Any = None) -> Tracer:  # noqa: A001
-    return _reduce("reduce_sum", x, axis)
+def sum(x: Tracer, axis: Any = None, keepdims: bool = False) -> Tracer:  # noqa: A001
+    if isinstance(x, Tracer) and x.dtype == BOOL:
+        x = convert_element_type(x, I32)
+    return _reduce("reduce_sum", x, axis, keepdims=keepdims)
 
 
-def max(x: Tracer, axis: Any = None) -> Tracer:  # noqa: A001
-    return _reduce("reduce_max", x, axis)
+def max(x: Tracer, axis: Any = None, keepdims: bool = False) -> Tracer:  # noqa: A001
+    return _reduce("reduce_max", x, axis, keepdims=keepdims)
 
 
-def min(x: Tracer, axis: Any = None) -> Tracer:  # noqa: A001
-    return _reduce("reduce_min", x, axis)
+def min(x: Tracer, axis: Any = None, keepdims: bool = False) -> Tracer:  # noqa: A001
+    return _reduce("reduce_min", x, axis, keepdims=keepdims)
 
 
-def any(x: Tracer, axis: Any = None) -> Tracer:  # noqa: A001
+def any(x: Tracer, axis: Any = None, keepdims: bool = False) -> Tracer:  # noqa: A001
     if x.dtype != BOOL:
         x = not_equal(x, 0)
-    return _reduce("reduce_or", x, axis)
+    return _reduce("reduce_or", x, axis, keepdims=keepdims)
 
 
-def all(x: Tracer, axis: Any = None) -> Tracer:  # noqa: A001
+def all(x: Tracer, axis: Any = None, keepdims: bool = False) -> Tracer:  # noqa: A001
     if x.dtype != BOOL:
         x = not_equal(x, 0)
-    return _reduce("reduce_and", x, axis)
+    return _reduce("reduce_and", x, axis, keepdims=keepdims)
 
 
-def mean(x: Tracer, axis: Any = None) -> Tracer:
-    s = _reduce("reduce_sum", x, axis)
+def mean(x: Tracer, axis: Any = None, keepdims: bool = False) -> Tracer:
+    """Sum, then divide by the reduced element count (integers promote to
+    float32, as in JAX)."""
+    if x.dtype.kind != "f":
+        x = convert_element_type(x, F32)
+    s = _reduce("reduce_sum", x, axis, keepdims=keepdims)
     n = x.size // builtins.max(s.size, 1)
     return divide(s, float(n))
 
