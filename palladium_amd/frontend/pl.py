@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import dataclasses
 import math
+import threading
 from builtins import min as builtins_min
 from typing import Any, Callable, Sequence
 
@@ -123,6 +124,10 @@ class _GridState:
 
 
 _grid_state = _GridState()
+
+# While `palladium_amd.trace` runs a plain function, pallas_calls append
+# (call, args) here and return zero placeholders instead of running.
+_recording = threading.local()
 
 
 class Ref:
@@ -319,6 +324,11 @@ class PallasCall:
         return specs
 
     def __call__(self, *args: Any) -> Any:
+        calls = getattr(_recording, "calls", None)
+        if calls is not None:
+            calls.append((self, args))
+            outs = tuple(np.zeros(s.shape, s.dtype) for s in self.out_shapes)
+            return outs if self.multiple_results else outs[0]
         if self.interpret:
             from palladium_amd.interpret import interpret_call
 

@@ -145,6 +145,27 @@ def _trace_frontend(call: "_pl.PallasCall", example_args: tuple) -> KernelSpec:
     )
 
 
+def _trace_function(fn: Callable, example_args: tuple) -> KernelSpec:
+    """Run `fn` with every frontend pallas_call recorded instead of run
+    (placeholders flow on to later code); exactly one must be found
+    (reference: `src/palladium/trace.py:118-150`)."""
+    args = [np.zeros(*_shape_dtype(a)) for a in example_args]
+    _pl._recording.calls = []
+    try:
+        fn(*args)
+        calls = _pl._recording.calls
+    finally:
+        _pl._recording.calls = None
+    if len(calls) != 1:
+        raise TraceError(
+            f"found {len(calls)} pallas_call(s) in {getattr(fn, '__name__', 'the function')}; "
+            "palladium_amd compiles exactly one pallas_call per trace"
+            + ("" if calls else " (pass palladium_amd.frontend.pl.pallas_call(...))")
+        )
+    call, call_args = calls[0]
+    return _trace_frontend(call, call_args)
+
+
 def trace(pallas_fn: Callable, *example_args: Any) -> KernelSpec:
     """Extract a KernelSpec from a staged pallas_call.
 
@@ -167,10 +188,7 @@ def trace(pallas_fn: Callable, *example_args: Any) -> KernelSpec:
     try:
         import jax  # noqa: F401
     except ImportError:
-        raise TraceError(
-            "no pallas_call found: pass palladium_amd.frontend.pl.pallas_call(...) "
-            "(JAX is not importable here, so JAX pallas_calls cannot be traced)"
-        ) from None
+        return _trace_function(pallas_fn, example_args)
     from palladium_amd.jax_adapter import trace_jax
 
     return trace_jax(pallas_fn, *example_args)

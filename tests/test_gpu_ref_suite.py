@@ -26,3 +26,21 @@ def test_safe_bit_exact_vs_interpreter(name):
     kernel, out_shape, args, _ = CASES[name]()
     f = pa.hip_call(kernel, out_shape=out_shape, math_mode="safe")
     np.testing.assert_array_equal(f(*args), f.interpret(*args))
+
+
+def test_preferred_element_type_accumulates_in_float32_on_device():
+    """float16 operands, float32 accumulation: each product 1 + 2^-9 + 2^-20
+    is exact only in float32 (reference tests/test_16_diagnostics.py:214-233)."""
+    from palladium_amd.frontend import jnp, lax, pl
+
+    def kernel(a_ref, b_ref, o_ref):
+        o_ref[...] = lax.dot_general(a_ref[...], b_ref[...], (((1,), (0,)), ((), ())),
+                                     preferred_element_type=jnp.float32)
+
+    k = 16
+    a = np.full((7, k), 1 + 2**-10, dtype=np.float16)
+    b = np.full((k, 8), 1 + 2**-10, dtype=np.float16)
+    for mode in ("safe", "fast"):
+        got = pa.hip_call(kernel, out_shape=pl.ShapeDtypeStruct((7, 8), np.float32), math_mode=mode)(a, b)
+        assert got.dtype == np.float32
+        np.testing.assert_allclose(got, np.full((7, 8), k * (1 + 2**-9 + 2**-20)), rtol=0, atol=2**-17)

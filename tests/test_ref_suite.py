@@ -37,3 +37,71 @@ def test_keepdims_stages_broadcast_in_dim():
                  np.zeros((3, 4), np.float32))
     names = [e.primitive.name for e in spec.jaxpr.eqns]
     assert names[names.index("reduce_sum") + 1] == "broadcast_in_dim"
+
+
+def test_function_with_one_pallas_call_traces():
+    from palladium_amd.frontend import jnp
+
+    def kernel(x_ref, o_ref):
+        o_ref[...] = jnp.abs(x_ref[...])
+
+    def wrapper(x):
+        return pl.pallas_call(kernel, out_shape=pl.ShapeDtypeStruct((8,), np.float32))(x * 2)
+
+    spec = trace(wrapper, np.zeros(8, np.float32))
+    assert spec.name == "kernel" and spec.inputs[0].array_shape == (8,)
+
+
+@pytest.mark.parametrize("n", [0, 2])
+def test_zero_or_several_pallas_calls_rejected(n):
+    """reference tests/test_16_diagnostics.py:135-149"""
+    def kernel(x_ref, o_ref):
+        o_ref[...] = x_ref[...]
+
+    def calls(x):
+        for _ in range(n):
+            x = pl.pallas_call(kernel, out_shape=pl.ShapeDtypeStruct((8,), np.float32))(x)
+        return x
+
+    with pytest.raises(TraceError, match=f"found {n} pallas_call"):
+        trace(calls, np.zeros(8, np.float32))
+
+
+def test_scanned_xs_and_strided_refs_rejected():
+    """reference tests/test_16_diagnostics.py:115-132: both rejected with the
+    cause named (here at trace time)."""
+    from palladium_amd.frontend import lax
+
+    def scan_kernel(x_ref, o_ref):
+        def body(c, x):
+            return c + x, c
+
+        _c, ys = lax.scan(body, x_ref[0], x_ref[...])
+        o_ref[...] = ys
+
+    def strided(x_ref, o_ref):
+        o_ref[...] = x_ref[::2]
+
+    with pytest.raises(TraceError, match="scanned xs"):
+        pa.debug_hip(scan_kernel, np.zeros(8, np.float32), out_shape=pl.ShapeDtypeStruct((8,), np.float32))
+    with pytest.raises(TraceError, match="stride"):
+        pa.debug_hip(strided, np.zeros(8, np.float32), out_shape=pl.ShapeDtypeStruct((4,), np.float32))
+
+
+def test_preferred_element_type_accumulates_in_float32():
+    """reference tests/test_16_diagnostics.py:214-233: a_i = b_i = 1 + 2^-10
+    (exact in float16); each product 1 + 2^-9 + 2^-20 is exact in float32 but
+    not in float16, so a kernel that multiplies in half is off by 2^-16."""
+    from palladium_amd.frontend import jnp
+
+    def kernel(a_ref, b_ref, o_ref):
+        o_ref[...] = lax.dot_general(a_ref[...], b_ref[...], (((1,), (0,)), ((), ())),
+                                     preferred_element_type=jnp.float32)
+
+    k = 16
+    a = np.full((7, k), 1 + 2**-10, dtype=np.float16)
+    b = np.full((k, 8), 1 + 2**-10, dtype=np.float16)
+    call = pa.hip_call(kernel, out_shape=pl.ShapeDtypeStruct((7, 8), np.float32))
+    got = call.interpret(a, b)
+    assert got.dtype == np.float32
+    np.testing.assert_allclose(got, np.full((7, 8), k * (1 + 2**-9 + 2**-20)), rtol=0, atol=2**-17)
