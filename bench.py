@@ -282,8 +282,11 @@ def bench_df32(steps: int, warmup: int, cpu: bool) -> dict:
                 "trajectory-steps/s", steps, warmup, ms,
                 {"workload": "RK4 LV df32, config 4b (config-1 inputs, dt=0.005, 4000 steps)", "math_mode": "safe"})
     res["dtype"] = "df32"
-    res["roofline"] = {"bound": "valu", "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None,
-                       "avg_launch_ms": ms, "df_ops_per_traj_step": 58}
+    achieved = ts * df32.LV_DF32_FLOPS_PER_STEP / (ms / 1e3)
+    res["roofline"] = {"bound": "valu", "achieved": achieved / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
+                       "frac": achieved / FP32_PEAK, "traffic": None, "avg_launch_ms": ms,
+                       "flop_per_traj_step": df32.LV_DF32_FLOPS_PER_STEP,
+                       "flop_note": "float32 ops of 32 df_mul (12 each) + 22 df_add (20 each) per step, FMA = 2"}
     if cpu:
         import oracle
 
@@ -376,7 +379,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="lv")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-secondary", action="store_true", help="skip the Gray-Scott line in the default run")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the other kernels' lines (Gray-Scott, GBM, BS3, df32) in the default run")
     a = ap.parse_args()
     if a.gpus != 1:
         print(
@@ -392,10 +396,15 @@ def main() -> int:
     res = fns[a.workload](a.steps, a.warmup, cpu=not a.no_cpu and rank == 0)
     if a.workload == "lv" and not a.no_secondary:
         # The headline metric names two rooflines: RK4 LV against FP32 VALU
-        # (above) and the Gray-Scott stencil against HBM; report the second
-        # beside the first.
-        gs = bench_gs(a.steps, a.warmup, cpu=False)
-        res["secondary"] = {"gray_scott_4096": {k: gs[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline")}}
+        # (above) and the Gray-Scott stencil against HBM. The second, and the
+        # other hot kernels at their configurations, are reported beside the
+        # first (GPU only, no CPU baselines: a few seconds in all).
+        res["secondary"] = {}
+        for key, fn in (("gray_scott_4096", bench_gs), ("gbm_paths", bench_gbm), ("bs3_vdp", bench_bs3),
+                        ("lv_rk4_df32", bench_df32)):
+            r = fn(a.steps, a.warmup, cpu=False)
+            res["secondary"][key] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline")
+                                     if k in r}
     if rank == 0:
         print(json.dumps(res), flush=True)
     return 0

@@ -105,6 +105,18 @@ lv_rk4_df32(const float* __restrict__ x0, const float* __restrict__ y0,
 }
 """
 
+# float32 operations per df32 operation as written above (FMA = 2):
+# df_add = 2 TwoSum (6 each) + 2 adds + 2 Fast2Sum (3 each) = 20;
+# df_mul = 2 muls + 3 FMAs + 1 add + 1 Fast2Sum = 12.
+DF_ADD_FLOPS = 20
+DF_MUL_FLOPS = 12
+# One RK4 step of lv_rk4_df32: four rhs (5 muls, 2 adds: x*y is shared),
+# four stage/final updates (2 muls, 2 adds), the weighted sums (4 muls,
+# 6 adds): 32 df_mul + 22 df_add.
+LV_DF32_MULS_PER_STEP = 32
+LV_DF32_ADDS_PER_STEP = 22
+LV_DF32_FLOPS_PER_STEP = LV_DF32_MULS_PER_STEP * DF_MUL_FLOPS + LV_DF32_ADDS_PER_STEP * DF_ADD_FLOPS
+
 _kernel: rt.Kernel | None = None
 
 
