@@ -145,13 +145,13 @@ class KernelCache {
     if (he != hipSuccess) return hip_fail(err, he, "hipModuleLoadData");
     he = hipModuleGetFunction(&k->function, k->module, name);
     if (he != hipSuccess) {
-      hipModuleUnload(k->module);
+      (void)hipModuleUnload(k->module);  // best effort: the lookup error is reported
       return hip_fail(err, he, (std::string("hipModuleGetFunction(") + name + ")").c_str());
     }
     std::lock_guard<std::mutex> lock(mutex_);
     auto it = entries_.find(key);
     if (it != entries_.end()) {
-      hipModuleUnload(k->module);
+      (void)hipModuleUnload(k->module);  // lost the race: keep the cached module
       *out = it->second.get();
       return PH_OK;
     }
@@ -300,10 +300,12 @@ int ph_dispatch(const char *src, size_t src_len, const char *name,
   hipError_t e = hipStreamCreate(&stream);
   if (e != hipSuccess) return hip_fail(err, e, "hipStreamCreate");
   std::vector<void *> dev(n_inputs + n_outputs, nullptr);
+  // Staging buffers and stream are released on every path; a failure to
+  // release cannot be reported better than the error already being returned.
   auto cleanup = [&]() {
     for (void *p : dev)
-      if (p) hipFree(p);
-    hipStreamDestroy(stream);
+      if (p) (void)hipFree(p);
+    (void)hipStreamDestroy(stream);
   };
   for (size_t i = 0; i < n_inputs + n_outputs; ++i) {
     size_t bytes = i < n_inputs ? input_bytes[i] : output_bytes[i - n_inputs];
@@ -445,7 +447,7 @@ int ph_stream_end_capture(void *stream, void **graph_exec, char **err) {
   if (e != hipSuccess) return hip_fail(err, e, "hipStreamEndCapture");
   hipGraphExec_t exec;
   e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
-  hipGraphDestroy(graph);
+  (void)hipGraphDestroy(graph);  // the executable graph no longer needs it
   if (e != hipSuccess) return hip_fail(err, e, "hipGraphInstantiate");
   *graph_exec = exec;
   return PH_OK;
