@@ -178,15 +178,17 @@ class HipCallable:
 
 
 def debug_hip(kernel: Callable, *example_args: Any, **pallas_kwargs: Any) -> str:
-    """Trace `kernel` through pallas_call and return the emitted HIP source.
+    """Trace `kernel` through pallas_call and return the emitted HIP source,
+    exactly as `hip_call` with the same keywords would compile it (FAST
+    math, the default, applies its jaxpr rewrites before emission).
     Nothing is compiled or dispatched."""
     threadgroup = pallas_kwargs.pop("threadgroup", None)
-    pallas_kwargs.pop("math_mode", None)
+    math_mode = pallas_kwargs.pop("math_mode", MathMode.FAST)
     frontend = pallas_kwargs.pop("frontend", "auto")
     staged, _ = _stage(kernel, pallas_kwargs, frontend)
     from palladium_amd.dispatch import _block_of
 
-    return emit_hip(trace(staged, *example_args), block=_block_of(threadgroup))
+    return emit_hip(trace(staged, *example_args), block=_block_of(threadgroup), math_mode=math_mode)
 
 
 def hip_call(kernel: Callable, **pallas_kwargs: Any) -> HipCallable:

@@ -69,6 +69,8 @@ class PendingResult:
     event: rt.Event
     out_bufs: list[rt.Buffer]
     stream: Any
+    # Host arrays an asynchronous upload may still be reading.
+    host_inputs: tuple = dataclasses.field(default=(), repr=False)
 
     def done(self) -> bool:
         return self.event.query()
@@ -76,6 +78,7 @@ class PendingResult:
     def wait(self) -> np.ndarray | tuple[np.ndarray, ...]:
         """Block until the GPU is done, then return the outputs."""
         self.event.synchronize()
+        self.host_inputs = ()
         outs = tuple(b.to_numpy(self.stream) for b in self.out_bufs)
         return outs[0] if len(outs) == 1 else outs
 
@@ -155,7 +158,9 @@ class BoundKernel:
             for buf, a in zip(self._in_bufs, arrs):
                 buf.copy_from(a, stream)
             outs = self._new_outputs()
-            return self._dispatch(self._in_bufs, outs)
+            pending = self._dispatch(self._in_bufs, outs)
+            pending.host_inputs = tuple(arrs)
+            return pending
 
     def __call__(self, *arrays: np.ndarray) -> np.ndarray | tuple[np.ndarray, ...]:
         """Launch over the grid and return the outputs (NumPy)."""

@@ -148,3 +148,20 @@ def test_math_mode_values():
     assert pa.MathMode("safe").ordinal == 0 and pa.MathMode.FAST.ordinal == 2
     with pytest.raises(ValueError):
         _double(4, math_mode="turbo")
+
+
+def test_debug_hip_matches_what_hip_call_compiles():
+    """debug_hip applies the math mode's emission (FAST factoring) exactly
+    as hip_call does."""
+
+    def kernel(x_ref, y_ref, o_ref):
+        x, y = x_ref[...], y_ref[...]
+        o_ref[...] = 2.0 * x - (3.0 * x) * y
+
+    x = np.zeros(8, F)
+    out = pl.ShapeDtypeStruct((8,), F)
+    spec = pa.trace(pl.pallas_call(kernel, out_shape=out), x, x)
+    for mode in ("safe", "fast"):
+        assert pa.debug_hip(kernel, x, x, out_shape=out, math_mode=mode) == pa.emit_hip(spec, math_mode=mode)
+    assert pa.debug_hip(kernel, x, x, out_shape=out) == pa.emit_hip(spec, math_mode="fast")
+    assert pa.debug_hip(kernel, x, x, out_shape=out, math_mode="safe") != pa.debug_hip(kernel, x, x, out_shape=out)
