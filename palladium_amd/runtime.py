@@ -503,11 +503,19 @@ class Batch:
         self._stop = Event()
         if graph:
             _call("ph_stream_begin_capture", _stream_handle(self.stream))
+            g = ctypes.c_void_p()
             try:
                 self._enqueue()
-            finally:
-                g = ctypes.c_void_p()
-                _call("ph_stream_end_capture", _stream_handle(self.stream), ctypes.byref(g))
+            except BaseException:
+                # End the capture so the stream is usable again; the launch
+                # error is the one worth reporting.
+                err = ctypes.c_void_p()
+                if lib().ph_stream_end_capture(_stream_handle(self.stream), ctypes.byref(g), ctypes.byref(err)) == PH_OK:
+                    lib().ph_graph_destroy(g)
+                elif err.value:
+                    lib().ph_free_error(err)
+                raise
+            _call("ph_stream_end_capture", _stream_handle(self.stream), ctypes.byref(g))
             self._graph = g.value
             self._start.record(self.stream)
             _call("ph_graph_launch", ctypes.c_void_p(self._graph), _stream_handle(self.stream))
@@ -530,4 +538,10 @@ class Batch:
 
     def __del__(self) -> None:
         if getattr(self, "_graph", None) and _lib is not None:
+            # The graph may still be running: let it finish before destroying it.
+            err = ctypes.c_void_p()
+            if self._stop is not None:
+                _lib.ph_event_synchronize(ctypes.c_void_p(self._stop.handle), ctypes.byref(err))
+                if err.value:
+                    _lib.ph_free_error(err)
             _lib.ph_graph_destroy(ctypes.c_void_p(self._graph))
