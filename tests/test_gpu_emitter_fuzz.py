@@ -5,6 +5,8 @@ must agree bit for bit. Programs mix expression trees, fori_loops with
 permuted carries, switch and bounded while loops (after the reference's
 tests/test_fuzz_emitter.py grammar)."""
 
+import os
+
 import numpy as np
 import pytest
 
@@ -67,7 +69,7 @@ def _make_kernel(seed):
     return kernel
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
 def test_random_program_bit_exact_vs_interpreter(seed):
     n = 300
     rng = np.random.default_rng(100 + seed)

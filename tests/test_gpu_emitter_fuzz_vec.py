@@ -2,6 +2,8 @@
 per-instance and lane-parallel launches under SAFE math, bit for bit
 against the NumPy interpreter."""
 
+import os
+
 import numpy as np
 import pytest
 
@@ -11,7 +13,7 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("lanes", [False, True], ids=["instance", "lanes"])
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
 def test_vector_program_bit_exact_vs_interpreter(seed, lanes):
     print(f"fuzz_vec seed={seed} lanes={lanes}", flush=True)
     call = make_call(seed, lanes=lanes, math_mode="safe")

@@ -3,6 +3,7 @@
 import dataclasses
 
 import numpy as np
+import pytest
 
 from palladium_amd.emit import emit_hip
 from palladium_amd.emit.optimize import factor_common_products
@@ -114,3 +115,53 @@ def test_emitter_applies_rewrite_only_under_fast():
     fast = emit_hip(spec, math_mode="fast")
     assert safe == emit_hip(spec)
     assert fast.count(" * ") < safe.count(" * ")
+
+
+def _poly_kernel(seed):
+    """A random branch-free sum of signed products over three inputs and
+    literals: the shape the common-factor rewrite targets, at random."""
+    def kernel(x_ref, y_ref, z_ref, o_ref, s_ref):
+        r = np.random.default_rng(seed)
+        leaves = [x_ref[...], y_ref[...], z_ref[...]]
+
+        def product():
+            p = leaves[r.integers(3)]
+            for _ in range(r.integers(0, 3)):
+                p = p * (leaves[r.integers(3)] if r.random() < 0.7 else float(np.float32(r.uniform(0.5, 2))))
+            return p
+
+        acc = product()
+        for _ in range(r.integers(1, 6)):
+            acc = acc + product() if r.random() < 0.5 else acc - product()
+        o_ref[...] = acc
+        # Magnitude bound: the same terms, all added in absolute value.
+        r = np.random.default_rng(seed)
+        leaves = [jnp.abs(v) for v in leaves]
+        mag = product()
+        for _ in range(r.integers(1, 6)):
+            r.random()
+            mag = mag + product()
+        s_ref[...] = mag
+
+    return kernel
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_rewrite_fuzz_random_sums_of_products(seed):
+    rng = np.random.default_rng(seed)
+    args = [rng.uniform(-2, 2, 64).astype(np.float32) for _ in range(3)]
+    call = pl.pallas_call(_poly_kernel(seed), out_shape=(pl.ShapeDtypeStruct((64,), np.float32),) * 2)
+    spec = trace(call, *args)
+    want, mag = interpret_spec(spec, *args)
+    got, _ = interpret_spec(_rewritten(spec), *args)
+    # Reassociation moves each result by a few float32 ulps of the terms.
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-5 * (mag.astype(np.float64) + 1e-30))
+
+
+def test_rewrite_fuzz_is_not_vacuous():
+    fired = 0
+    for seed in range(40):
+        spec = trace(pl.pallas_call(_poly_kernel(seed), out_shape=(pl.ShapeDtypeStruct((64,), np.float32),) * 2),
+                     *[np.zeros(64, np.float32)] * 3)
+        fired += _count(_rewritten(spec).jaxpr, "mul") < _count(spec.jaxpr, "mul")
+    assert fired >= 10
