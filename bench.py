@@ -372,6 +372,30 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     return res
 
 
+def bench_bs3_lockstep(steps: int, warmup: int, cpu: bool) -> dict:
+    """The reference's formulation of config 2: every lane runs a fixed
+    trip of attempts (the ensemble's largest need), idling after T1. Timed
+    beside `bs3` to show what the while loop's early exit is worth."""
+    from palladium_amd import runtime as rt
+    from palladium_amd.workloads import BS3_CFG, bs3_inputs, bs3_vdp_lockstep_call
+
+    cfg = BS3_CFG
+    host = bs3_inputs(cfg.n)
+    max_steps = 2656  # config 2's largest per-trajectory attempt count (2641) + 15
+    bound = bs3_vdp_lockstep_call(cfg.n, max_steps).bound(*host)
+    ins = [rt.Buffer.from_numpy(a) for a in host]
+    outs = [rt.Buffer.empty((cfg.n,), np.float32) for _ in range(5)]
+    ms, avg = _timed_launches(bound, ins + outs, steps, warmup)
+    t = outs[0].to_numpy()
+    res = _base("BS3(2)+PI lockstep (fixed-trip) launches, N=262,144", 1e3 / ms, "launches/s", steps, warmup, ms,
+                {"workload": "adaptive BS3(2) Van der Pol, config 2, reference fixed-trip loop", "n": cfg.n,
+                 "max_steps": max_steps, "math_mode": "fast"})
+    res["all_reached_t1"] = bool(np.all(t == np.float32(cfg.t1)))
+    res["roofline"] = {"bound": "valu", "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None,
+                       "avg_launch_ms": avg}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -390,7 +414,8 @@ def main() -> int:
         )
         return 2
     rank = int(os.environ.get("RANK", "0"))
-    fns = {"lv": bench_lv, "gbm": bench_gbm, "gs": bench_gs, "bs3": bench_bs3, "copy": bench_copy, "df32": bench_df32}
+    fns = {"lv": bench_lv, "gbm": bench_gbm, "gs": bench_gs, "bs3": bench_bs3, "bs3_lockstep": bench_bs3_lockstep,
+           "copy": bench_copy, "df32": bench_df32}
     if a.workload not in fns:
         raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")
     res = fns[a.workload](a.steps, a.warmup, cpu=not a.no_cpu and rank == 0)

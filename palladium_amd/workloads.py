@@ -155,66 +155,81 @@ class BS3Config:
 BS3_CFG = BS3Config()
 
 
-def bs3_vdp_kernel(cfg: BS3Config):
-    """Kernel: refs (x0, v0, mu) -> (t, x, v, accepted, rejected).
-
-    The reference's BS3(2)+FSAL+PI step (`tests/test_08_adaptive.py:76-122`)
-    inside a `while_loop` that runs until t reaches T1 (bounded by
-    `max_attempts`), so each lane takes exactly the attempts it needs;
-    accepted/rejected are int32 counts of real attempts."""
+def _bs3_attempt(cfg: BS3Config, mu: Any, t: Any, dt: Any, x: Any, v: Any, k1x: Any, k1v: Any,
+                 prev_inv_err: Any) -> tuple:
+    """One BS3(2)+FSAL+PI attempt (`tests/test_08_adaptive.py:76-122`):
+    returns (accept, t, dt, x, v, k1x, k1v, prev_inv_err) after it. The
+    step clamps to T1 first, so a lane at T1 attempts a zero step, which
+    is accepted and changes nothing."""
     t1, rtol, atol = cfg.t1, cfg.rtol, cfg.atol
     error_order = 3
     coeff1 = (cfg.icoeff + cfg.pcoeff) / error_order
     coeff2 = -cfg.pcoeff / error_order
     safety, factormin, factormax = 0.9, 0.2, 10.0
 
+    def rhs(x, v):
+        return v, mu * (1.0 - x**2) * v - x
+
+    dt = jnp.minimum(dt, t1 - t)
+    k2x, k2v = rhs(x + 0.5 * dt * k1x, v + 0.5 * dt * k1v)
+    k3x, k3v = rhs(x + 0.75 * dt * k2x, v + 0.75 * dt * k2v)
+    y3 = (
+        x + dt * (2 / 9 * k1x + 1 / 3 * k2x + 4 / 9 * k3x),
+        v + dt * (2 / 9 * k1v + 1 / 3 * k2v + 4 / 9 * k3v),
+    )
+    k4x, k4v = rhs(*y3)
+    y2 = (
+        x + dt * (7 / 24 * k1x + 1 / 4 * k2x + 1 / 3 * k3x + 1 / 8 * k4x),
+        v + dt * (7 / 24 * k1v + 1 / 4 * k2v + 1 / 3 * k3v + 1 / 8 * k4v),
+    )
+    err_x, err_v = y3[0] - y2[0], y3[1] - y2[1]
+    x3, v3 = y3
+    err_norm = jnp.maximum(
+        jnp.abs(err_x) / (atol + rtol * jnp.abs(x3)),
+        jnp.abs(err_v) / (atol + rtol * jnp.abs(v3)),
+    )
+    accept = err_norm <= 1.0
+    t2 = jnp.where(accept, t + dt, t)
+    x2 = jnp.where(accept, y3[0], x)
+    v2 = jnp.where(accept, y3[1], v)
+    nk1x = jnp.where(accept, k4x, k1x)
+    nk1v = jnp.where(accept, k4v, k1v)
+    err_norm = jnp.maximum(err_norm, 1e-9)
+    inv_err = 1 / err_norm
+    factor = safety * inv_err**coeff1 * prev_inv_err**coeff2
+    prev_inv_err = jnp.where(accept, inv_err, prev_inv_err)
+    dt = dt * jnp.clip(factor, factormin, factormax)
+    return accept, t2, dt, x2, v2, nk1x, nk1v, prev_inv_err
+
+
+def _bs3_rhs(mu: Any, x: Any, v: Any) -> tuple:
+    return v, mu * (1.0 - x**2) * v - x
+
+
+def bs3_vdp_kernel(cfg: BS3Config):
+    """Kernel: refs (x0, v0, mu) -> (t, x, v, accepted, rejected).
+
+    The reference's adaptive step inside a `while_loop` that runs until t
+    reaches T1 (bounded by `max_attempts`), so each lane takes exactly the
+    attempts it needs; accepted/rejected are int32 counts of real
+    attempts."""
+
     def kernel(x0_ref, v0_ref, mu_ref, to_ref, xo_ref, vo_ref, acc_ref, rej_ref):
         mu = mu_ref[...]
 
-        def rhs(x, v):
-            return v, mu * (1.0 - x**2) * v - x
-
         def cond(c):
             t, it = c[0], c[9]
-            return jnp.logical_and(t < t1, it < cfg.max_attempts)
+            return jnp.logical_and(t < cfg.t1, it < cfg.max_attempts)
 
         def body(c):
             t, dt, x, v, k1x, k1v, prev_inv_err, acc, rej, it = c
-            dt = jnp.minimum(dt, t1 - t)
-            k2x, k2v = rhs(x + 0.5 * dt * k1x, v + 0.5 * dt * k1v)
-            k3x, k3v = rhs(x + 0.75 * dt * k2x, v + 0.75 * dt * k2v)
-            y3 = (
-                x + dt * (2 / 9 * k1x + 1 / 3 * k2x + 4 / 9 * k3x),
-                v + dt * (2 / 9 * k1v + 1 / 3 * k2v + 4 / 9 * k3v),
-            )
-            k4x, k4v = rhs(*y3)
-            y2 = (
-                x + dt * (7 / 24 * k1x + 1 / 4 * k2x + 1 / 3 * k3x + 1 / 8 * k4x),
-                v + dt * (7 / 24 * k1v + 1 / 4 * k2v + 1 / 3 * k3v + 1 / 8 * k4v),
-            )
-            err_x, err_v = y3[0] - y2[0], y3[1] - y2[1]
-            x3, v3 = y3
-            err_norm = jnp.maximum(
-                jnp.abs(err_x) / (atol + rtol * jnp.abs(x3)),
-                jnp.abs(err_v) / (atol + rtol * jnp.abs(v3)),
-            )
-            accept = err_norm <= 1.0
-            t2 = jnp.where(accept, t + dt, t)
-            x2 = jnp.where(accept, y3[0], x)
-            v2 = jnp.where(accept, y3[1], v)
-            nk1x = jnp.where(accept, k4x, k1x)
-            nk1v = jnp.where(accept, k4v, k1v)
-            err_norm = jnp.maximum(err_norm, 1e-9)
-            inv_err = 1 / err_norm
-            factor = safety * inv_err**coeff1 * prev_inv_err**coeff2
-            prev_inv_err = jnp.where(accept, inv_err, prev_inv_err)
-            dt = dt * jnp.clip(factor, factormin, factormax)
+            accept, t, dt, x, v, k1x, k1v, prev_inv_err = _bs3_attempt(cfg, mu, t, dt, x, v, k1x, k1v, prev_inv_err)
             acc = acc + jnp.where(accept, 1, 0)
             rej = rej + jnp.where(accept, 0, 1)
-            return (t2, dt, x2, v2, nk1x, nk1v, prev_inv_err, acc, rej, it + 1)
+            return (t, dt, x, v, k1x, k1v, prev_inv_err, acc, rej, it + 1)
 
         x0, v0 = x0_ref[...], v0_ref[...]
-        k1x, k1v = rhs(x0, v0)
+        k1x, k1v = _bs3_rhs(mu, x0, v0)
         zeros_i = jnp.zeros(x0.shape, jnp.int32)
         init = (
             jnp.zeros_like(x0), jnp.full_like(x0, cfg.dt0), x0, v0, k1x, k1v,
@@ -228,6 +243,38 @@ def bs3_vdp_kernel(cfg: BS3Config):
         rej_ref[...] = rej
 
     kernel.__name__ = "bs3_vdp"
+    return kernel
+
+
+def bs3_vdp_lockstep_kernel(cfg: BS3Config, max_steps: int):
+    """The reference's own formulation (`tests/test_08_adaptive.py:33-142`):
+    the same attempt in a fixed-trip `fori_loop` of `max_steps`; a lane
+    that reaches T1 keeps attempting zero steps, which change nothing.
+    Outputs (t, x, v, steps, rejected) as float32 counters; `steps` counts
+    accepted attempts including the idle ones after T1."""
+
+    def kernel(x0_ref, v0_ref, mu_ref, to_ref, xo_ref, vo_ref, steps_ref, rej_ref):
+        mu = mu_ref[...]
+
+        def step(_, c):
+            t, dt, x, v, k1x, k1v, prev_inv_err, steps, rej = c
+            accept, t, dt, x, v, k1x, k1v, prev_inv_err = _bs3_attempt(cfg, mu, t, dt, x, v, k1x, k1v, prev_inv_err)
+            steps = steps + jnp.where(accept, 1.0, 0.0)
+            rej = rej + jnp.where(accept, 0.0, 1.0)
+            return (t, dt, x, v, k1x, k1v, prev_inv_err, steps, rej)
+
+        x0, v0 = x0_ref[...], v0_ref[...]
+        k1x, k1v = _bs3_rhs(mu, x0, v0)
+        init = (jnp.zeros_like(x0), jnp.full_like(x0, cfg.dt0), x0, v0, k1x, k1v, jnp.ones_like(x0),
+                jnp.zeros_like(x0), jnp.zeros_like(x0))
+        t, _, x, v, _, _, _, steps, rej = lax.fori_loop(0, max_steps, step, init)
+        to_ref[...] = t
+        xo_ref[...] = x
+        vo_ref[...] = v
+        steps_ref[...] = steps
+        rej_ref[...] = rej
+
+    kernel.__name__ = "bs3_vdp_lockstep"
     return kernel
 
 
@@ -245,6 +292,21 @@ def bs3_vdp_call(n: int, cfg: BS3Config = BS3_CFG, **kw: Any):
             pl.ShapeDtypeStruct((n,), np.int32), pl.ShapeDtypeStruct((n,), np.int32),
         ),
         name="bs3_vdp",
+        **kw,
+    )
+
+
+def bs3_vdp_lockstep_call(n: int, max_steps: int, cfg: BS3Config = BS3_CFG, **kw: Any):
+    import palladium_amd as pa
+
+    spec = pl.BlockSpec((1,), lambda i: (i,))
+    return pa.hip_call(
+        bs3_vdp_lockstep_kernel(cfg, max_steps),
+        grid=(n,),
+        in_specs=[spec] * 3,
+        out_specs=tuple([spec] * 5),
+        out_shape=tuple(pl.ShapeDtypeStruct((n,), F32) for _ in range(5)),
+        name="bs3_vdp_lockstep",
         **kw,
     )
 

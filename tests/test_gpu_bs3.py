@@ -56,3 +56,22 @@ def test_attempt_cap_ends_every_lane():
     for g, w in zip(got, want):
         np.testing.assert_array_equal(g, w)
     assert np.all(got[3] + got[4] <= 50)
+
+
+def test_reference_lockstep_formulation_matches_while_loop():
+    """The reference's fixed-trip, self-stalling loop
+    (tests/test_08_adaptive.py:33-142) ends in the same state: after T1 a
+    lane only attempts zero steps. Its `steps` counter includes those idle
+    accepts, so it equals max_steps - rejected."""
+    from palladium_amd.workloads import bs3_vdp_lockstep_call
+
+    n = 2048
+    x0, v0, mu = bs3_inputs(n, seed=BS3_CFG.seed)
+    want = oracle.bs3_vdp(x0, v0, mu, BS3_CFG)
+    max_steps = int((want[3] + want[4]).max()) + 16
+    t, x, v, steps, rej = bs3_vdp_lockstep_call(n, max_steps, math_mode=pa.MathMode.SAFE)(x0, v0, mu)
+    np.testing.assert_array_equal(t, want[0])
+    np.testing.assert_array_equal(x, want[1])
+    np.testing.assert_array_equal(v, want[2])
+    np.testing.assert_array_equal(rej, want[4].astype(np.float32))
+    np.testing.assert_array_equal(steps, (max_steps - want[4]).astype(np.float32))
