@@ -133,7 +133,35 @@ def bench_lv(steps: int, warmup: int, cpu: bool) -> dict:
             "kind": "port",
             "sample": f"first {n_cpu} of {n} trajectories of config 1, all {cfg.steps} steps, C oracle (gcc -O2, OpenMP, same op order), {dt_cpu:.2f} s",
         }
+        result["cpu_baselines_more"] = _lv_cpu_more(host, cfg)
     return result
+
+
+def _lv_cpu_more(host, cfg) -> dict:
+    """The same C oracle on one core, and the float64 NumPy restatement
+    vectorised over trajectories (the interpret-like Python baseline), each
+    on a bounded sample of config 1."""
+    import oracle
+    from oracle.ref64 import lv_rk4_f64
+
+    out = {}
+    n1 = 20_000
+    oracle.set_threads(1)
+    try:
+        t0 = time.perf_counter()
+        oracle.lv_rk4(*(a[:n1] for a in host), cfg.dt, cfg.steps, track_max=True)
+        dt1 = time.perf_counter() - t0
+    finally:
+        oracle.set_threads(_cpu_cores())
+    out["oracle_1_core"] = {"value": n1 * cfg.steps / dt1, "unit": "trajectory-steps/s", "cores": 1, "kind": "port",
+                            "sample": f"first {n1} trajectories, all {cfg.steps} steps, {dt1:.2f} s"}
+    n2, s2 = 100_000, 400
+    t0 = time.perf_counter()
+    lv_rk4_f64(*(a[:n2] for a in host), cfg.dt, s2)
+    dt2 = time.perf_counter() - t0
+    out["numpy_f64_vectorized"] = {"value": n2 * s2 / dt2, "unit": "trajectory-steps/s", "cores": 1, "kind": "port",
+                                   "sample": f"first {n2} trajectories, {s2} of {cfg.steps} steps, float64 NumPy, {dt2:.2f} s"}
+    return out
 
 
 def _timed_launches(bound, ops, steps: int, warmup: int):

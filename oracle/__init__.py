@@ -40,8 +40,20 @@ def lib() -> ctypes.CDLL:
         L.oracle_fold_in.argtypes = [ctypes.c_uint32] * 3 + [_U, _U]
         L.oracle_bits_to_uniform.argtypes = [ctypes.c_uint32, ctypes.c_float, ctypes.c_float]
         L.oracle_bits_to_uniform.restype = ctypes.c_float
+        L.oracle_set_threads.argtypes = [ctypes.c_int]
+        L.oracle_set_threads.restype = None
+        L.oracle_max_threads.restype = ctypes.c_int
         _lib = L
     return _lib
+
+
+def set_threads(n: int) -> None:
+    """OpenMP threads for the oracle's parallel loops."""
+    lib().oracle_set_threads(int(n))
+
+
+def max_threads() -> int:
+    return int(lib().oracle_max_threads())
 
 
 def _fp(a: np.ndarray):

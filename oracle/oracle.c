@@ -5,12 +5,19 @@
  *
  * Each function restates, in plain C with IEEE single precision and no
  * contraction (built with -ffp-contract=off), the algorithm the reference
- * runs for that kernel, citing the reference file:line it follows. The
- * parity pinning of each function is listed in oracle/README.md.
+ * runs for that kernel, citing the reference file:line it follows. What
+ * pins each function (known answers, float64 restatements, invariants) is
+ * tested in tests/test_oracle.py, tests/test_oracle_sensitivity.py and
+ * tests/test_golden.py.
  */
 #include <math.h>
+#include <omp.h>
 #include <stdint.h>
 #include <string.h>
+
+/* Threads the OpenMP loops below use (the CPU baselines time 1 and all). */
+void oracle_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int oracle_max_threads(void) { return omp_get_max_threads(); }
 
 /* ------------------------------------------------------------------------
  * RK4 Lotka-Volterra, op for op as the reference's staged kernel body:
