@@ -517,6 +517,13 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
     for axis in range(len(grid)):
         pid_vals.append(CVal(f"_pid{axis}", (), "int"))
     env.pids = pid_vals  # type: ignore[attr-defined]
+    if plan is not None and plan.rows is not None:
+        # Ragged tail: lanes past the last valid row read the last row
+        # (in bounds; rows are independent) and store nothing.
+        cursor.emit(f"const bool _live = _pid0 * {lanes} + _lane < {plan.rows};")
+        cursor.emit(f"const int _lane_ld = _live ? _lane : {plan.rows - 1} - _pid0 * {lanes};")
+        env.lane_expr = "_lane_ld"  # type: ignore[attr-defined]
+        env.live = "_live"  # type: ignore[attr-defined]
 
     ref_vals: list[CVal] = []
     for k, info in enumerate(operands):

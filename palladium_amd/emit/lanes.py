@@ -65,9 +65,14 @@ class _Bail(Exception):
 
 @dataclasses.dataclass(frozen=True)
 class LanePlan:
+    """`rows`: when the lane operands' last block runs past their arrays
+    (a ragged tail, e.g. N = 100,000 in blocks of 256), the number of valid
+    rows; lanes past it load a clamped row and skip their stores."""
+
     lanes: int
     jaxpr: Jaxpr
     lane_operands: tuple[int, ...]
+    rows: int | None = None
 
 
 def _depends_on_grid(info) -> bool:
@@ -228,11 +233,11 @@ class _Pass:
                     tmpl.append(_Leaf(len(leaves) - 1))
             new_tree = IndexerTree(NDIndexer(tuple(tmpl), tuple(env[ref].aval.shape)), len(leaves))
             if name == "get":
-                out(L, params={"tree": new_tree}, invars=[env[ref], *leaves])
+                out(L, params={"tree": new_tree, "lane_row": True}, invars=[env[ref], *leaves])
             else:
                 val = e.invars[1]
                 vnew = a(val)
-                out(L, params={"tree": new_tree}, invars=[env[ref], vnew, *leaves])
+                out(L, params={"tree": new_tree, "lane_row": True}, invars=[env[ref], vnew, *leaves])
             return
         if name == "iota":
             dim = int(e.params["dimension"])
@@ -413,7 +418,51 @@ def lane_transform(spec: KernelSpec) -> LanePlan | None:
         nj, _ = p.jaxpr(spec.jaxpr, [U] * len(spec.jaxpr.invars), ref_lane)
     except _Bail:
         return None
-    return LanePlan(b, nj, lane_ops)
+    rows = _ragged_rows(spec, b, lane_ops, nj)
+    if rows is False:
+        return None
+    return LanePlan(b, nj, lane_ops, rows)
+
+
+def _uses(j: Jaxpr, names: set[str]) -> bool:
+    for e in j.eqns:
+        if e.primitive.name in names:
+            return True
+        for v in e.params.values():
+            for sub in (v if isinstance(v, tuple) else (v,)):
+                inner = getattr(sub, "jaxpr", sub)
+                if isinstance(inner, Jaxpr) and _uses(inner, names):
+                    return True
+    return False
+
+
+def _ragged_rows(spec: KernelSpec, b: int, lane_ops: tuple[int, ...], nj: Jaxpr) -> int | None | bool:
+    """None when every lane block lies inside its array; the valid row
+    count R when the last block of a 1-D grid runs past it (all lane
+    operands of R rows, block i at rows [i*b, i*b + b), no cross-lane
+    reduction, so rows are independent); False when blocks run past the
+    arrays in any other way (not lowered)."""
+    from palladium_amd.interpret import _grid_pids, eval_index_map
+
+    operands = list(spec.inputs) + list(spec.outputs)
+    if not lane_ops or not any(b * spec.num_programs > operands[k].array_shape[0] for k in lane_ops):
+        return None
+    if len(spec.grid) != 1:
+        return False
+    rows = {operands[k].array_shape[0] for k in lane_ops}
+    if len(rows) != 1:
+        return False
+    (r,) = rows
+    g = spec.grid[0]
+    if not (g - 1) * b < r <= g * b:
+        return False
+    pids = _grid_pids(tuple(spec.grid))
+    for k in lane_ops:
+        if not (eval_index_map(operands[k], pids, spec.num_programs)[0] == pids[0]).all():
+            return False
+    if _uses(nj, {"lane_reduce"}):
+        return False
+    return r
 
 
 def lanes_of(spec: KernelSpec) -> int:

@@ -268,9 +268,13 @@ def _rule_swap(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
         old = declare(env, cursor, out, init=dst.at("0")) if size == 1 else declare(env, cursor, out)
         if size != 1:
             cursor.copy(old, dst, size)
-    guard = eqn.params.get("lane0_only") and getattr(env, "lanes", 1) > 1
+    guard = None
+    if eqn.params.get("lane0_only") and getattr(env, "lanes", 1) > 1:
+        guard = "_lane == 0"
+    elif eqn.params.get("lane_row") and getattr(env, "live", None):
+        guard = env.live  # type: ignore[attr-defined]
     if guard:
-        cursor.emit("if (_lane == 0) {")
+        cursor.emit(f"if ({guard}) {{")
         cursor.indent += 1
     if value.size == 1 and size > 1:
         with cursor.loop(size) as i:
@@ -835,7 +839,7 @@ def _rule_iota(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
 @rule("lane_index")
 def _rule_lane_index(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     """This lane's row within its instance's block (lane-parallel mode)."""
-    env.bind(eqn.outvars[0], CVal("_lane", (), "int"))
+    env.bind(eqn.outvars[0], CVal(getattr(env, "lane_expr", "_lane"), (), "int"))
 
 
 _WAVE = 64

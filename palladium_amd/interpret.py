@@ -18,6 +18,7 @@ NaN-suppressing `fmin`/`fmax`, matching the emitted code.
 
 from __future__ import annotations
 
+import dataclasses
 import math
 from typing import Any
 
@@ -472,17 +473,29 @@ def block_offsets(spec: KernelSpec, info: BlockInfo, pids: list[np.ndarray] | No
     return off
 
 
+def _ragged_lane_operands(spec: KernelSpec) -> tuple[int, ...]:
+    """Operands whose ragged last block the lane-parallel lowering handles
+    (lanes past the array load a clamped row and store nothing)."""
+    from palladium_amd.emit.lanes import lane_transform
+
+    plan = lane_transform(spec)
+    return plan.lane_operands if plan is not None and plan.rows is not None else ()
+
+
 def check_block_bounds(spec: KernelSpec) -> None:
     """Raise EmitError if any instance's block extends past its array
     (ragged blocks are not lowered: they would read and write out of
     bounds on the device)."""
     pids = _grid_pids(tuple(spec.grid))
+    ragged_ok = _ragged_lane_operands(spec)
     for k, info in enumerate(list(spec.inputs) + list(spec.outputs)):
         imj = info.index_map_jaxpr.jaxpr
         full = info.full_block()
         outs = eval_index_map(info, pids, spec.num_programs)
         for d, (bi, b, a) in enumerate(zip(outs, full, info.array_shape)):
             lo, hi = int(bi.min()), int(bi.max())
+            if d == 0 and k in ragged_ok:
+                continue  # a ragged tail the lane-parallel lowering masks
             if lo < 0 or (hi + 1) * b > a:
                 raise EmitError(
                     f"operand {k}: the index map places a block of {b} along dim {d} at block index "
@@ -498,11 +511,21 @@ def interpret_spec(spec: KernelSpec, *arrays: np.ndarray) -> tuple[np.ndarray, .
     refs = []
     outs = []
     operands = list(spec.inputs) + list(spec.outputs)
+    ragged = _ragged_lane_operands(spec)
     for k, info in enumerate(operands):
+        shape = tuple(info.array_shape)
+        if k in ragged:
+            # Rows are independent in a ragged lane kernel: pad the tail
+            # block with copies of the last row, drop its outputs after.
+            shape = (spec.grid[0] * info.block_shape[0],) + shape[1:]
+            info = dataclasses.replace(info, array_shape=shape)
         if k < len(spec.inputs):
-            flat = np.ascontiguousarray(arrays[k], dtype=info.dtype).reshape(-1).copy()
+            arr = np.ascontiguousarray(arrays[k], dtype=info.dtype)
+            if arr.shape != shape:
+                arr = np.pad(arr, [(0, shape[0] - arr.shape[0])] + [(0, 0)] * (arr.ndim - 1), mode="edge")
+            flat = arr.reshape(-1).copy()
         else:
-            flat = np.zeros(math.prod(info.array_shape), info.dtype)
+            flat = np.zeros(math.prod(shape), info.dtype)
             outs.append(flat)
         check_contiguous(info, f"operand {k}")
         bshape = tuple(info.block_shape) or (1,)
@@ -510,7 +533,7 @@ def interpret_spec(spec: KernelSpec, *arrays: np.ndarray) -> tuple[np.ndarray, .
         refs.append(_Ref(flat, block_offsets(spec, info, pids), bshape, strides, k < len(spec.inputs)))
     env = _Env(n, pids, tuple(spec.grid))
     _eval(spec.jaxpr, env, refs, np.ones(n, bool))
-    return tuple(o.reshape(info.array_shape) for o, info in zip(outs, spec.outputs))
+    return tuple(o[: math.prod(info.array_shape)].reshape(info.array_shape) for o, info in zip(outs, spec.outputs))
 
 
 def interpret_call(call: Any, *args: Any) -> Any:

@@ -83,16 +83,16 @@ def lv_rk4_kernel(dt: float, steps: int, track_max: bool = False):
 
 def lv_rk4_call(n: int, dt: float, steps: int, track_max: bool = False, block: int = 1, **kw: Any):
     """`hip_call` of the LV ensemble over `n` trajectories; `block`
-    trajectories per program instance (1 = one lane each)."""
+    trajectories per program instance (1 = one lane each). The grid is
+    ceil(n / block), as config 0 states it (N = 100,000 in blocks of 256):
+    a ragged last block is lowered lane-parallel with its tail masked."""
     import palladium_amd as pa
 
-    if n % block:
-        raise ValueError(f"n={n} is not a multiple of block={block}")
     spec = pl.BlockSpec((block,), lambda i: (i,))
     n_out = 3 if track_max else 2
     return pa.hip_call(
         lv_rk4_kernel(dt, steps, track_max),
-        grid=(n // block,),
+        grid=(-(-n // block),),
         in_specs=[spec] * 6,
         out_specs=tuple([spec] * n_out),
         out_shape=tuple(pl.ShapeDtypeStruct((n,), F32) for _ in range(n_out)),

@@ -9,6 +9,7 @@ from palladium_amd import runtime as rt
 from palladium_amd.emit import emit_hip, rule
 from palladium_amd.errors import EmitError, UnsupportedPrimitiveError
 from palladium_amd.frontend import jnp, lax, pl, random
+from palladium_amd.interpret import interpret_call
 from palladium_amd.trace import trace
 
 
@@ -153,11 +154,38 @@ def test_block_size_validation():
     assert "__launch_bounds__(512)" in emit_hip(spec, block=512)
 
 
-def test_ragged_blocks_rejected_before_launch():
+def test_ragged_tail_of_independent_rows_is_lowered_masked():
+    """Config 0's layout: N = 100,000 in blocks of 256, grid ceil(N/256)."""
+    from palladium_amd.emit.lanes import lane_transform
     from palladium_amd.interpret import check_block_bounds
 
-    spec_ok = pl.BlockSpec((256,), lambda i: (i,))
-    call = pl.pallas_call(lambda x, o: None, grid=(391,), in_specs=[spec_ok], out_specs=spec_ok,
+    blk = pl.BlockSpec((256,), lambda i: (i,))
+
+    def kernel(x_ref, o_ref):
+        o_ref[...] = x_ref[...] * 2.0
+
+    call = pl.pallas_call(kernel, grid=(391,), in_specs=[blk], out_specs=blk,
+                          out_shape=pl.ShapeDtypeStruct((100_000,), F))
+    spec = trace(call, np.zeros(100_000, F))
+    check_block_bounds(spec)
+    assert lane_transform(spec).rows == 100_000
+    src = emit_hip(spec)
+    assert "const bool _live = _pid0 * 256 + _lane < 100000;" in src
+    assert "if (_live) {" in src
+    x = np.arange(100_000, dtype=F)
+    np.testing.assert_array_equal(interpret_call(call, x), x * 2)
+
+
+def test_ragged_blocks_rejected_when_rows_interact():
+    """A reduction across the block would see the tail: not lowered."""
+    from palladium_amd.interpret import check_block_bounds
+
+    blk = pl.BlockSpec((256,), lambda i: (i,))
+
+    def kernel(x_ref, o_ref):
+        o_ref[...] = x_ref[...] - jnp.max(x_ref[...])
+
+    call = pl.pallas_call(kernel, grid=(391,), in_specs=[blk], out_specs=blk,
                           out_shape=pl.ShapeDtypeStruct((100_000,), F))
     spec = trace(call, np.zeros(100_000, F))
     with pytest.raises(EmitError, match="past the array extent"):

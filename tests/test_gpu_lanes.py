@@ -23,6 +23,24 @@ def test_lv_cfg0_layout_blocks_of_256_bit_exact():
         np.testing.assert_array_equal(g, w)
 
 
+def test_lv_cfg0_exact_ragged_layout_bit_exact():
+    """Config 0 exactly: N = 100,000 (not a multiple of 256), grid
+    ceil(N/256) = 391 blocks of 256; the last block's 96 tail lanes are
+    masked."""
+    from palladium_amd.workloads import LV_CFG0
+
+    n = LV_CFG0.n
+    args = lv_inputs(n, LV_CFG0.seed)
+    call = lv_rk4_call(n, LV_CFG0.dt, LV_CFG0.steps, track_max=True, block=256, math_mode="safe")
+    assert call.bound(*args).geometry.blocks == 391
+    got = call(*args)
+    want = oracle.lv_rk4(*args, LV_CFG0.dt, LV_CFG0.steps, track_max=True)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
+    fast = lv_rk4_call(n, LV_CFG0.dt, LV_CFG0.steps, block=256)(*args)
+    np.testing.assert_allclose(fast[0], want[0], rtol=1e-4)
+
+
 def test_gbm_block_sums_match_oracle_paths():
     cfg = GBMConfig(n_steps=32)
     n = 256 * 64
