@@ -362,6 +362,88 @@ def bench_gs(steps: int, warmup: int, cpu: bool) -> dict:
     return res
 
 
+# A hand-written LDS halo-tiled Gray-Scott step: 128 x 8 cells per 256-lane
+# workgroup (4 rows per lane), the tile plus a one-cell halo staged through
+# LDS. Same operation order as the emitted kernel, so results are identical;
+# it exists to measure the tiling alternative against the emitted per-cell
+# kernel (which reads neighbours straight from L1/L2).
+_GS_LDS_TX, _GS_LDS_TY, _GS_LDS_RY = 128, 8, 4
+
+
+def _gs_lds_source(size: int, cfg) -> str:
+    tx_, ty_, ry = _GS_LDS_TX, _GS_LDS_TY, _GS_LDS_RY
+    f32 = lambda v: repr(float(np.float32(v))) + "f"  # noqa: E731
+    return f"""
+extern "C" __global__ void __launch_bounds__({tx_ * (ty_ // ry)})
+gs_lds(const float* __restrict__ u, const float* __restrict__ v, float* __restrict__ uo, float* __restrict__ vo)
+{{
+    __shared__ float su[{ty_ + 2}][{tx_ + 2}];
+    __shared__ float sv[{ty_ + 2}][{tx_ + 2}];
+    const int tx = threadIdx.x % {tx_}, ty = threadIdx.x / {tx_};
+    const int x0 = (blockIdx.x % {size // tx_}) * {tx_}, y0 = (blockIdx.x / {size // tx_}) * {ty_};
+    for (int r = ty; r < {ty_ + 2}; r += {ty_ // ry}) {{
+        int gy = y0 + r - 1;
+        gy = gy < 0 ? {size - 1} : (gy >= {size} ? 0 : gy);
+        su[r][tx + 1] = u[gy * {size} + x0 + tx];
+        sv[r][tx + 1] = v[gy * {size} + x0 + tx];
+        if (tx < 2) {{
+            const int gx = tx == 0 ? (x0 == 0 ? {size - 1} : x0 - 1) : (x0 + {tx_} == {size} ? 0 : x0 + {tx_});
+            const int cx = tx == 0 ? 0 : {tx_ + 1};
+            su[r][cx] = u[gy * {size} + gx];
+            sv[r][cx] = v[gy * {size} + gx];
+        }}
+    }}
+    __syncthreads();
+    #pragma unroll
+    for (int k = 0; k < {ry}; ++k) {{
+        const int r = ty * {ry} + k + 1, c = tx + 1;
+        const float uc = su[r][c], vc = sv[r][c];
+        const float lu = ((su[r + 1][c] + su[r - 1][c]) + su[r][c + 1]) + su[r][c - 1] - 4.0f * uc;
+        const float lv = ((sv[r + 1][c] + sv[r - 1][c]) + sv[r][c + 1]) + sv[r][c - 1] - 4.0f * vc;
+        const float uvv = uc * vc * vc;
+        const int gi = (y0 + r - 1) * {size} + x0 + tx;
+        uo[gi] = uc + {f32(cfg.dt)} * (({f32(cfg.du)} * lu - uvv) + {f32(cfg.f)} * (1.0f - uc));
+        vo[gi] = vc + {f32(cfg.dt)} * (({f32(cfg.dv)} * lv + uvv) - {f32(cfg.f + cfg.k)} * vc);
+    }}
+}}
+"""
+
+
+def bench_gs_lds(steps: int, warmup: int, cpu: bool) -> dict:
+    """The LDS halo-tiled alternative to the emitted Gray-Scott step, timed
+    the same way (all steps as one HIP graph) and checked against it."""
+    from palladium_amd import runtime as rt
+    from palladium_amd.workloads import GS_BYTES_PER_CELL_STEP, GS_CFG, gray_scott_call, gray_scott_initial, gray_scott_run
+
+    cfg = GS_CFG
+    size = cfg.size
+    u0, v0 = gray_scott_initial(size)
+    n_steps = int(os.environ.get("PALLADIUM_GS_STEPS", 200))
+    k = rt.Kernel(_gs_lds_source(size, cfg), "gs_lds", "fast")
+    blocks = (size // _GS_LDS_TX) * (size // _GS_LDS_TY)
+    block = _GS_LDS_TX * (_GS_LDS_TY // _GS_LDS_RY)
+    bufs = [rt.Buffer.from_numpy(u0), rt.Buffer.from_numpy(v0), rt.Buffer.empty((size, size), np.float32),
+            rt.Buffer.empty((size, size), np.float32)]
+    stream = rt.Stream()
+    a, b = (bufs[0], bufs[1]), (bufs[2], bufs[3])
+    batch = rt.Batch(stream)
+    for _ in range(n_steps):
+        batch.add(k, blocks, block, [a[0].ptr, a[1].ptr, b[0].ptr, b[1].ptr])
+        a, b = b, a
+    batch.commit(graph=True)
+    ms = batch.gpu_time * 1e3 / n_steps
+    emitted_u, _, _ = gray_scott_run(gray_scott_call(cfg), u0, v0, n_steps)
+    cells = size * size
+    res = _base("Gray-Scott LDS-tiled alternative, cell-steps/s (4096^2)", cells / (ms / 1e3), "cell-steps/s",
+                n_steps, 0, ms, {"workload": f"Gray-Scott 4096x4096, {n_steps} steps as one HIP graph, "
+                                 f"hand-written LDS tiles {_GS_LDS_TX}x{_GS_LDS_TY}", "math_mode": "fast"})
+    achieved = GS_BYTES_PER_CELL_STEP * cells / (ms / 1e3)
+    res["roofline"] = {"bound": "hbm", "achieved": achieved / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                       "frac": achieved / HBM_PEAK, "traffic": None, "avg_launch_ms": ms}
+    res["identical_to_emitted"] = bool(np.array_equal(a[0].to_numpy(), emitted_u))
+    return res
+
+
 def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     from palladium_amd import runtime as rt
     from palladium_amd.workloads import BS3_CFG, bs3_inputs, bs3_vdp_call
@@ -442,8 +524,8 @@ def main() -> int:
         )
         return 2
     rank = int(os.environ.get("RANK", "0"))
-    fns = {"lv": bench_lv, "gbm": bench_gbm, "gs": bench_gs, "bs3": bench_bs3, "bs3_lockstep": bench_bs3_lockstep,
-           "copy": bench_copy, "df32": bench_df32}
+    fns = {"lv": bench_lv, "gbm": bench_gbm, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
+           "bs3_lockstep": bench_bs3_lockstep, "copy": bench_copy, "df32": bench_df32}
     if a.workload not in fns:
         raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")
     res = fns[a.workload](a.steps, a.warmup, cpu=not a.no_cpu and rank == 0)
