@@ -38,21 +38,30 @@ def _cpu_cores() -> int:
     return min(os.cpu_count() or 1, 16)
 
 
-def bench_lv(steps: int, warmup: int, cpu: bool) -> dict:
+def bench_lv0(steps: int, warmup: int, cpu: bool) -> dict:
+    """Config 0 on the GPU: N=100,000, dt=0.01, 1,000 steps, grid
+    ceil(N/256) of 256-trajectory blocks (lane-parallel, masked tail)."""
+    from palladium_amd.workloads import LV_CFG0
+
+    return bench_lv(steps, warmup, cpu, cfg=LV_CFG0, block=256, track_max=False, label="config 0")
+
+
+def bench_lv(steps: int, warmup: int, cpu: bool, cfg=None, block: int = 1, track_max: bool = True,
+             label: str = "config 1") -> dict:
     import palladium_amd as pa
     from palladium_amd import runtime as rt
     from palladium_amd.workloads import LV_CFG1, LV_FLOP_PER_STEP, lv_inputs, lv_rk4_call
 
-    cfg = LV_CFG1
+    cfg = cfg or LV_CFG1
     n = cfg.n
     host = lv_inputs(n, cfg.seed)
-    call = lv_rk4_call(n, cfg.dt, cfg.steps, track_max=True, math_mode=pa.MathMode.FAST)
+    call = lv_rk4_call(n, cfg.dt, cfg.steps, track_max=track_max, block=block, math_mode=pa.MathMode.FAST)
     bound = call.bound(*host)
     ins = [rt.Buffer.from_numpy(a) for a in host]
-    outs = [rt.Buffer.empty((n,), np.float32) for _ in range(3)]
+    outs = [rt.Buffer.empty((n,), np.float32) for _ in range(3 if track_max else 2)]
     stream = bound.stream
     ops = [*ins, *outs]
-    print(f"[bench] lv_rk4 n={n} steps/traj={cfg.steps} blocks={bound.geometry.blocks}x{bound.geometry.block}", flush=True)
+    print(f"[bench] lv_rk4 n={n} steps/traj={cfg.steps} blocks={bound.geometry.blocks}x{bound.geometry.block}", file=sys.stderr, flush=True)
     for _ in range(warmup):
         bound.launch_device(*ops, stream=stream)
     stream.synchronize()
@@ -80,7 +89,8 @@ def bench_lv(steps: int, warmup: int, cpu: bool) -> dict:
         raise RuntimeError("non-finite results in the benchmark output")
 
     result = {
-        "metric": "trajectory-steps/sec (RK4 LV N=1e6 fp32) + % of FP32 VALU / HBM roofline",
+        "metric": ("trajectory-steps/sec (RK4 LV N=1e6 fp32) + % of FP32 VALU / HBM roofline" if cfg is LV_CFG1 else
+                   f"trajectory-steps/sec (RK4 LV N={n} fp32, {label})"),
         "value": value,
         "unit": "trajectory-steps/s",
         "n_gpus": 1,
@@ -91,9 +101,11 @@ def bench_lv(steps: int, warmup: int, cpu: bool) -> dict:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded numpy default_rng, seed 1)",
+        "data": f"synthetic (seeded numpy default_rng, seed {cfg.seed})",
         "config": {
-            "workload": "RK4 Lotka-Volterra ensemble, N=1,000,000, dt=0.005, 4,000 steps, max|y| carried (config 1)",
+            "workload": (f"RK4 Lotka-Volterra ensemble, N={n:,}, dt={cfg.dt}, {cfg.steps:,} steps"
+                         + (", max|y| carried" if track_max else "") + f" ({label})"
+                         + (f", blocks of {block} trajectories" if block > 1 else "")),
             "n": n,
             "dt": cfg.dt,
             "rk4_steps": cfg.steps,
@@ -109,8 +121,8 @@ def bench_lv(steps: int, warmup: int, cpu: bool) -> dict:
             "frac": achieved / FP32_PEAK,
             # HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE passes,
             # scaled by the copy-kernel calibration (profiles/hbm_traffic_lv_rk4_n1e6.md).
-            "traffic": LV_MEASURED_TRAFFIC_BYTES,
-            "traffic_algorithmic": 36 * n,
+            "traffic": LV_MEASURED_TRAFFIC_BYTES if cfg is LV_CFG1 else None,
+            "traffic_algorithmic": (36 if track_max else 32) * n,
             "flop_per_traj_step": LV_FLOP_PER_STEP,
             "avg_launch_ms": avg_launch_s * 1e3,
         },
@@ -122,18 +134,19 @@ def bench_lv(steps: int, warmup: int, cpu: bool) -> dict:
         os.environ.setdefault("OMP_NUM_THREADS", str(cores))
         n_cpu = int(os.environ.get("PALLADIUM_BENCH_CPU_N", n))
         sample = tuple(a[:n_cpu] for a in host)
-        oracle.lv_rk4(*(a[:64] for a in host), cfg.dt, 10, track_max=True)  # load + warm
+        oracle.lv_rk4(*(a[:64] for a in host), cfg.dt, 10, track_max=track_max)  # load + warm
         t0 = time.perf_counter()
-        oracle.lv_rk4(*sample, cfg.dt, cfg.steps, track_max=True)
+        oracle.lv_rk4(*sample, cfg.dt, cfg.steps, track_max=track_max)
         dt_cpu = time.perf_counter() - t0
         result["cpu_baseline"] = {
             "value": n_cpu * cfg.steps / dt_cpu,
             "unit": "trajectory-steps/s",
             "cores": cores,
             "kind": "port",
-            "sample": f"first {n_cpu} of {n} trajectories of config 1, all {cfg.steps} steps, C oracle (gcc -O2, OpenMP, same op order), {dt_cpu:.2f} s",
+            "sample": f"first {n_cpu} of {n} trajectories of {label}, all {cfg.steps} steps, C oracle (gcc -O2, OpenMP, same op order), {dt_cpu:.2f} s",
         }
-        result["cpu_baselines_more"] = _lv_cpu_more(host, cfg)
+        if cfg is LV_CFG1:
+            result["cpu_baselines_more"] = _lv_cpu_more(host, cfg)
     return result
 
 
@@ -524,7 +537,7 @@ def main() -> int:
         )
         return 2
     rank = int(os.environ.get("RANK", "0"))
-    fns = {"lv": bench_lv, "gbm": bench_gbm, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
+    fns = {"lv": bench_lv, "lv0": bench_lv0, "gbm": bench_gbm, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
            "bs3_lockstep": bench_bs3_lockstep, "copy": bench_copy, "df32": bench_df32}
     if a.workload not in fns:
         raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")
