@@ -331,7 +331,7 @@ def bench_df32(steps: int, warmup: int, cpu: bool) -> dict:
     if cpu:
         import oracle
 
-        n_cpu = 2048
+        n_cpu = 16384
         sample = tuple(a[:n_cpu] for a in host)
         t0 = time.perf_counter()
         want = oracle.lv_rk4_df32(*sample, cfg.dt, cfg.steps)
@@ -366,7 +366,7 @@ def bench_gs(steps: int, warmup: int, cpu: bool) -> dict:
     if cpu:
         import oracle
 
-        size, cs = cfg.size, 40
+        size, cs = cfg.size, 200
         t0 = time.perf_counter()
         oracle.gray_scott(u0, v0, cfg, cs)
         dt = time.perf_counter() - t0
