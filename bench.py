@@ -519,6 +519,82 @@ def bench_bs3_lockstep(steps: int, warmup: int, cpu: bool) -> dict:
     return res
 
 
+def bench_dispatch(steps: int, warmup: int, cpu: bool) -> dict:
+    """Host-side dispatch costs, the reference's published figures
+    (`docs/performance.md:35-44`): the blocking round trip of a tiny kernel
+    through `hip_call` (upload, launch, download, wait), the floor with 16
+    launches in flight, and the per-call cost of the C-ABI dispatch
+    (`ph_dispatch`, the FFI handler body) at 16 KB and 1 MB."""
+    import ctypes
+
+    import palladium_amd as pa
+    from palladium_amd import runtime as rt
+    from palladium_amd.emit import emit_hip, launch_geometry
+    from palladium_amd.frontend import pl
+
+    def inc(x_ref, o_ref):
+        o_ref[...] = x_ref[...] + 1.0
+
+    reps = max(steps, 200)
+    out: dict = {}
+    x = np.zeros(1, np.float32)
+    f = pa.hip_call(inc, out_shape=pl.ShapeDtypeStruct((1,), np.float32))
+    for _ in range(20):
+        f(x)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        f(x)
+    out["blocking_call_us"] = (time.perf_counter() - t0) / reps * 1e6
+
+    bound = f.bound(x)
+    for _ in range(20):
+        bound.launch(x).wait()
+    t0 = time.perf_counter()
+    for _ in range(reps // 16):
+        pend = [bound.launch(x) for _ in range(16)]
+        for p in pend:
+            p.wait()
+    out["in_flight_16_us"] = (time.perf_counter() - t0) / (reps // 16 * 16) * 1e6
+
+    for nbytes in (16 * 1024, 1024 * 1024):
+        n = nbytes // 4
+        blk = pl.BlockSpec((256,), lambda i: (i,))
+        g = pa.hip_call(inc, grid=(n // 256,), in_specs=[blk], out_specs=blk,
+                        out_shape=pl.ShapeDtypeStruct((n,), np.float32))
+        xa = np.zeros(n, np.float32)
+        spec = pa.trace(g._staged, xa)
+        src = emit_hip(spec).encode()
+        geo = launch_geometry(spec)
+        oa = np.empty_like(xa)
+        ins = (ctypes.c_void_p * 1)(xa.ctypes.data)
+        in_b = (ctypes.c_size_t * 1)(xa.nbytes)
+        outs = (ctypes.c_void_p * 1)(oa.ctypes.data)
+        out_b = (ctypes.c_size_t * 1)(oa.nbytes)
+        err = ctypes.c_void_p()
+
+        def call():
+            rc = rt.lib().ph_dispatch(src, len(src), spec.name.encode(), spec.grid[0], 1, 1, geo.block, geo.lanes, 2,
+                                      ins, in_b, 1, outs, out_b, 1, ctypes.byref(err))
+            if rc:
+                raise RuntimeError(ctypes.cast(err, ctypes.c_char_p).value)
+
+        for _ in range(10):
+            call()
+        t0 = time.perf_counter()
+        for _ in range(reps // 2):
+            call()
+        out[f"c_abi_dispatch_{nbytes // 1024}KB_us"] = (time.perf_counter() - t0) / (reps // 2) * 1e6
+        if not np.array_equal(oa, xa + 1.0):
+            raise RuntimeError("dispatch benchmark produced wrong values")
+    res = _base("host dispatch cost per call (us)", out["blocking_call_us"], "us", reps, 20, out["blocking_call_us"] / 1e3,
+                {"workload": "1-element kernel through hip_call; C-ABI ph_dispatch at 16 KB / 1 MB"})
+    res["higher_is_better"] = False
+    res["dispatch"] = out
+    res["reference_m1_pro"] = {"blocking_call_us": 136, "in_flight_16_us": 33, "ffi_call_us": "190 (16 KB) / 250 (1 MB)",
+                               "source": "reference docs/performance.md:35-44"}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -538,7 +614,7 @@ def main() -> int:
         return 2
     rank = int(os.environ.get("RANK", "0"))
     fns = {"lv": bench_lv, "lv0": bench_lv0, "gbm": bench_gbm, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
-           "bs3_lockstep": bench_bs3_lockstep, "copy": bench_copy, "df32": bench_df32}
+           "bs3_lockstep": bench_bs3_lockstep, "copy": bench_copy, "df32": bench_df32, "dispatch": bench_dispatch}
     if a.workload not in fns:
         raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")
     res = fns[a.workload](a.steps, a.warmup, cpu=not a.no_cpu and rank == 0)

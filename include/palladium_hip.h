@@ -117,6 +117,10 @@ int ph_malloc(size_t bytes, void **ptr, char **err);
 int ph_free(void *ptr);
 int ph_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream, char **err);
 int ph_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream, char **err);
+/* Device -> host copy ordered on `stream`, returning once `dst` holds the
+ * data (the readback half of a dispatch; small copies bounce through a
+ * per-thread pinned buffer). */
+int ph_memcpy_d2h_wait(void *dst, const void *src, size_t bytes, void *stream, char **err);
 int ph_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream, char **err);
 int ph_stream_create(void **stream, char **err);
 int ph_stream_destroy(void *stream);

@@ -263,6 +263,51 @@ int dispatch_geometry(int64_t grid_x, int64_t grid_y, int64_t grid_z, int64_t bl
   return PH_OK;
 }
 
+// Per-thread, per-device staging for host-buffer dispatch: one stream and
+// one device buffer per operand slot, grown on demand and reused by every
+// later call on that thread, so a dispatch allocates nothing in the steady
+// state (hipMalloc/hipFree and stream creation cost tens of microseconds
+// each). XLA:CPU calls the handler from its thread pool; thread-local
+// staging needs no lock. Kept for the life of the process, like the kernel
+// cache.
+struct DispatchStaging {
+  hipStream_t stream = nullptr;
+  std::vector<void *> bufs;
+  std::vector<size_t> caps;
+
+  int reserve(size_t slot, size_t bytes, char **err) {
+    if (slot >= bufs.size()) {
+      bufs.resize(slot + 1, nullptr);
+      caps.resize(slot + 1, 0);
+    }
+    if (bytes <= caps[slot] && bufs[slot]) return PH_OK;
+    size_t cap = bytes < 256 ? 256 : bytes;
+    if (bufs[slot]) (void)hipFree(bufs[slot]);  // grown: the old one is idle
+    bufs[slot] = nullptr;
+    caps[slot] = 0;
+    hipError_t e = hipMalloc(&bufs[slot], cap);
+    if (e != hipSuccess) return hip_fail(err, e, "hipMalloc");
+    caps[slot] = cap;
+    return PH_OK;
+  }
+};
+
+int dispatch_staging(DispatchStaging **out, char **err) {
+  thread_local std::unordered_map<int, DispatchStaging *> per_device;
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return hip_fail(err, e, "hipGetDevice");
+  DispatchStaging *&st = per_device[device];
+  if (!st) {
+    auto fresh = std::make_unique<DispatchStaging>();
+    e = hipStreamCreate(&fresh->stream);
+    if (e != hipSuccess) return hip_fail(err, e, "hipStreamCreate");
+    st = fresh.release();
+  }
+  *out = st;
+  return PH_OK;
+}
+
 }  // namespace
 
 int ph_dispatch_device(const char *src, size_t src_len, const char *name,
@@ -296,48 +341,29 @@ int ph_dispatch(const char *src, size_t src_len, const char *name,
   rc = ph_get_kernel(src, src_len, name, (int)math_mode, &k, err);
   if (rc != PH_OK) return rc;
 
-  hipStream_t stream = nullptr;
-  hipError_t e = hipStreamCreate(&stream);
-  if (e != hipSuccess) return hip_fail(err, e, "hipStreamCreate");
-  std::vector<void *> dev(n_inputs + n_outputs, nullptr);
-  // Staging buffers and stream are released on every path; a failure to
-  // release cannot be reported better than the error already being returned.
-  auto cleanup = [&]() {
-    for (void *p : dev)
-      if (p) (void)hipFree(p);
-    (void)hipStreamDestroy(stream);
-  };
-  for (size_t i = 0; i < n_inputs + n_outputs; ++i) {
-    size_t bytes = i < n_inputs ? input_bytes[i] : output_bytes[i - n_inputs];
-    e = hipMalloc(&dev[i], bytes ? bytes : 4);
-    if (e != hipSuccess) {
-      cleanup();
-      return hip_fail(err, e, "hipMalloc");
-    }
+  DispatchStaging *st = nullptr;
+  rc = dispatch_staging(&st, err);
+  if (rc != PH_OK) return rc;
+  const size_t n_ops = n_inputs + n_outputs;
+  for (size_t i = 0; i < n_ops; ++i) {
+    rc = st->reserve(i, i < n_inputs ? input_bytes[i] : output_bytes[i - n_inputs], err);
+    if (rc != PH_OK) return rc;
   }
+  std::vector<void *> dev(st->bufs.begin(), st->bufs.begin() + n_ops);
+  hipError_t e;
   for (size_t i = 0; i < n_inputs; ++i) {
     if (!input_bytes[i]) continue;
-    e = hipMemcpyHtoDAsync(dev[i], const_cast<void *>(inputs[i]), input_bytes[i], stream);
-    if (e != hipSuccess) {
-      cleanup();
-      return hip_fail(err, e, "hipMemcpyHtoDAsync");
-    }
+    e = hipMemcpyHtoDAsync(dev[i], const_cast<void *>(inputs[i]), input_bytes[i], st->stream);
+    if (e != hipSuccess) return hip_fail(err, e, "hipMemcpyHtoDAsync");
   }
-  rc = ph_launch_ptrs(k, blocks, block, stream, dev.data(), dev.size(), err);
-  if (rc != PH_OK) {
-    cleanup();
-    return rc;
-  }
+  rc = ph_launch_ptrs(k, blocks, block, st->stream, dev.data(), dev.size(), err);
+  if (rc != PH_OK) return rc;
   for (size_t i = 0; i < n_outputs; ++i) {
     if (!output_bytes[i]) continue;
-    e = hipMemcpyDtoHAsync(outputs[i], dev[n_inputs + i], output_bytes[i], stream);
-    if (e != hipSuccess) {
-      cleanup();
-      return hip_fail(err, e, "hipMemcpyDtoHAsync");
-    }
+    e = hipMemcpyDtoHAsync(outputs[i], dev[n_inputs + i], output_bytes[i], st->stream);
+    if (e != hipSuccess) return hip_fail(err, e, "hipMemcpyDtoHAsync");
   }
-  e = hipStreamSynchronize(stream);
-  cleanup();
+  e = hipStreamSynchronize(st->stream);
   if (e != hipSuccess) return hip_fail(err, e, "hipStreamSynchronize");
   return PH_OK;
 }
@@ -373,6 +399,34 @@ int ph_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream, char *
 int ph_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream, char **err) {
   hipError_t e = hipMemcpyDtoHAsync(dst, const_cast<void *>(src), bytes, (hipStream_t)stream);
   return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipMemcpyDtoHAsync");
+}
+
+int ph_memcpy_d2h_wait(void *dst, const void *src, size_t bytes, void *stream, char **err) {
+  // Small readbacks bounce through a per-thread pinned buffer: a DMA into
+  // pinned memory plus a memcpy takes about 13 us on MI355X, a copy into
+  // pageable memory about 23 us. Kept for the life of the process.
+  constexpr size_t kBounce = 64 * 1024;
+  thread_local void *bounce = nullptr;
+  hipStream_t s = (hipStream_t)stream;
+  if (bytes <= kBounce) {
+    if (!bounce) {
+      hipError_t e = hipHostMalloc(&bounce, kBounce, hipHostMallocDefault);
+      if (e != hipSuccess) {
+        bounce = nullptr;
+        return hip_fail(err, e, "hipHostMalloc");
+      }
+    }
+    hipError_t e = hipMemcpyDtoHAsync(bounce, const_cast<void *>(src), bytes, s);
+    if (e != hipSuccess) return hip_fail(err, e, "hipMemcpyDtoHAsync");
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return hip_fail(err, e, "hipStreamSynchronize");
+    std::memcpy(dst, bounce, bytes);
+    return PH_OK;
+  }
+  hipError_t e = hipMemcpyDtoHAsync(dst, const_cast<void *>(src), bytes, s);
+  if (e != hipSuccess) return hip_fail(err, e, "hipMemcpyDtoHAsync");
+  e = hipStreamSynchronize(s);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipStreamSynchronize");
 }
 
 int ph_memcpy_d2d(void *dst, const void *src, size_t bytes, void *stream, char **err) {

@@ -35,6 +35,9 @@ from palladium_amd.trace import KernelSpec
 
 __all__ = ["BoundKernel", "PendingResult", "bind"]
 
+# Launches a BoundKernel keeps in flight before `launch` blocks.
+IN_FLIGHT = 4
+
 
 def _dump_hip(name: str, source: str) -> None:
     dump = os.environ.get("PALLADIUM_DUMP_HIP")
@@ -103,8 +106,12 @@ class BoundKernel:
     hip_source: str
     threadgroup: int | tuple[int, ...] | None = None
     geometry: LaunchGeometry | None = None
-    _in_bufs: list[rt.Buffer] = dataclasses.field(default_factory=list, compare=False, repr=False)
-    _last_pending: list[PendingResult] = dataclasses.field(default_factory=list, compare=False, repr=False)
+    # Input buffer sets for launches in flight: set k serves launches
+    # k, k + IN_FLIGHT, ...; a launch waits only for the last launch that
+    # used its set, so uploads for the next call overlap the running kernel.
+    _ring: list[list[rt.Buffer]] = dataclasses.field(default_factory=list, compare=False, repr=False)
+    _ring_pending: list[PendingResult | None] = dataclasses.field(default_factory=list, compare=False, repr=False)
+    _ring_next: list[int] = dataclasses.field(default_factory=lambda: [0], compare=False, repr=False)
     _launch_lock: threading.Lock = dataclasses.field(default_factory=threading.Lock, compare=False, repr=False)
     _stream: list[rt.Stream] = dataclasses.field(default_factory=list, compare=False, repr=False)
 
@@ -140,8 +147,9 @@ class BoundKernel:
         """Upload inputs and launch without blocking on the result.
 
         Thread-safe: uploads and launches are serialised on a per-kernel
-        lock (after waiting out the previous launch, whose reads of the
-        reused input buffers must finish first); waits are not locked.
+        lock; waits are not locked. Up to IN_FLIGHT launches may be queued:
+        each uses one of IN_FLIGHT input buffer sets in turn, after waiting
+        out the launch that last read that set.
 
         Raises
         ------
@@ -150,16 +158,21 @@ class BoundKernel:
         """
         arrs = self._check_args(arrays)
         with self._launch_lock:
-            if self._last_pending:
-                self._last_pending[0].event.synchronize()
+            k = self._ring_next[0]
+            self._ring_next[0] = (k + 1) % IN_FLIGHT
+            if len(self._ring) <= k:
+                self._ring.append([rt.Buffer.empty(a.shape, a.dtype) for a in arrs])
+                self._ring_pending.append(None)
+            previous = self._ring_pending[k]
+            if previous is not None:
+                previous.event.synchronize()
+            bufs = self._ring[k]
             stream = self.stream
-            if len(self._in_bufs) < len(arrs):
-                self._in_bufs[:] = [rt.Buffer.empty(a.shape, a.dtype) for a in arrs]
-            for buf, a in zip(self._in_bufs, arrs):
+            for buf, a in zip(bufs, arrs):
                 buf.copy_from(a, stream)
-            outs = self._new_outputs()
-            pending = self._dispatch(self._in_bufs, outs)
+            pending = self._dispatch(bufs, self._new_outputs())
             pending.host_inputs = tuple(arrs)
+            self._ring_pending[k] = pending
             return pending
 
     def __call__(self, *arrays: np.ndarray) -> np.ndarray | tuple[np.ndarray, ...]:
@@ -171,21 +184,21 @@ class BoundKernel:
         ptrs = [b.ptr for b in in_bufs] + [b.ptr for b in out_bufs]
         self.kernel.launch_ptrs(geo.blocks, geo.block, ptrs, self.stream)
         ev = rt.Event().record(self.stream)
-        pending = PendingResult(ev, out_bufs, self.stream)
-        self._last_pending[:] = [pending]
-        return pending
+        return PendingResult(ev, out_bufs, self.stream)
 
     def pinned(self, *arrays: np.ndarray) -> Callable[[], np.ndarray | tuple[np.ndarray, ...]]:
         """Upload once; return a zero-argument callable that re-dispatches
         on the pinned device buffers with fresh outputs
-        (`src/palladium/dispatch.py:230-255`)."""
-        self.launch(*arrays).wait()
+        (`src/palladium/dispatch.py:230-255`). The pinned inputs live in
+        buffers of their own, so later `launch` calls cannot overwrite them."""
+        arrs = self._check_args(arrays)
+        pinned = [rt.Buffer.empty(a.shape, a.dtype) for a in arrs]
+        for buf, a in zip(pinned, arrs):
+            buf.copy_from(a)  # synchronous: the host arrays may go away
 
         def call() -> np.ndarray | tuple[np.ndarray, ...]:
             with self._launch_lock:
-                if self._last_pending:
-                    self._last_pending[0].event.synchronize()
-                pending = self._dispatch(self._in_bufs, self._new_outputs())
+                pending = self._dispatch(pinned, self._new_outputs())
             return pending.wait()
 
         return call

@@ -118,6 +118,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "ph_free": (c.c_int, [_P]),
         "ph_memcpy_h2d": (c.c_int, [_P, _P, c.c_size_t, _P, _PP]),
         "ph_memcpy_d2h": (c.c_int, [_P, _P, c.c_size_t, _P, _PP]),
+        "ph_memcpy_d2h_wait": (c.c_int, [_P, _P, c.c_size_t, _P, _PP]),
         "ph_memcpy_d2d": (c.c_int, [_P, _P, c.c_size_t, _P, _PP]),
         "ph_stream_create": (c.c_int, [_PP, _PP]),
         "ph_stream_destroy": (c.c_int, [_P]),
@@ -356,11 +357,11 @@ class Buffer:
                 synchronize_stream(None)
 
     def to_numpy(self, stream: Any = None) -> np.ndarray:
+        """Copy to a new host array after the work queued on `stream`."""
         out = np.empty(self.shape, self.dtype)
         if self.nbytes:
-            _call("ph_memcpy_d2h", out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(self.ptr),
+            _call("ph_memcpy_d2h_wait", out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(self.ptr),
                   ctypes.c_size_t(self.nbytes), _stream_handle(stream))
-            synchronize_stream(stream)
         return out
 
     def __del__(self) -> None:
