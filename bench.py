@@ -340,7 +340,26 @@ def bench_df32(steps: int, warmup: int, cpu: bool) -> dict:
         res["parity_sample_max_abs_diff"] = float(max(np.max(np.abs(g - w)) for g, w in zip(got, want)))
         res["cpu_baseline"] = {"value": n_cpu * cfg.steps / dt, "unit": "trajectory-steps/s", "cores": _cpu_cores(),
                                "kind": "port", "sample": f"first {n_cpu} trajectories, C oracle df32, {dt:.2f} s"}
+    res["accuracy"] = _df32_accuracy(host, [o.to_numpy(stream) for o in outs], cfg)
     return res
+
+
+def _df32_accuracy(host, outs, cfg, n_acc: int = 2048) -> dict:
+    """Max relative error of x against a float64 RK4 with the same float32
+    step constants, for the df32 result and for the fp32 oracle (the
+    `err_df32 < err_fp32` check of examples/05_df32_precision.py:197)."""
+    import oracle
+    from oracle.ref64 import lv_rk4_f64
+
+    sample = tuple(a[:n_acc] for a in host)
+    d32 = np.float32(cfg.dt)
+    consts = (float(np.float32(0.5) * d32), float(d32), float(d32 / np.float32(6.0)))
+    x64, _ = lv_rk4_f64(*sample, cfg.dt, cfg.steps, consts=consts)
+    x_df = outs[0][:n_acc].astype(np.float64) + outs[1][:n_acc].astype(np.float64)
+    x_f32, _ = oracle.lv_rk4(*sample, cfg.dt, cfg.steps)
+    return {"sample": f"first {n_acc} trajectories, all {cfg.steps} steps",
+            "max_rel_err_df32": float(np.max(np.abs(x_df - x64) / np.abs(x64))),
+            "max_rel_err_fp32": float(np.max(np.abs(x_f32 - x64) / np.abs(x64)))}
 
 
 def bench_gs(steps: int, warmup: int, cpu: bool) -> dict:
@@ -478,6 +497,7 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
                 steps, warmup, ms, {"workload": "adaptive BS3(2) Van der Pol, config 2", "n": cfg.n, "math_mode": "fast"})
     ops = loop_ops_per_iteration(trace(call._staged, *host), "while")
     achieved = total * ops / (avg / 1e3)
+    res["accepted_steps_per_s"] = float(acc.sum()) / (ms / 1e3)
     res["roofline"] = {"bound": "valu", "achieved": achieved / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TOP/s",
                        "frac": achieved / FP32_PEAK, "traffic": None, "ops_per_attempt": ops,
                        "ops_note": "elementwise eqns of the while condition + body per attempt (pow = 1)",
@@ -627,8 +647,8 @@ def main() -> int:
         for key, fn in (("gray_scott_4096", bench_gs), ("gbm_paths", bench_gbm), ("bs3_vdp", bench_bs3),
                         ("lv_rk4_df32", bench_df32)):
             r = fn(a.steps, a.warmup, cpu=False)
-            res["secondary"][key] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline")
-                                     if k in r}
+            res["secondary"][key] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline",
+                                                        "accuracy", "accepted_steps_per_s") if k in r}
     if rank == 0:
         print(json.dumps(res), flush=True)
     return 0
