@@ -55,8 +55,8 @@ def _lv_mutant(x0, y0, a, b, c, d, dt, steps, mutation):
 def test_lv_pin_detects(mutation):
     args = lv_inputs(2000, 0)
     x, y = oracle.lv_rk4(*args, 0.01, 1000)
-    mx, my = _lv_mutant(*args, 0.01, 1000, mutation)
-    with np.errstate(all="ignore"):
+    with np.errstate(all="ignore"):  # some mutants blow up; that counts as detected
+        mx, my = _lv_mutant(*args, 0.01, 1000, mutation)
         rel = max(np.nanmax(np.abs(x - mx) / np.abs(mx)), np.nanmax(np.abs(y - my) / np.abs(my)))
     assert not rel < 10 * LV_TOL  # NaN/inf from a blown-up mutant also counts as detected
 
