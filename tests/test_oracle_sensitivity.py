@@ -57,7 +57,7 @@ def test_lv_pin_detects(mutation):
     x, y = oracle.lv_rk4(*args, 0.01, 1000)
     with np.errstate(all="ignore"):  # some mutants blow up; that counts as detected
         mx, my = _lv_mutant(*args, 0.01, 1000, mutation)
-        rel = max(np.nanmax(np.abs(x - mx) / np.abs(mx)), np.nanmax(np.abs(y - my) / np.abs(my)))
+        rel = max(np.max(np.abs(x - mx) / np.abs(mx)), np.max(np.abs(y - my) / np.abs(my)))
     assert not rel < 10 * LV_TOL  # NaN/inf from a blown-up mutant also counts as detected
 
 
