@@ -205,13 +205,18 @@ _NOT_OPS = {"broadcast_in_dim", "bitcast_convert_type", "reshape", "squeeze", "e
 def loop_ops_per_iteration(spec, loop: str) -> int:
     """Elementwise ops executed per iteration of the kernel's `loop`
     (`while`: condition + body; `scan`: body), counted from the IR: one per
-    eqn (pow = 1), THREEFRY_OPS per threefry2x32, nothing for data movement."""
+    eqn (pow = 1), THREEFRY_OPS per Threefry block (threefry2x32, fold_in,
+    and each element of random_bits plus its xor), nothing for data
+    movement."""
     def count(j) -> int:
         n = 0
         for e in j.eqns:
             name = e.primitive.name
-            if name == "threefry2x32":
+            if name in ("threefry2x32", "random_fold_in"):
                 n += THREEFRY_OPS
+            elif name == "random_bits":
+                # One block per output element, its two words xored.
+                n += (THREEFRY_OPS + 1) * max(1, int(np.prod(e.outvars[0].aval.shape)))
             elif name not in _NOT_OPS and not any(hasattr(getattr(v, "jaxpr", v), "eqns") for v in e.params.values()):
                 n += 1
         return n
@@ -476,6 +481,33 @@ def bench_gs_lds(steps: int, warmup: int, cpu: bool) -> dict:
     return res
 
 
+def bench_gbm_fold_in(steps: int, warmup: int, cpu: bool) -> dict:
+    """Config 3 with the reference's own key derivation (examples/03: a
+    fold_in per path, two per step, each uniform its own Threefry block),
+    timed beside the one-block counter form of `gbm`."""
+    from palladium_amd import runtime as rt
+    from palladium_amd.frontend import random
+    from palladium_amd.workloads import GBM_CFG, gbm_fold_in_call
+
+    cfg = GBM_CFG
+    key = random.key(cfg.seed)
+    call = gbm_fold_in_call(cfg)
+    bound = call.bound(key)
+    ops = [rt.Buffer.from_numpy(key), rt.Buffer.empty((cfg.n_paths,), np.float32)]
+    ms, avg = _timed_launches(bound, ops, steps, warmup)
+    ps = cfg.n_paths * cfg.n_steps
+    per_step = loop_ops_per_iteration(trace(call._staged, key), "scan")
+    achieved = ps * per_step / (avg / 1e3)
+    res = _base("GBM path-steps/s, reference fold_in derivation (4 Threefry blocks per step)", ps / (ms / 1e3),
+                "path-steps/s", steps, warmup, ms,
+                {"workload": "GBM Monte Carlo, config 3, examples/03 key derivation", "paths": cfg.n_paths,
+                 "steps": cfg.n_steps, "math_mode": "fast"})
+    res["roofline"] = {"bound": "valu", "achieved": achieved / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TOP/s",
+                       "frac": achieved / FP32_PEAK, "traffic": None, "ops_per_path_step": per_step,
+                       "avg_launch_ms": avg}
+    return res
+
+
 def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     from palladium_amd import runtime as rt
     from palladium_amd.workloads import BS3_CFG, bs3_inputs, bs3_vdp_call
@@ -633,7 +665,7 @@ def main() -> int:
         )
         return 2
     rank = int(os.environ.get("RANK", "0"))
-    fns = {"lv": bench_lv, "lv0": bench_lv0, "gbm": bench_gbm, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
+    fns = {"lv": bench_lv, "lv0": bench_lv0, "gbm": bench_gbm, "gbm_fold_in": bench_gbm_fold_in, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
            "bs3_lockstep": bench_bs3_lockstep, "copy": bench_copy, "df32": bench_df32, "dispatch": bench_dispatch}
     if a.workload not in fns:
         raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")

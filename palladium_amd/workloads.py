@@ -394,6 +394,61 @@ def gbm_call(cfg: GBMConfig = GBM_CFG, n_paths: int | None = None, **kw: Any):
     )
 
 
+def gbm_fold_in_kernel(cfg: GBMConfig, record_steps: int = 0):
+    """The reference's own derivation (`examples/03_sde_montecarlo.py:95-117`):
+    key0 = fold_in(key, path); per step i, u1 from fold_in(key0, 2i) and u2
+    from fold_in(key0, 2i + 1), each through `random.uniform` (four Threefry
+    blocks per step, against the one-block counter form of `gbm_kernel`).
+    With `record_steps`, the first steps' (u1, u2) are also written out, so
+    the raw uniforms can be checked bit for bit."""
+    drift, vol = cfg.drift_dt, cfg.vol_sqdt
+
+    def kernel(key_ref, o_ref, *u_refs):
+        base = random.wrap_key_data(key_ref[...])
+        key0 = random.fold_in(base, pl.program_id(0))
+
+        def uniforms(i):
+            k1 = random.fold_in(key0, 2 * i)
+            k2 = random.fold_in(key0, 2 * i + 1)
+            return jnp.maximum(random.uniform(k1, ()), 1e-7), random.uniform(k2, ())
+
+        def step(i, s):
+            u1, u2 = uniforms(i)
+            z = jnp.sqrt(-2.0 * jnp.log(u1)) * jnp.cos(2.0 * jnp.pi * u2)
+            return s * jnp.exp(drift + vol * z)
+
+        s = lax.fori_loop(0, cfg.n_steps, step, cfg.s0)
+        o_ref[0] = jnp.maximum(s - cfg.strike, 0.0)
+        for j in range(record_steps):
+            u1, u2 = uniforms(j)
+            u_refs[0][0, j] = u1
+            u_refs[1][0, j] = u2
+
+    kernel.__name__ = "gbm_fold_in"
+    return kernel
+
+
+def gbm_fold_in_call(cfg: GBMConfig = GBM_CFG, n_paths: int | None = None, record_steps: int = 0, **kw: Any):
+    import palladium_amd as pa
+
+    n = n_paths or cfg.n_paths
+    out_specs = [pl.BlockSpec((1,), lambda i: (i,))]
+    out_shape = [pl.ShapeDtypeStruct((n,), F32)]
+    if record_steps:
+        rec = pl.BlockSpec((1, record_steps), lambda i: (i, 0))
+        out_specs += [rec, rec]
+        out_shape += [pl.ShapeDtypeStruct((n, record_steps), F32)] * 2
+    return pa.hip_call(
+        gbm_fold_in_kernel(cfg, record_steps),
+        grid=(n,),
+        in_specs=[pl.BlockSpec((2,), lambda i: (0,))],
+        out_specs=tuple(out_specs) if record_steps else out_specs[0],
+        out_shape=tuple(out_shape) if record_steps else out_shape[0],
+        name="gbm_fold_in",
+        **kw,
+    )
+
+
 def black_scholes_call(s0: float, k: float, t: float, r: float, sigma: float) -> float:
     """Closed-form European call (`examples/03_sde_montecarlo.py:73-76`)."""
     d1 = (math.log(s0 / k) + (r + sigma**2 / 2) * t) / (sigma * math.sqrt(t))

@@ -69,3 +69,29 @@ def test_price_within_three_standard_errors_full_size():
     se = disc * payoff.std(ddof=1) / np.sqrt(payoff.size)
     exact = black_scholes_call(cfg.s0, cfg.strike, cfg.t, cfg.r, cfg.sigma)
     assert abs(price - exact) < 3 * se, (price, exact, se)
+
+
+def test_reference_fold_in_derivation():
+    """examples/03's own key derivation: the raw uniforms bit-exact against
+    the oracle's fold_in / random_bits / bits_to_uniform, and the price
+    within 3 standard errors of Black-Scholes."""
+    import math
+
+    from palladium_amd.workloads import gbm_fold_in_call
+
+    cfg = GBM_CFG
+    n, rec = 512, 3
+    key = random.key(cfg.seed)
+    payoff, u1, u2 = gbm_fold_in_call(cfg, n_paths=n, record_steps=rec, math_mode="safe")(key)
+    for p in (0, 1, 77, 511):
+        k0 = oracle.fold_in(key, p)
+        for j in range(rec):
+            b1 = oracle.random_bits(oracle.fold_in(k0, 2 * j), 1)[0]
+            b2 = oracle.random_bits(oracle.fold_in(k0, 2 * j + 1), 1)[0]
+            assert u1[p, j] == max(oracle.bits_to_uniform(b1), np.float32(1e-7))
+            assert u2[p, j] == oracle.bits_to_uniform(b2)
+    big = 262_144
+    payoff = gbm_fold_in_call(cfg, n_paths=big)(key).astype(np.float64)
+    disc = math.exp(-cfg.r * cfg.t)
+    price, se = disc * payoff.mean(), disc * payoff.std(ddof=1) / math.sqrt(big)
+    assert abs(price - black_scholes_call(cfg.s0, cfg.strike, cfg.t, cfg.r, cfg.sigma)) < 3 * se
