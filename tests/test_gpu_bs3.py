@@ -75,3 +75,15 @@ def test_reference_lockstep_formulation_matches_while_loop():
     np.testing.assert_array_equal(v, want[2])
     np.testing.assert_array_equal(rej, want[4].astype(np.float32))
     np.testing.assert_array_equal(steps, (max_steps - want[4]).astype(np.float32))
+
+
+def test_full_config2_safe_states_and_counts_exact():
+    """Config 2 at its full size (N = 262,144, mu log-uniform in [0.1, 100]):
+    final states and accepted/rejected counts equal the oracle's exactly."""
+    n = BS3_CFG.n
+    x0, v0, mu = bs3_inputs(n, seed=BS3_CFG.seed)
+    got = bs3_vdp_call(n, math_mode=pa.MathMode.SAFE)(x0, v0, mu)
+    want = oracle.bs3_vdp(x0, v0, mu, BS3_CFG)
+    for g, w, name in zip(got, want, ["t", "x", "v", "accepted", "rejected"]):
+        np.testing.assert_array_equal(g, w, err_msg=name)
+    assert got[3].sum() > 2e8  # the full workload ran: ~2.5e8 accepted steps

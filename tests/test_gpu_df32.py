@@ -27,3 +27,18 @@ def test_df32_more_accurate_than_fp32():
     ref = wxh.astype(np.float64) + wxl
     assert np.max(np.abs(xh.astype(np.float64) + xl - ref)) == 0.0
     assert np.max(np.abs(x32 - ref)) > 1e3 * 1e-10
+
+
+def test_full_config4b_bit_exact_on_a_sample():
+    """Config 4b at full size (N = 1e6, config-1 inputs, dt = 0.005, 4,000
+    steps, SAFE); the first 16,384 trajectories against the oracle."""
+    from palladium_amd.workloads import LV_CFG1
+
+    cfg = LV_CFG1
+    args = lv_inputs(cfg.n, cfg.seed)
+    got = lv_rk4_df32(*args, cfg.dt, cfg.steps)
+    m = 16384
+    want = oracle.lv_rk4_df32(*(a[:m] for a in args), cfg.dt, cfg.steps)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g[:m], w)
+    assert all(np.all(np.isfinite(g)) for g in got)

@@ -95,3 +95,25 @@ def test_reference_fold_in_derivation():
     disc = math.exp(-cfg.r * cfg.t)
     price, se = disc * payoff.mean(), disc * payoff.std(ddof=1) / math.sqrt(big)
     assert abs(price - black_scholes_call(cfg.s0, cfg.strike, cfg.t, cfg.r, cfg.sigma)) < 3 * se
+
+
+def test_threefry_bits_bit_exact_across_config3_counter_range():
+    """Counters (path, step) sampled over config 3's full ranges
+    (paths < 4,194,304, steps < 252), including the corners."""
+    rng = np.random.default_rng(3)
+    m = 4096
+    paths = rng.integers(0, GBM_CFG.n_paths, m).astype(np.uint32)
+    steps = rng.integers(0, GBM_CFG.n_steps, m).astype(np.uint32)
+    paths[:4] = [0, 0, GBM_CFG.n_paths - 1, GBM_CFG.n_paths - 1]
+    steps[:4] = [0, GBM_CFG.n_steps - 1, 0, GBM_CFG.n_steps - 1]
+
+    def kernel(key_ref, p_ref, s_ref, o0_ref, o1_ref):
+        o0_ref[0], o1_ref[0] = random.threefry2x32_p(key_ref[0], key_ref[1], p_ref[0], s_ref[0])
+
+    one = pl.BlockSpec((1,), lambda i: (i,))
+    f = pa.hip_call(kernel, grid=(m,), in_specs=[pl.BlockSpec((2,), lambda i: (0,)), one, one],
+                    out_specs=(one, one), out_shape=(pl.ShapeDtypeStruct((m,), np.uint32),) * 2)
+    key = random.key(GBM_CFG.seed)
+    g0, g1 = f(key, paths, steps)
+    for i in range(m):
+        assert (g0[i], g1[i]) == oracle.threefry2x32(int(key[0]), int(key[1]), int(paths[i]), int(steps[i]))

@@ -52,3 +52,15 @@ def test_fast_close_to_oracle():
     wu, wv = oracle.gray_scott(u0, v0, GS_CFG, steps)
     np.testing.assert_allclose(u, wu, rtol=1e-4, atol=1e-5)
     np.testing.assert_allclose(v, wv, rtol=1e-4, atol=1e-5)
+
+
+def test_full_config4_safe_bit_exact():
+    """Config 4 at full size: 4096^2, 2,000 steps as one HIP graph, SAFE,
+    equal to the oracle bit for bit."""
+    size, steps = GS_CFG.size, GS_CFG.steps
+    u0, v0 = gray_scott_initial(size)
+    u, v, _ = gray_scott_run(gray_scott_call(size=size, math_mode="safe"), u0, v0, steps)
+    wu, wv = oracle.gray_scott(u0, v0, GS_CFG, steps)
+    np.testing.assert_array_equal(u, wu)
+    np.testing.assert_array_equal(v, wv)
+    assert float(np.abs(v).sum()) > 1.0  # a pattern grew
