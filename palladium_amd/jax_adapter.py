@@ -153,8 +153,10 @@ def trace_jax(pallas_fn: Any, *example_args: Any) -> KernelSpec:
 
     mappings = list(gm.block_mappings)
     grid = tuple(int(g) for g in gm.grid) or (1,)
+    nsi = params.get("name_and_src_info")  # newer JAX: NameAndSrcInfo(name=...)
+    name = params.get("name") or getattr(nsi, "name", None) or "palladium_kernel"
     return KernelSpec(
-        name=params.get("name") or "palladium_kernel",
+        name=name if str(name).isidentifier() else "palladium_kernel",
         jaxpr=conv.jaxpr(kj),
         grid=grid,
         inputs=infos(mappings[:n_in]),
