@@ -547,6 +547,49 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     return res
 
 
+def bench_bs3_sorted(steps: int, warmup: int, cpu: bool) -> dict:
+    """What divergence costs the adaptive solver: config 2 with the
+    trajectories ordered by mu (stiffness), so each wavefront holds similar
+    step counts, results scattered back and checked equal to the unsorted
+    run's. A measurement of lane coherence, not a different benchmark: the
+    `bs3` line keeps the given order."""
+    from palladium_amd import runtime as rt
+    from palladium_amd.workloads import BS3_CFG, bs3_inputs, bs3_vdp_call
+
+    cfg = BS3_CFG
+    host = bs3_inputs(cfg.n)
+    order = np.argsort(host[2], kind="stable")
+    sorted_host = tuple(np.ascontiguousarray(a[order]) for a in host)
+    call = bs3_vdp_call(cfg.n)
+    bound = call.bound(*host)
+
+    def run(h):
+        ins = [rt.Buffer.from_numpy(a) for a in h]
+        outs = [rt.Buffer.empty((cfg.n,), np.float32) for _ in range(3)] + \
+               [rt.Buffer.empty((cfg.n,), np.int32) for _ in range(2)]
+        ms, avg = _timed_launches(bound, ins + outs, steps, warmup)
+        return ms, [o.to_numpy() for o in outs]
+
+    ms_given, out_given = run(host)
+    ms_sorted, out_sorted = run(sorted_host)
+    unsorted = [np.empty_like(o) for o in out_sorted]
+    for u, o in zip(unsorted, out_sorted):
+        u[order] = o
+    attempts = (out_sorted[3] + out_sorted[4]).astype(np.int64)
+    waves = attempts.reshape(-1, 64)
+    active = float(waves.sum() / (waves.max(axis=1).sum() * 64))
+    total = int(attempts.sum())
+    res = _base("BS3(2)+PI attempted steps/s, trajectories ordered by stiffness", total / (ms_sorted / 1e3),
+                "attempts/s", steps, warmup, ms_sorted,
+                {"workload": "adaptive BS3(2) Van der Pol, config 2, inputs sorted by mu", "n": cfg.n,
+                 "math_mode": "fast"})
+    res["given_order_ms"] = ms_given
+    res["useful_lane_fraction"] = active
+    res["identical_per_trajectory"] = all(np.array_equal(a, b) for a, b in zip(unsorted, out_given))
+    res["roofline"] = {"bound": "valu", "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None}
+    return res
+
+
 def bench_bs3_lockstep(steps: int, warmup: int, cpu: bool) -> dict:
     """The reference's formulation of config 2: every lane runs a fixed
     trip of attempts (the ensemble's largest need), idling after T1. Timed
@@ -754,7 +797,7 @@ def main() -> int:
         return 2
     rank = int(os.environ.get("RANK", "0"))
     fns = {"lv": bench_lv, "lv0": bench_lv0, "gbm": bench_gbm, "gbm_fold_in": bench_gbm_fold_in, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
-           "bs3_lockstep": bench_bs3_lockstep, "copy": bench_copy, "df32": bench_df32, "dispatch": bench_dispatch,
+           "bs3_lockstep": bench_bs3_lockstep, "bs3_sorted": bench_bs3_sorted, "copy": bench_copy, "df32": bench_df32, "dispatch": bench_dispatch,
            "valu_rates": bench_valu_rates}
     if a.workload not in fns:
         raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")
