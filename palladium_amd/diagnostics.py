@@ -26,6 +26,11 @@ _VGPRS_PER_SIMD = 512
 _MAX_WAVES_PER_SIMD = 8
 
 
+# Per-instance scratch above this size earns a hint in the explain text: a
+# large gridless block runs as one thread walking arrays in scratch memory.
+SCRATCH_HINT_BYTES = 4096
+
+
 @dataclasses.dataclass(frozen=True)
 class ResourceUsage:
     vgprs: int
@@ -84,7 +89,14 @@ class KernelDiagnostics:
                 f"vgprs={r.vgprs} sgprs={r.sgprs} spills={r.vgpr_spills + r.sgpr_spills} "
                 f"scratch={r.scratch_bytes}B lds={r.lds_bytes}B waves/simd={r.waves_per_simd}"
             )
-        return " ".join(parts)
+        text = " ".join(parts)
+        if r is not None and r.scratch_bytes > SCRATCH_HINT_BYTES:
+            text += (
+                f"\n  hint: each program instance keeps {r.scratch_bytes} B of arrays in scratch "
+                "memory; split the work with a grid and BlockSpecs so each instance holds a "
+                "small block"
+            )
+        return text
 
 
 def _notes(code: bytes) -> list[tuple[str, int, bytes]]:

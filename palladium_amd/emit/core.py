@@ -64,6 +64,8 @@ CTYPES = {
 # Loads of read-only blocks up to this many elements go to registers;
 # larger blocks are aliased and read through the pointer.
 REGISTER_BLOCK_LIMIT = 16
+# Element loops up to this many trips are fully unrolled.
+UNROLL_LIMIT = 64
 DEFAULT_BLOCK = 256
 NUM_XCDS = 8
 
@@ -142,12 +144,16 @@ class Cursor:
         self.emit("}")
 
     def loop(self, count: int, prefix: str = "_i") -> "contextlib.AbstractContextManager[str]":
-        """`for (int i = 0; i < count; ++i)` fully unrolled; yields `i`."""
+        """`for (int i = 0; i < count; ++i)`, yields `i`. Loops up to
+        UNROLL_LIMIT trips are fully unrolled (constant indices let small
+        arrays stay in registers); longer ones are left to the compiler,
+        since their arrays live in scratch either way."""
 
         @contextlib.contextmanager
         def cm() -> Iterator[str]:
             i = self.fresh(prefix)
-            self.emit("#pragma unroll")
+            if count <= UNROLL_LIMIT:
+                self.emit("#pragma unroll")
             with self.block(f"for (int {i} = 0; {i} < {count}; ++{i})"):
                 yield i
 

@@ -43,6 +43,25 @@ def test_explain_reports_geometry_and_resources():
     assert f"palladium kernel {diag.name}" in str(diag)
 
 
+def test_large_gridless_block_compiles_and_hints_at_blockspecs():
+    """A 4096-element gridless block (reference tests/test_17_robustness.py:
+    202-214 expects such a kernel to either work or name the fix): it
+    compiles, long element loops are not force-unrolled, and explain names
+    the fix for the scratch it needs."""
+
+    def kernel(x_ref, y_ref, o_ref):
+        o_ref[...] = 2.0 * x_ref[...] + y_ref[...]
+
+    call = pa.hip_call(kernel, out_shape=pl.ShapeDtypeStruct((4096,), F))
+    x = np.zeros(4096, F)
+    src = pa.debug_hip(kernel, x, x, out_shape=pl.ShapeDtypeStruct((4096,), F))
+    assert "< 4096" in src and "#pragma unroll" not in src
+    diag = call.explain(x, x)
+    assert diag.resources.scratch_bytes > 4096
+    assert "grid and BlockSpecs" in str(diag)
+    assert "hint" not in str(_double(64).explain(np.zeros(64, F)))
+
+
 def test_explain_explicit_threadgroup():
     diag = _double(128, threadgroup=64).explain(np.zeros(128, F), compile=False)
     assert diag.threadgroup == (64,)

@@ -35,6 +35,19 @@ def test_copy_2d_gridless(rng):
     np.testing.assert_array_equal(_both(f, x), x)
 
 
+def test_large_gridless_block_runs(rng):
+    """4096 elements in one gridless block (reference tests/test_17_robustness.py:
+    202-214): one instance walks scratch-resident arrays, results exact."""
+
+    def kernel(x_ref, y_ref, o_ref):
+        o_ref[...] = 2.0 * x_ref[...] + y_ref[...]
+
+    f = pa.hip_call(kernel, out_shape=SDS((4096,), F), math_mode="safe")
+    x = rng.standard_normal(4096, dtype=F)
+    y = rng.standard_normal(4096, dtype=F)
+    np.testing.assert_array_equal(_both(f, x, y), F(2.0) * x + y)
+
+
 def test_blocked_saxpy(rng):
     def kernel(a_ref, x_ref, y_ref, o_ref):
         o_ref[...] = a_ref[0] * x_ref[...] + y_ref[...]
