@@ -24,6 +24,7 @@ from palladium_amd import runtime
 from palladium_amd.diagnostics import KernelDiagnostics, explain_spec, log_compile
 from palladium_amd.dispatch import BoundKernel, PendingResult, bind
 from palladium_amd.emit import emit_hip, emit_jaxpr, rule
+from palladium_amd.dtypes import name as _dtype_name
 from palladium_amd.emit.core import CTYPES as _CTYPES
 from palladium_amd.errors import (
     CompileError,
@@ -73,7 +74,7 @@ def _check_dtypes(args: tuple) -> None:
     the message (reference: `src/palladium/__init__.py:58-80`)."""
     for i, a in enumerate(args):
         dtype = getattr(a, "dtype", None)
-        name = np.dtype(dtype if dtype is not None else np.asarray(a).dtype).name
+        name = _dtype_name(dtype if dtype is not None else np.asarray(a).dtype)
         if name not in _CTYPES:
             hint = (
                 "; float64 usually means jax_enable_x64 is on, disable it or cast to float32"

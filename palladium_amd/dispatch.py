@@ -29,6 +29,7 @@ from typing import Any
 import numpy as np
 
 from palladium_amd import runtime as rt
+from palladium_amd.dtypes import name as _dtype_name
 from palladium_amd.emit.core import LaunchGeometry, launch_geometry
 from palladium_amd.errors import CompileError, DispatchError
 from palladium_amd.trace import KernelSpec
@@ -133,7 +134,8 @@ class BoundKernel:
             arr = np.asarray(a)
             if arr.dtype != info.dtype:
                 raise DispatchError(
-                    f"argument {i}: dtype {arr.dtype} does not match the traced {info.dtype}; cast explicitly"
+                    f"argument {i}: dtype {_dtype_name(arr.dtype)} does not match the traced "
+                    f"{_dtype_name(info.dtype)}; cast explicitly"
                 )
             if arr.shape != info.array_shape:
                 raise DispatchError(f"argument {i}: expected shape {info.array_shape}, got {arr.shape}")
@@ -215,7 +217,9 @@ class BoundKernel:
         for i, (o, info) in enumerate(zip(operands, infos)):
             b = o if isinstance(o, rt.Buffer) else rt.Buffer.wrap(o)
             if b.dtype != info.dtype:
-                raise DispatchError(f"operand {i}: dtype {b.dtype} does not match the traced {info.dtype}")
+                raise DispatchError(
+                    f"operand {i}: dtype {_dtype_name(b.dtype)} does not match the traced {_dtype_name(info.dtype)}"
+                )
             if b.shape != tuple(info.array_shape):
                 raise DispatchError(f"operand {i}: expected shape {info.array_shape}, got {b.shape}")
             ptrs.append(b.ptr)

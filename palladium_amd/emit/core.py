@@ -32,6 +32,8 @@ from typing import Any
 
 import numpy as np
 
+from palladium_amd.dtypes import is_bf16, scalar_f32
+from palladium_amd.dtypes import name as dtype_name
 from palladium_amd.errors import EmitError, UnsupportedPrimitiveError
 from palladium_amd.ir import Jaxpr, JaxprEqn, KeyAval, Literal, NDIndexer, Slice, Var
 from palladium_amd.runtime import math_mode_ordinal
@@ -56,6 +58,7 @@ PRIMITIVE_INVARS = string.ascii_lowercase[:MAX_PRIMITIVE_ARITY]
 CTYPES = {
     "float32": "float",
     "float16": "_Float16",
+    "bfloat16": "__bf16",
     "int32": "int",
     "uint32": "unsigned int",
     "bool": "bool",
@@ -71,7 +74,7 @@ NUM_XCDS = 8
 
 
 def ctype_of(dtype: Any) -> str:
-    name = np.dtype(dtype).name
+    name = dtype_name(dtype)
     c = CTYPES.get(name)
     if c is None:
         raise EmitError(f"dtype {name} has no HIP lowering (supported: {', '.join(CTYPES)})")
@@ -208,10 +211,12 @@ def format_float(v: float) -> str:
 def literal_cval(v: Any, dtype: Any) -> CVal:
     dt = np.dtype(dtype)
     ctype = ctype_of(dt)
-    if dt.kind == "f":
-        # Round to the literal's own type first: a float16 literal is emitted
-        # as the float32 spelling of its float16 value (exact), so mixed
-        # expressions round exactly as float16 arithmetic would.
+    if is_bf16(dt):
+        expr = format_float(scalar_f32(v))
+    elif dt.kind == "f":
+        # Round to the literal's own type first: a float16 (or bfloat16)
+        # literal is emitted as the float32 spelling of its value (exact), so
+        # mixed expressions round exactly as the narrow arithmetic would.
         expr = format_float(float(np.asarray(v, dt)))
     elif dt.kind == "b":
         expr = "true" if v else "false"

@@ -37,14 +37,28 @@ from palladium_amd.ir import JaxprEqn, KeyAval, Literal, Var
 
 F32 = "float"
 F16 = "_Float16"
-FLOAT_CTYPES = (F32, F16)
+BF16 = "__bf16"
+FLOAT_CTYPES = (F32, F16, BF16)
 
 
 def _is_float(c: CVal) -> bool:
-    """float32 and float16 share every template: float16 operands promote to
-    float in the float functions, and assigning the result to a float16
-    variable rounds it once."""
+    """float32, float16 and bfloat16 share every template: narrow operands
+    promote to float in the float functions, and assigning the result to a
+    narrow variable rounds it once. bfloat16 operands are widened explicitly
+    (`(float)x`), so a template evaluates wholly in float32 whatever the
+    compiler's bf16 excess-precision setting."""
     return c.ctype in FLOAT_CTYPES
+
+
+def _acc_ctype(ctype: str) -> str:
+    """Accumulator type of reductions and contractions: bfloat16 sums and
+    dot products accumulate in float32 and round once, as XLA's CPU backend
+    computes bf16 reductions; other types accumulate in their own type."""
+    return F32 if ctype == BF16 else ctype
+
+
+def _operand(expr: str, src_ctype: str) -> str:
+    return f"((float){expr})" if src_ctype == BF16 else expr
 
 
 # ---------------------------------------------------------------------------
@@ -176,6 +190,10 @@ def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
         template = f"(({dst_ctype}){{a}})"
         if dst_ctype == "bool":
             template = "({a} != 0)"
+        elif dst_ctype == BF16 and ops[0].ctype not in (F32, BF16):
+            # integers and float16 reach bfloat16 through float32 (one rule
+            # for device and interpreter)
+            template = f"(({BF16})(float){{a}})"
     elif opname == "bitcast_convert_type":
         template = f"__builtin_bit_cast({dst_ctype}, {{a}})"
     elif opname == "select_n":
@@ -199,16 +217,20 @@ def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     n_fields = len({f for f in PRIMITIVE_INVARS if "{" + f + "}" in template})
     if n_fields != len(ops):
         raise EmitError(f"{opname} requires {n_fields} operands, got {len(ops)}")
+    widen = opname != "bitcast_convert_type"
+
+    def operand(o: CVal, e: str) -> str:
+        return _operand(e, o.ctype) if widen else e
 
     dst_shape = tuple(int(d) for d in out.aval.shape)
     if math.prod(dst_shape) == 1:
-        expr = template.format(**{n: o.at("0") for n, o in zip(PRIMITIVE_INVARS, ops)})
+        expr = template.format(**{n: operand(o, o.at("0")) for n, o in zip(PRIMITIVE_INVARS, ops)})
         declare(env, cursor, out, init=expr)
         return
     dst = declare(env, cursor, out)
 
     def body(idx_vars: list[str], flat: str) -> None:
-        vals = {n: o.at(_op_index(o, dst_shape, idx_vars)) for n, o in zip(PRIMITIVE_INVARS, ops)}
+        vals = {n: operand(o, o.at(_op_index(o, dst_shape, idx_vars))) for n, o in zip(PRIMITIVE_INVARS, ops)}
         cursor.emit(f"{dst.at(flat)} = {template.format(**vals)};")
 
     _emit_elementwise_loops(cursor, dst, body)
@@ -391,15 +413,17 @@ def _rule_dot_general(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     scalar_out = m * n == 1
     dst = None if scalar_out else declare(env, cursor, out)
 
+    act = _acc_ctype(ctype)
+
     def conv(expr: str, src: CVal) -> str:
-        return expr if src.ctype == ctype else f"(({ctype}){expr})"
+        return expr if src.ctype == act else f"(({act}){expr})"
 
     def term(idx: list[tuple[str, int]]) -> str:
         return flat_index([(v, st) for v, st in idx if v != "0"])
 
     def contraction(i: str, j: str) -> str:
         acc = cursor.fresh("_acc")
-        cursor.emit(f"{ctype} {acc} = ({ctype})0;")
+        cursor.emit(f"{act} {acc} = ({act})0;")
 
         def step(kk: str) -> None:
             li = term(([(i, ls[lfree[0]])] if lfree else []) + [(kk, ls[lcd])])
@@ -416,7 +440,11 @@ def _rule_dot_general(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
         return acc
 
     if scalar_out:
-        env.bind(out, CVal(contraction("0", "0"), tuple(int(d) for d in out.aval.shape), ctype))
+        acc = contraction("0", "0")
+        if act != ctype:
+            declare(env, cursor, out, init=f"(({ctype}){acc})")
+        else:
+            env.bind(out, CVal(acc, tuple(int(d) for d in out.aval.shape), ctype))
         return
 
     def rows(i: str) -> None:
@@ -584,23 +612,27 @@ def _emit_reduce(env: Environment, cursor: Cursor, eqn: JaxprEqn, init: str, com
 
     result = {}
 
+    act = _acc_ctype(ctype)
+
     def accumulate() -> None:
         acc = cursor.fresh("_acc")
-        cursor.emit(f"{ctype} {acc} = {init};")
+        cursor.emit(f"{act} {acc} = {init};")
 
         def inner() -> None:
             sidx = flat_index([(idx[d], s_strides[d]) for d in range(rank)])
-            cursor.emit(f"{acc} = {combine(acc, src.at(sidx))};")
+            cursor.emit(f"{acc} = {combine(acc, _operand(src.at(sidx), src.ctype))};")
 
         loops(red, inner)
-        if scalar_out:
+        if scalar_out and act != ctype:
+            result["acc"] = declare(env, cursor, out, init=f"(({ctype}){acc})").expr
+        elif scalar_out:
             result["acc"] = acc
         else:
             didx = flat_index([(idx[d], d_strides[i]) for i, d in enumerate(kept)])
             cursor.emit(f"{dst.at(didx)} = {acc};")
 
     loops(kept, accumulate)
-    if scalar_out:
+    if scalar_out and act == ctype:
         env.bind(out, CVal(result["acc"], out_shape, ctype))
 
 
@@ -609,10 +641,12 @@ def _reduce_init(eqn: JaxprEqn, kind: str) -> str:
     if kind == "sum":
         return "0.0f" if ct in FLOAT_CTYPES else "0"
     if kind == "max":
-        return {"float": "(-__builtin_inff())", F16: "(-__builtin_inff())", "int": "(-2147483647 - 1)",
+        return {"float": "(-__builtin_inff())", F16: "(-__builtin_inff())", BF16: "(-__builtin_inff())",
+                "int": "(-2147483647 - 1)",
                 "unsigned int": "0u", "bool": "false"}[ct]
     if kind == "min":
-        return {"float": "__builtin_inff()", F16: "__builtin_inff()", "int": "2147483647",
+        return {"float": "__builtin_inff()", F16: "__builtin_inff()", BF16: "__builtin_inff()",
+                "int": "2147483647",
                 "unsigned int": "0xFFFFFFFFu", "bool": "true"}[ct]
     return {"or": "false", "and": "true"}[kind]
 
@@ -831,7 +865,8 @@ def _rule_iota(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     dst = declare(env, cursor, out)
 
     def body(idx_vars: list[str], flat: str) -> None:
-        cursor.emit(f"{dst.at(flat)} = ({ct}){idx_vars[dim]};")
+        via = "(float)" if ct == BF16 else ""
+        cursor.emit(f"{dst.at(flat)} = ({ct}){via}{idx_vars[dim]};")
 
     _emit_elementwise_loops(cursor, dst, body)
 
@@ -858,7 +893,7 @@ def _rule_lane_reduce(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     is_bool = ct == "bool"
     # Shuffles move 32-bit values: bools travel as int, float16 as float
     # (a float16 sum is then accumulated in float32 and rounded once).
-    wt = "int" if is_bool else (F32 if ct == F16 else ct)
+    wt = "int" if is_bool else (F32 if ct in (F16, BF16) else ct)
     isf = ct in FLOAT_CTYPES
     comb = {
         "sum": lambda a, b: f"({a} + {b})",

@@ -24,6 +24,8 @@ from typing import Any
 
 import numpy as np
 
+from palladium_amd.dtypes import name as _dtype_name
+
 from palladium_amd.diagnostics import KernelDiagnostics, explain_spec, log_compile
 from palladium_amd.emit import emit_hip, launch_geometry
 from palladium_amd.runtime import MathMode, math_mode_ordinal
@@ -106,7 +108,7 @@ class FfiCallable:
         return explain_spec(trace(self._staged, *args), self._threadgroup, self._math_mode, compile=compile)
 
     def spec_and_source(self, args: tuple) -> tuple[KernelSpec, str]:
-        key = tuple((tuple(a.shape), np.dtype(a.dtype).str) for a in args)
+        key = tuple((tuple(a.shape), _dtype_name(a.dtype)) for a in args)
         entry = self._cache.get(key)
         if entry is None:
             with self._lock:

@@ -21,6 +21,7 @@ from typing import Any, Iterator
 
 import numpy as np
 
+from palladium_amd import dtypes as _dtypes
 from palladium_amd.errors import TraceError
 from palladium_amd.ir import (
     ClosedJaxpr,
@@ -40,8 +41,9 @@ U32 = np.dtype(np.uint32)
 BOOL = np.dtype(np.bool_)
 
 F16 = np.dtype(np.float16)
+BF16 = _dtypes.bfloat16
 
-SUPPORTED_DTYPES = (F32, F16, I32, U32, BOOL)
+SUPPORTED_DTYPES = (F32, F16, BF16, I32, U32, BOOL)
 
 _state = threading.local()
 
@@ -129,8 +131,12 @@ def building(builder: Builder) -> Iterator[Builder]:
 
 def literal(value: Any, dtype: Any, weak: bool = True) -> Literal:
     dtype = np.dtype(dtype)
+    if isinstance(value, np.ndarray) and _dtypes.is_bf16(value.dtype):
+        value = float(_dtypes.to_float(value).reshape(()))
     if dtype == BOOL:
         val: Any = bool(value)
+    elif _dtypes.is_bf16(dtype):
+        val = _dtypes.scalar_f32(value)
     elif dtype.kind == "f":
         val = float(np.asarray(value, dtype=dtype))
     elif dtype.kind in "iu":
@@ -276,8 +282,8 @@ def check_dtype(dtype: Any) -> np.dtype:
     dt = np.dtype(dtype)
     if dt not in SUPPORTED_DTYPES:
         raise TraceError(
-            f"dtype {dt.name} is not supported in kernels "
-            f"(supported: {', '.join(d.name for d in SUPPORTED_DTYPES)})"
+            f"dtype {_dtypes.name(dt)} is not supported in kernels "
+            f"(supported: {', '.join(_dtypes.name(d) for d in SUPPORTED_DTYPES)})"
         )
     return dt
 

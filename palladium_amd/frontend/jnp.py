@@ -29,10 +29,13 @@ from palladium_amd.frontend.core import (
     literal,
     scalar_kind,
 )
+from palladium_amd.dtypes import bfloat16_type as _bfloat16_type
+from palladium_amd.dtypes import kind as _kind
 from palladium_amd.ir import KeyAval, Literal, ShapedArray
 
 float32 = np.float32
 float16 = np.float16
+bfloat16 = _bfloat16_type
 int32 = np.int32
 uint32 = np.uint32
 bool_ = np.bool_
@@ -78,22 +81,22 @@ def _result_dtype(args: Sequence[Any]) -> np.dtype:
         dt = strong[0]
         for d in strong[1:]:
             if d != dt:
-                if d.kind == "f" and dt.kind == "f":
+                if _kind(d) == "f" and _kind(dt) == "f":
                     dt = F32  # float16 with float32
-                elif d.kind == "f" or dt.kind == "f":
-                    dt = d if d.kind == "f" else dt
+                elif _kind(d) == "f" or _kind(dt) == "f":
+                    dt = d if _kind(d) == "f" else dt
                 elif {d, dt} <= {I32, U32, BOOL}:
                     dt = I32 if BOOL in (d, dt) and U32 not in (d, dt) else (U32 if U32 in (d, dt) and BOOL in (d, dt) else I32)
                 else:
                     raise TraceError(f"cannot mix dtypes {dt} and {d}; cast explicitly")
         # A weak float meeting a strong int promotes to float (JAX semantics).
-        if dt.kind in "iub" and builtins.any(w.kind == "f" for w in weak):
+        if _kind(dt) in "iub" and builtins.any(_kind(w) == "f" for w in weak):
             return F32
-        if dt == BOOL and builtins.any(w.kind in "iu" for w in weak):
+        if dt == BOOL and builtins.any(_kind(w) in "iu" for w in weak):
             return I32
         return dt
-    best = builtins.max(weak, key=lambda d: kinds.index(d.kind))
-    return {"f": F32, "i": I32, "u": U32, "b": BOOL}[best.kind]
+    best = builtins.max(weak, key=lambda d: kinds.index(_kind(d)))
+    return {"f": F32, "i": I32, "u": U32, "b": BOOL}[_kind(best)]
 
 
 def _as_operand(x: Any, dtype: np.dtype, shape: tuple[int, ...]) -> Any:
@@ -134,7 +137,7 @@ def _nary(name: str, *args: Any, out_dtype: np.dtype | None = None, **params: An
 def _unary(name: str, x: Any, float_only: bool = False, **params: Any) -> Tracer:
     if not isinstance(x, Tracer):
         x = full((), x, dtype=default_dtype(x))
-    if float_only and x.dtype.kind != "f":
+    if float_only and _kind(x.dtype) != "f":
         x = convert_element_type(x, F32)
     return _stage(name, [x], x.shape, x.dtype, x.weak_type, **params)
 
@@ -315,7 +318,7 @@ def maximum(a, b): return _nary("max", a, b)
 
 def divide(a: Any, b: Any) -> Tracer:
     dt = _result_dtype((a, b))
-    if dt.kind != "f":
+    if _kind(dt) != "f":
         a = convert_element_type(a, F32) if isinstance(a, Tracer) else float(a)
         b = convert_element_type(b, F32) if isinstance(b, Tracer) else float(b)
     return _nary("div", a, b)
@@ -326,7 +329,7 @@ true_divide = divide
 
 def floor_divide(a: Any, b: Any) -> Tracer:
     dt = _result_dtype((a, b))
-    if dt.kind == "f":
+    if _kind(dt) == "f":
         return floor(divide(a, b))
     q = _nary("div", a, b)
     r = _nary("rem", a, b)
@@ -392,7 +395,7 @@ def not_equal(a, b): return _nary("ne", a, b, out_dtype=BOOL)
 
 def _int_or_bool(name: str, a: Any, b: Any) -> Tracer:
     dt = _result_dtype((a, b))
-    if dt.kind == "f":
+    if _kind(dt) == "f":
         raise TraceError(f"{name} requires integer or bool operands")
     return _nary(name, a, b)
 
@@ -406,7 +409,7 @@ logical_xor = bitwise_xor
 
 
 def invert(x: Tracer) -> Tracer:
-    if x.dtype.kind == "f":
+    if _kind(x.dtype) == "f":
         raise TraceError("~ requires an integer or bool operand")
     return _unary("not", x)
 
@@ -519,7 +522,7 @@ def all(x: Tracer, axis: Any = None, keepdims: bool = False) -> Tracer:  # noqa:
 def mean(x: Tracer, axis: Any = None, keepdims: bool = False) -> Tracer:
     """Sum, then divide by the reduced element count (integers promote to
     float32, as in JAX)."""
-    if x.dtype.kind != "f":
+    if _kind(x.dtype) != "f":
         x = convert_element_type(x, F32)
     s = _reduce("reduce_sum", x, axis, keepdims=keepdims)
     n = x.size // builtins.max(s.size, 1)

@@ -16,6 +16,7 @@ from typing import Any, Callable, Sequence
 
 import numpy as np
 
+from palladium_amd.dtypes import name as _dtype_name
 from palladium_amd.errors import TraceError
 from palladium_amd.frontend import jnp
 from palladium_amd.frontend.core import (
@@ -163,7 +164,7 @@ def _match_carry(outs: list[Any], avals: list[ShapedArray], what: str) -> tuple[
             if oa.weak_type:
                 new.append(a)
                 continue
-            raise TraceError(f"{what}: carry dtype changed from {a.dtype} to {oa.dtype}")
+            raise TraceError(f"{what}: carry dtype changed from {_dtype_name(a.dtype)} to {_dtype_name(oa.dtype)}")
         if a.weak_type and not oa.weak_type:
             new.append(ShapedArray(a.shape, a.dtype, False))
             changed = True

@@ -13,7 +13,10 @@ in lockstep; `while` masks finished instances (their stores are
 suppressed), `cond` evaluates each branch under its instance mask.
 Arithmetic is NumPy's, in the kernel's dtypes (fp32 ops are IEEE; libm-style
 functions may differ from the device by an ulp); `min`/`max` on floats are
-NaN-suppressing `fmin`/`fmax`, matching the emitted code.
+NaN-suppressing `fmin`/`fmax`, matching the emitted code. bfloat16 values
+are carried as float32 arrays: each operation is evaluated in float32 and
+rounded to bfloat16 (ties to even), and bfloat16 sums and contractions
+accumulate in float32 in the emitted order and round once.
 """
 
 from __future__ import annotations
@@ -24,6 +27,7 @@ from typing import Any
 
 import numpy as np
 
+from palladium_amd.dtypes import bits_from_f32, f32_from_bits, from_float, is_bf16, round_f32, to_float
 from palladium_amd.emit.core import check_contiguous
 from palladium_amd.errors import EmitError, UnsupportedPrimitiveError
 from palladium_amd.ir import Jaxpr, JaxprEqn, KeyAval, Literal, Slice, Var
@@ -108,6 +112,8 @@ class _Env:
 
     def read(self, atom: Any) -> Any:
         if isinstance(atom, Literal):
+            if is_bf16(atom.aval.dtype):
+                return round_f32(np.float32(atom.val))
             return np.asarray(atom.val, dtype=atom.aval.dtype)
         return self.vals[atom]
 
@@ -132,7 +138,8 @@ def _round_half_away(x):
 
 def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
     out_aval = eqn.outvars[0].aval
-    dt = np.dtype(out_aval.dtype)
+    bf_out = is_bf16(out_aval.dtype)
+    dt = np.dtype(np.float32) if bf_out else np.dtype(out_aval.dtype)
     rank = len(out_aval.shape)
     ops = [_align(o, rank, n) for o in ops]
     a = ops[0] if ops else None
@@ -217,12 +224,19 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
         elif name == "convert_element_type":
             r = (np.asarray(a) != 0) if dt == np.bool_ else np.asarray(a).astype(dt)
         elif name == "bitcast_convert_type":
-            r = np.ascontiguousarray(np.asarray(a)).view(dt)
+            if bf_out:  # float16 bits -> bfloat16
+                r = f32_from_bits(np.ascontiguousarray(np.asarray(a)).view(np.uint16))
+            elif is_bf16(eqn.invars[0].aval.dtype):  # bfloat16 bits -> float16
+                r = bits_from_f32(a).view(dt)
+            else:
+                r = np.ascontiguousarray(np.asarray(a)).view(dt)
         else:
             raise UnsupportedPrimitiveError(f"interpreter has no rule for primitive '{name}'")
     r = np.asarray(r)
     if r.dtype != dt:
         r = r.astype(dt)
+    if bf_out:
+        r = round_f32(r)
     full = (n,) + tuple(out_aval.shape)
     if r.shape != full:
         r = np.broadcast_to(r, full).copy()
@@ -270,7 +284,9 @@ def _eval(jaxpr: Jaxpr, env: _Env, invals: list[Any], mask: np.ndarray) -> list[
         elif name == "iota":
             shape = tuple(eqn.params["shape"])
             dim = int(eqn.params["dimension"])
-            r = np.arange(shape[dim], dtype=eqn.outvars[0].aval.dtype).reshape([-1 if k == dim else 1 for k in range(len(shape))])
+            bf = is_bf16(eqn.outvars[0].aval.dtype)
+            r = np.arange(shape[dim], dtype=np.float32 if bf else eqn.outvars[0].aval.dtype)
+            r = (round_f32(r) if bf else r).reshape([-1 if k == dim else 1 for k in range(len(shape))])
             env.write(eqn.outvars[0], np.broadcast_to(r, (n,) + shape).copy())
         elif name == "program_id":
             env.write(eqn.outvars[0], env.pids[int(eqn.params["axis"])])
@@ -302,13 +318,17 @@ def _eval(jaxpr: Jaxpr, env: _Env, invals: list[Any], mask: np.ndarray) -> list[
             src = np.asarray(env.read(eqn.invars[0]))
             axes = tuple(int(a) + 1 for a in eqn.params["axes"])
             f = {"reduce_sum": np.sum, "reduce_or": np.any, "reduce_and": np.all}.get(name)
+            bf = is_bf16(eqn.outvars[0].aval.dtype)
             if name == "reduce_max":
                 r = np.fmax.reduce(src, axis=axes) if src.dtype.kind == "f" else np.max(src, axis=axes)
             elif name == "reduce_min":
                 r = np.fmin.reduce(src, axis=axes) if src.dtype.kind == "f" else np.min(src, axis=axes)
+            elif name == "reduce_sum" and bf:
+                r = _ordered_sum(src, axes)
             else:
                 r = f(src, axis=axes)
-            env.write(eqn.outvars[0], np.asarray(r).astype(eqn.outvars[0].aval.dtype))
+            r = round_f32(r) if bf else np.asarray(r).astype(eqn.outvars[0].aval.dtype)
+            env.write(eqn.outvars[0], r)
         elif name in ("random_wrap", "random_unwrap"):
             env.write(eqn.outvars[0], np.asarray(env.read(eqn.invars[0])).reshape(n, 2))
         elif name == "random_fold_in":
@@ -349,11 +369,26 @@ def _eval(jaxpr: Jaxpr, env: _Env, invals: list[Any], mask: np.ndarray) -> list[
     return [env.read(v) for v in jaxpr.outvars]
 
 
+def _ordered_sum(src: np.ndarray, axes: tuple[int, ...]) -> np.ndarray:
+    """float32 sum over `axes` in row-major order of the reduced indices,
+    one add at a time (the emitter's accumulation order)."""
+    src = np.asarray(src, np.float32)
+    kept = [d for d in range(src.ndim) if d not in axes]
+    moved = np.transpose(src, kept + list(axes))
+    flat = moved.reshape(moved.shape[: len(kept)] + (-1,))
+    acc = np.zeros(flat.shape[:-1], np.float32)
+    for r in range(flat.shape[-1]):
+        acc = acc + flat[..., r]
+    return acc
+
+
 def _dot_general(eqn: JaxprEqn, lhs: Any, rhs: Any, n: int) -> np.ndarray:
     """Contraction accumulated in k order from zero in the output dtype,
-    `acc = acc + a*b`, the operation sequence the emitter produces."""
+    `acc = acc + a*b`, the operation sequence the emitter produces
+    (bfloat16: accumulated in float32, rounded once)."""
     (lc, rc), _ = eqn.params["dimension_numbers"]
-    out_dt = np.dtype(eqn.outvars[0].aval.dtype)
+    bf = is_bf16(eqn.outvars[0].aval.dtype)
+    out_dt = np.dtype(np.float32) if bf else np.dtype(eqn.outvars[0].aval.dtype)
     la, ra = eqn.invars[0].aval, eqn.invars[1].aval
     lhs = np.broadcast_to(np.asarray(lhs), (n,) + tuple(la.shape)).astype(out_dt)
     rhs = np.broadcast_to(np.asarray(rhs), (n,) + tuple(ra.shape)).astype(out_dt)
@@ -367,6 +402,8 @@ def _dot_general(eqn: JaxprEqn, lhs: Any, rhs: Any, n: int) -> np.ndarray:
     with np.errstate(all="ignore"):
         for kk in range(a.shape[-1]):
             acc = acc + a[..., kk] * b[..., kk]
+    if bf:
+        acc = round_f32(acc)
     return acc.reshape((n,) + tuple(m_shape) + tuple(r_shape))
 
 
@@ -519,13 +556,16 @@ def interpret_spec(spec: KernelSpec, *arrays: np.ndarray) -> tuple[np.ndarray, .
             # block with copies of the last row, drop its outputs after.
             shape = (spec.grid[0] * info.block_shape[0],) + shape[1:]
             info = dataclasses.replace(info, array_shape=shape)
+        bf = is_bf16(info.dtype)
         if k < len(spec.inputs):
             arr = np.ascontiguousarray(arrays[k], dtype=info.dtype)
+            if bf:
+                arr = to_float(arr)
             if arr.shape != shape:
                 arr = np.pad(arr, [(0, shape[0] - arr.shape[0])] + [(0, 0)] * (arr.ndim - 1), mode="edge")
             flat = arr.reshape(-1).copy()
         else:
-            flat = np.zeros(math.prod(shape), info.dtype)
+            flat = np.zeros(math.prod(shape), np.float32 if bf else info.dtype)
             outs.append(flat)
         check_contiguous(info, f"operand {k}")
         bshape = tuple(info.block_shape) or (1,)
@@ -533,7 +573,15 @@ def interpret_spec(spec: KernelSpec, *arrays: np.ndarray) -> tuple[np.ndarray, .
         refs.append(_Ref(flat, block_offsets(spec, info, pids), bshape, strides, k < len(spec.inputs)))
     env = _Env(n, pids, tuple(spec.grid))
     _eval(spec.jaxpr, env, refs, np.ones(n, bool))
-    return tuple(o[: math.prod(info.array_shape)].reshape(info.array_shape) for o, info in zip(outs, spec.outputs))
+    return tuple(
+        _to_storage(o[: math.prod(info.array_shape)].reshape(info.array_shape), info.dtype)
+        for o, info in zip(outs, spec.outputs)
+    )
+
+
+def _to_storage(a: np.ndarray, dtype: Any) -> np.ndarray:
+    """bfloat16 values are carried as float32 inside the interpreter."""
+    return from_float(a) if is_bf16(dtype) else a
 
 
 def interpret_call(call: Any, *args: Any) -> Any:

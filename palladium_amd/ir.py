@@ -23,6 +23,8 @@ from typing import Any
 
 import numpy as np
 
+from palladium_amd.dtypes import name as _dtype_name
+
 __all__ = [
     "ClosedJaxpr",
     "IndexerTree",
@@ -88,7 +90,8 @@ class ShapedArray:
         return hash((self.shape, self.dtype))
 
     def str_short(self) -> str:
-        name = _SHORT.get(self.dtype.name, self.dtype.name)
+        dn = _dtype_name(self.dtype)
+        name = _SHORT.get(dn, dn)
         return f"{name}[{','.join(str(d) for d in self.shape)}]"
 
     __repr__ = str_short

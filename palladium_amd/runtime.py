@@ -21,6 +21,8 @@ from typing import Any, Sequence
 
 import numpy as np
 
+from palladium_amd import dtypes as _dtypes
+
 from palladium_amd.errors import CompileError, PalladiumError
 
 __all__ = [
@@ -339,7 +341,8 @@ class Buffer:
         if hasattr(obj, "data_ptr") and getattr(obj, "is_cuda", False):
             if not obj.is_contiguous():
                 raise ValueError("device tensors must be contiguous")
-            dt = np.dtype(str(obj.dtype).replace("torch.", ""))
+            tname = str(obj.dtype).replace("torch.", "")
+            dt = _dtypes.bfloat16 if tname == "bfloat16" else np.dtype(tname)
             return cls(tuple(obj.shape), dt, ptr=obj.data_ptr(), owner=obj)
         cai = getattr(obj, "__cuda_array_interface__", None)
         if cai is not None:

@@ -3,7 +3,9 @@ under SAFE math against the NumPy interpreter (`.interpret`). Only IEEE
 operations are generated (+ - * / fmin fmax abs neg select), so results
 must agree bit for bit. Programs mix expression trees, fori_loops with
 permuted carries, switch and bounded while loops (after the reference's
-tests/test_fuzz_emitter.py grammar)."""
+tests/test_fuzz_emitter.py grammar). The same programs run in bfloat16,
+where each operation is evaluated in float32 and rounded to bfloat16 on
+both sides."""
 
 import os
 
@@ -11,6 +13,7 @@ import numpy as np
 import pytest
 
 import palladium_amd as pa
+from palladium_amd import dtypes
 from palladium_amd.frontend import jnp, lax, pl
 
 pytestmark = pytest.mark.gpu
@@ -43,28 +46,30 @@ def _expr(rng, leaves, depth):
     return jnp.clip(a, -4.0, 4.0)
 
 
-def _tame(v):
-    return jnp.broadcast_to(jnp.clip(v, -100.0, 100.0), (1,))
+def _tame(v, dt=F):
+    v = jnp.clip(v, -100.0, 100.0)
+    return jnp.broadcast_to(v if v.dtype == dt else v.astype(dt), (1,))
 
 
 def _make_kernel(seed):
     def kernel(x_ref, y_ref, o_ref, p_ref):
         rng = np.random.default_rng(seed)
         x, y = x_ref[...], y_ref[...]
-        v = _tame(_expr(rng, [x, y], 4))
+        dt = x.dtype
+        v = _tame(_expr(rng, [x, y], 4), dt)
 
         def body(i, c):
             a, b, c3 = c
             r = np.random.default_rng(seed + 1)
-            na = _tame(_expr(r, [a, b, c3], 3))
+            na = _tame(_expr(r, [a, b, c3], 3), dt)
             return (b, c3, na) if seed % 2 else (na, a, b)  # permuted carries
 
         a, b, c = lax.fori_loop(0, 5 + seed % 7, body, (v, x, y))
         k = lax.switch(pl.program_id(0) % 3, [lambda t: t * 2.0, lambda t: t - 1.0, lambda t: jnp.abs(t)], a)
         n, w = lax.while_loop(lambda s: jnp.logical_and(s[0] < 3 + pl.program_id(0) % 4, s[1] < 50.0),
                               lambda s: (s[0] + 1, s[1] * 1.5 + 1.0), (0, jnp.abs(b)))
-        o_ref[...] = _tame(k + c * 0.5)
-        p_ref[...] = w + n.astype(jnp.float32)
+        o_ref[...] = _tame(k + c * 0.5, dt)
+        p_ref[...] = w + n.astype(x.dtype)
 
     return kernel
 
@@ -82,3 +87,18 @@ def test_random_program_bit_exact_vs_interpreter(seed):
     want = call.interpret(x, y)
     for g, w in zip(got, want):
         np.testing.assert_array_equal(g, w)
+
+
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+def test_random_program_bf16_bit_exact_vs_interpreter(seed):
+    n = 300
+    rng = np.random.default_rng(200 + seed)
+    x = dtypes.from_float(rng.uniform(-3, 3, n).astype(F))
+    y = dtypes.from_float(rng.uniform(-3, 3, n).astype(F))
+    spec = pl.BlockSpec((1,), lambda i: (i,))
+    call = pa.hip_call(_make_kernel(seed), grid=(n,), in_specs=[spec, spec], out_specs=(spec, spec),
+                       out_shape=(pl.ShapeDtypeStruct((n,), dtypes.bfloat16),) * 2, math_mode="safe")
+    got = call(x, y)
+    want = call.interpret(x, y)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(dtypes.as_bits(g), dtypes.as_bits(w))
