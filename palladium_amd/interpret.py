@@ -16,7 +16,8 @@ functions may differ from the device by an ulp); `min`/`max` on floats are
 NaN-suppressing `fmin`/`fmax`, matching the emitted code. bfloat16 values
 are carried as float32 arrays: each operation is evaluated in float32 and
 rounded to bfloat16 (ties to even), and bfloat16 sums and contractions
-accumulate in float32 in the emitted order and round once.
+accumulate in float32 and round once. Float sums add one element at a time
+in the emitted order (row-major over the reduced indices).
 """
 
 from __future__ import annotations
@@ -323,8 +324,8 @@ def _eval(jaxpr: Jaxpr, env: _Env, invals: list[Any], mask: np.ndarray) -> list[
                 r = np.fmax.reduce(src, axis=axes) if src.dtype.kind == "f" else np.max(src, axis=axes)
             elif name == "reduce_min":
                 r = np.fmin.reduce(src, axis=axes) if src.dtype.kind == "f" else np.min(src, axis=axes)
-            elif name == "reduce_sum" and bf:
-                r = _ordered_sum(src, axes)
+            elif name == "reduce_sum" and (bf or src.dtype.kind == "f"):
+                r = _ordered_sum(src, axes, np.float32 if bf else src.dtype)
             else:
                 r = f(src, axis=axes)
             r = round_f32(r) if bf else np.asarray(r).astype(eqn.outvars[0].aval.dtype)
@@ -369,14 +370,15 @@ def _eval(jaxpr: Jaxpr, env: _Env, invals: list[Any], mask: np.ndarray) -> list[
     return [env.read(v) for v in jaxpr.outvars]
 
 
-def _ordered_sum(src: np.ndarray, axes: tuple[int, ...]) -> np.ndarray:
-    """float32 sum over `axes` in row-major order of the reduced indices,
-    one add at a time (the emitter's accumulation order)."""
-    src = np.asarray(src, np.float32)
+def _ordered_sum(src: np.ndarray, axes: tuple[int, ...], acc_dtype: Any) -> np.ndarray:
+    """Sum over `axes` in row-major order of the reduced indices, one add
+    at a time in `acc_dtype` (the emitter's accumulation order; NumPy's own
+    sum is pairwise)."""
+    src = np.asarray(src, acc_dtype)
     kept = [d for d in range(src.ndim) if d not in axes]
     moved = np.transpose(src, kept + list(axes))
     flat = moved.reshape(moved.shape[: len(kept)] + (-1,))
-    acc = np.zeros(flat.shape[:-1], np.float32)
+    acc = np.zeros(flat.shape[:-1], acc_dtype)
     for r in range(flat.shape[-1]):
         acc = acc + flat[..., r]
     return acc

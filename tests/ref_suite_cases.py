@@ -6,6 +6,7 @@ and GPU tests."""
 import numpy as np
 
 import palladium_amd as pa
+from palladium_amd import dtypes
 from palladium_amd.frontend import jnp, lax, pl
 
 F = np.float32
@@ -101,6 +102,17 @@ def _np_softmax(v):
     return e / e.sum(-1, keepdims=True)
 
 
+def bf16_matmul(m, k, n):
+    def kernel(a_ref, b_ref, o_ref):
+        o_ref[...] = jnp.dot(a_ref[...], b_ref[...])
+
+    r = _rng()
+    a = dtypes.from_float(r.standard_normal((m, k)).astype(F))
+    b = dtypes.from_float(r.standard_normal((k, n)).astype(F))
+    return (kernel, pl.ShapeDtypeStruct((m, n), dtypes.bfloat16), (a, b),
+            lambda a, b: dtypes.to_float(a).astype(np.float64) @ dtypes.to_float(b))
+
+
 def dtype_case(name):
     """Round trip + one op per dtype (reference test_17_robustness.py:85-140)."""
     r = _rng()
@@ -113,6 +125,10 @@ def dtype_case(name):
         "float16_sum": (r.standard_normal(16).astype(np.float16), lambda v: jnp.sum(v, keepdims=True),
                         lambda v: np.sum(v.astype(np.float64), keepdims=True)),
         "int32_sum": (np.arange(16, dtype=np.int32), lambda v: jnp.sum(v, keepdims=True), lambda v: np.sum(v, keepdims=True)),
+        "bfloat16": (dtypes.from_float(r.standard_normal(16).astype(np.float32)), lambda v: v * 2.0 + 1.0,
+                     lambda v: dtypes.to_float(v) * 2 + 1),
+        "bfloat16_sum": (dtypes.from_float(r.standard_normal(16).astype(np.float32)), lambda v: jnp.sum(v, keepdims=True),
+                         lambda v: np.sum(dtypes.to_float(v).astype(np.float64), keepdims=True)),
     }
     x, op, ref = cases[name]
     oshape = (1,) if name.endswith("_sum") else x.shape
@@ -135,7 +151,8 @@ CASES = {
     **{f"reduce_{k}": (lambda k=k: reduction(k)) for k in
        ("sum_scalar", "sum_last", "sum_first", "mean", "mse", "max_scalar", "max_last", "softmax")},
     **{f"dtype_{k}": (lambda k=k: dtype_case(k)) for k in
-       ("float32", "float16", "int32", "uint32", "bool", "float16_sum", "int32_sum")},
+       ("float32", "float16", "int32", "uint32", "bool", "float16_sum", "int32_sum", "bfloat16", "bfloat16_sum")},
+    "matmul_bfloat16": lambda: bf16_matmul(4, 16, 5),
 }
 
 
@@ -144,7 +161,10 @@ def check(name, got):
     want = np.asarray(ref(*args))
     got = np.asarray(got)
     assert got.shape == tuple(out_shape.shape), (got.shape, out_shape.shape)
-    if np.issubdtype(got.dtype, np.floating):
+    if dtypes.is_bf16(got.dtype):
+        # the reference's bf16 tolerance (tests/test_17_robustness.py:180)
+        np.testing.assert_allclose(dtypes.to_float(got).astype(np.float64), want, rtol=2e-2, atol=2e-2 * max(1.0, np.abs(want).max()))
+    elif np.issubdtype(got.dtype, np.floating):
         tol = 1e-2 if got.dtype == np.float16 else 1e-4
         np.testing.assert_allclose(got.astype(np.float64), want, rtol=tol, atol=tol)
     else:
