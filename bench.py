@@ -151,14 +151,14 @@ def bench_lv(steps: int, warmup: int, cpu: bool, cfg=None, block: int = 1, track
 
 
 def _lv_cpu_more(host, cfg) -> dict:
-    """The same C oracle on one core, and the float64 NumPy restatement
-    vectorised over trajectories (the interpret-like Python baseline), each
+    """The same C oracle on one core, the float64 NumPy restatement
+    vectorised over trajectories, and the kernel's own `.interpret()`, each
     on a bounded sample of config 1."""
     import oracle
     from oracle.ref64 import lv_rk4_f64
 
     out = {}
-    n1 = 20_000
+    n1 = 100_000
     oracle.set_threads(1)
     try:
         t0 = time.perf_counter()
@@ -168,12 +168,25 @@ def _lv_cpu_more(host, cfg) -> dict:
         oracle.set_threads(_cpu_cores())
     out["oracle_1_core"] = {"value": n1 * cfg.steps / dt1, "unit": "trajectory-steps/s", "cores": 1, "kind": "port",
                             "sample": f"first {n1} trajectories, all {cfg.steps} steps, {dt1:.2f} s"}
-    n2, s2 = 100_000, 400
+    n2, s2 = 100_000, 2000
     t0 = time.perf_counter()
     lv_rk4_f64(*(a[:n2] for a in host), cfg.dt, s2)
     dt2 = time.perf_counter() - t0
     out["numpy_f64_vectorized"] = {"value": n2 * s2 / dt2, "unit": "trajectory-steps/s", "cores": 1, "kind": "port",
                                    "sample": f"first {n2} trajectories, {s2} of {cfg.steps} steps, float64 NumPy, {dt2:.2f} s"}
+    # The same Pallas kernel through `.interpret()`, this backend's NumPy
+    # interpreter: the counterpart of the reference's `interpret=True` CPU
+    # path (src/palladium/__init__.py:110).
+    from palladium_amd.workloads import lv_rk4_call
+
+    n3, s3 = 100_000, 2000
+    icall = lv_rk4_call(n3, cfg.dt, s3, track_max=True, math_mode="safe")
+    t0 = time.perf_counter()
+    icall.interpret(*(a[:n3] for a in host))
+    dt3 = time.perf_counter() - t0
+    out["interpret"] = {"value": n3 * s3 / dt3, "unit": "trajectory-steps/s", "cores": 1, "kind": "port",
+                        "sample": f"first {n3} trajectories, {s3} of {cfg.steps} steps, hip_call(...).interpret() "
+                                  f"(NumPy, float32, SAFE order), {dt3:.2f} s"}
     return out
 
 
