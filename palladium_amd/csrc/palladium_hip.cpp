@@ -100,10 +100,14 @@ int compile(const char *src, size_t src_len, const char *name, int math_mode,
                     "):\n" + log);
   }
   size_t size = 0;
-  hiprtcGetCodeSize(prog, &size);
-  code->resize(size);
-  hiprtcGetCode(prog, code->data());
-  hiprtcDestroyProgram(&prog);
+  r = hiprtcGetCodeSize(prog, &size);
+  if (r == HIPRTC_SUCCESS) {
+    code->resize(size);
+    r = hiprtcGetCode(prog, code->data());
+  }
+  (void)hiprtcDestroyProgram(&prog);
+  if (r != HIPRTC_SUCCESS)
+    return fail(err, PH_ERR_COMPILE, std::string("hiprtcGetCode: ") + hiprtcGetErrorString(r));
   return PH_OK;
 }
 
@@ -227,6 +231,7 @@ int ph_launch(ph_kernel *k, unsigned int gx, unsigned int gy, unsigned int gz,
 
 int ph_launch_ptrs(ph_kernel *k, unsigned int blocks, unsigned int block,
                    void *stream, void *const *ptrs, size_t n_ptrs, char **err) {
+  if (n_ptrs && !ptrs) return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_launch_ptrs: null pointer array");
   std::vector<void *> values(ptrs, ptrs + n_ptrs);
   std::vector<void *> params(n_ptrs);
   for (size_t i = 0; i < n_ptrs; ++i) params[i] = &values[i];
@@ -315,6 +320,8 @@ int ph_dispatch_device(const char *src, size_t src_len, const char *name,
                        int64_t lanes, int64_t math_mode, void *stream,
                        const void *const *inputs, size_t n_inputs,
                        void *const *outputs, size_t n_outputs, char **err) {
+  if ((n_inputs && !inputs) || (n_outputs && !outputs))
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_dispatch_device: null operand array");
   unsigned int blocks = 0, block = 0;
   int rc = dispatch_geometry(grid_x, grid_y, grid_z, block_x, lanes, math_mode, &blocks, &block, err);
   if (rc != PH_OK) return rc;
@@ -334,6 +341,8 @@ int ph_dispatch(const char *src, size_t src_len, const char *name,
                 const size_t *input_bytes, size_t n_inputs,
                 void *const *outputs, const size_t *output_bytes,
                 size_t n_outputs, char **err) {
+  if ((n_inputs && (!inputs || !input_bytes)) || (n_outputs && (!outputs || !output_bytes)))
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_dispatch: null operand array");
   unsigned int blocks = 0, block = 0;
   int rc = dispatch_geometry(grid_x, grid_y, grid_z, block_x, lanes, math_mode, &blocks, &block, err);
   if (rc != PH_OK) return rc;
@@ -350,18 +359,25 @@ int ph_dispatch(const char *src, size_t src_len, const char *name,
     if (rc != PH_OK) return rc;
   }
   std::vector<void *> dev(st->bufs.begin(), st->bufs.begin() + n_ops);
+  // Once work is queued, every exit drains the staging stream first: a
+  // queued copy must not touch the caller's host buffers after we return,
+  // nor a staging buffer the next call on this thread regrows.
+  auto drain_and = [&](int code) {
+    (void)hipStreamSynchronize(st->stream);  // best effort: `code` is the error reported
+    return code;
+  };
   hipError_t e;
   for (size_t i = 0; i < n_inputs; ++i) {
     if (!input_bytes[i]) continue;
     e = hipMemcpyHtoDAsync(dev[i], const_cast<void *>(inputs[i]), input_bytes[i], st->stream);
-    if (e != hipSuccess) return hip_fail(err, e, "hipMemcpyHtoDAsync");
+    if (e != hipSuccess) return drain_and(hip_fail(err, e, "hipMemcpyHtoDAsync"));
   }
   rc = ph_launch_ptrs(k, blocks, block, st->stream, dev.data(), dev.size(), err);
-  if (rc != PH_OK) return rc;
+  if (rc != PH_OK) return drain_and(rc);
   for (size_t i = 0; i < n_outputs; ++i) {
     if (!output_bytes[i]) continue;
     e = hipMemcpyDtoHAsync(outputs[i], dev[n_inputs + i], output_bytes[i], st->stream);
-    if (e != hipSuccess) return hip_fail(err, e, "hipMemcpyDtoHAsync");
+    if (e != hipSuccess) return drain_and(hip_fail(err, e, "hipMemcpyDtoHAsync"));
   }
   e = hipStreamSynchronize(st->stream);
   if (e != hipSuccess) return hip_fail(err, e, "hipStreamSynchronize");

@@ -82,3 +82,20 @@ def test_kernel_load_without_device_fails_loudly():
     k = rt.Kernel('extern "C" __global__ void k(float* o) { o[0] = 1.0f; }', "k")
     with pytest.raises(rt.HipError):
         k.load()
+
+
+def test_dispatch_entry_points_reject_null_operand_arrays():
+    """Argument validation happens before any HIP call (no GPU needed)."""
+    import ctypes
+
+    lib = rt.lib()
+    src = b'extern "C" __global__ void k(float* o) {}'
+    calls = [
+        lambda e: lib.ph_dispatch(src, len(src), b"k", 1, 1, 1, 0, 1, 0, None, None, 1, None, None, 0, ctypes.byref(e)),
+        lambda e: lib.ph_dispatch_device(src, len(src), b"k", 1, 1, 1, 0, 1, 0, None, None, 0, None, 1, ctypes.byref(e)),
+    ]
+    for call in calls:
+        err = ctypes.c_void_p()
+        assert call(err) == 1
+        assert b"null operand array" in ctypes.string_at(err.value)
+        lib.ph_free_error(err)
