@@ -346,18 +346,29 @@ class Buffer:
             return cls(tuple(obj.shape), dt, ptr=obj.data_ptr(), owner=obj)
         cai = getattr(obj, "__cuda_array_interface__", None)
         if cai is not None:
-            return cls(cai["shape"], np.dtype(cai["typestr"]), ptr=cai["data"][0], owner=obj)
+            dt = np.dtype(cai["typestr"])
+            strides = cai.get("strides")
+            if strides is not None:
+                dense = tuple(int(np.prod(cai["shape"][k + 1 :], dtype=np.int64)) * dt.itemsize for k in range(len(cai["shape"])))
+                if tuple(strides) != dense:
+                    raise ValueError("device arrays must be C-contiguous")
+            return cls(cai["shape"], dt, ptr=cai["data"][0], owner=obj)
         raise TypeError(f"cannot wrap {type(obj).__name__} as a device buffer")
 
     def copy_from(self, arr: np.ndarray, stream: Any = None) -> None:
-        arr = np.ascontiguousarray(arr)
-        if arr.nbytes != self.nbytes:
-            raise ValueError(f"copy_from: {arr.nbytes} bytes into a {self.nbytes}-byte buffer")
+        """Host -> device copy. With `stream`, the copy is ordered on it and
+        may still be reading `arr` on return: the caller keeps `arr` alive
+        until the stream passes this point. A non-contiguous `arr` is
+        compacted into a temporary first, and then the copy is waited for,
+        since nothing would keep the temporary alive."""
+        src = np.ascontiguousarray(arr)
+        if src.nbytes != self.nbytes:
+            raise ValueError(f"copy_from: {src.nbytes} bytes into a {self.nbytes}-byte buffer")
         if self.nbytes:
-            _call("ph_memcpy_h2d", ctypes.c_void_p(self.ptr), arr.ctypes.data_as(ctypes.c_void_p),
+            _call("ph_memcpy_h2d", ctypes.c_void_p(self.ptr), src.ctypes.data_as(ctypes.c_void_p),
                   ctypes.c_size_t(self.nbytes), _stream_handle(stream))
-            if stream is None:
-                synchronize_stream(None)
+            if stream is None or src is not arr:
+                synchronize_stream(stream)
 
     def to_numpy(self, stream: Any = None) -> np.ndarray:
         """Copy to a new host array after the work queued on `stream`."""
@@ -503,6 +514,7 @@ class Batch:
     def commit(self, graph: bool = False) -> "Batch":
         for k, *_ in self._items:
             k.load()
+        self._release_graph()  # a re-commit replaces the previous graph
         self._start = Event()
         self._stop = Event()
         if graph:
@@ -540,7 +552,7 @@ class Batch:
         self.wait()
         return self._start.elapsed_ms(self._stop) / 1e3
 
-    def __del__(self) -> None:
+    def _release_graph(self) -> None:
         if getattr(self, "_graph", None) and _lib is not None:
             # The graph may still be running: let it finish before destroying it.
             err = ctypes.c_void_p()
@@ -549,3 +561,7 @@ class Batch:
                 if err.value:
                     _lib.ph_free_error(err)
             _lib.ph_graph_destroy(ctypes.c_void_p(self._graph))
+        self._graph = None
+
+    def __del__(self) -> None:
+        self._release_graph()

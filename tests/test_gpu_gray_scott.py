@@ -64,3 +64,27 @@ def test_full_config4_safe_bit_exact():
     np.testing.assert_array_equal(u, wu)
     np.testing.assert_array_equal(v, wv)
     assert float(np.abs(v).sum()) > 1.0  # a pattern grew
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_batch_recommit_replays_the_steps(graph):
+    """Committing a batch again re-runs its launches (a graph batch is
+    re-captured, the old graph released): 2 commits of 6 ping-pong steps
+    equal 12 steps of the oracle."""
+    from palladium_amd import runtime as rt
+
+    size, steps = 64, 6
+    u0, v0 = gray_scott_initial(size)
+    bound = gray_scott_call(size=size, math_mode="safe").bound(u0, v0)
+    geo = bound.geometry
+    bufs = [[rt.Buffer.from_numpy(u0), rt.Buffer.from_numpy(v0)],
+            [rt.Buffer.empty(u0.shape, np.float32), rt.Buffer.empty(v0.shape, np.float32)]]
+    batch = rt.Batch(stream=bound.stream)
+    for s in range(steps):
+        src, dst = bufs[s % 2], bufs[1 - s % 2]
+        batch.add(bound.kernel, geo.blocks, geo.block, [b.ptr for b in src] + [b.ptr for b in dst])
+    batch.commit(graph=graph).wait()
+    batch.commit(graph=graph).wait()
+    wu, wv = oracle.gray_scott(u0, v0, GS_CFG, 2 * steps)
+    np.testing.assert_array_equal(bufs[0][0].to_numpy(bound.stream), wu)
+    np.testing.assert_array_equal(bufs[0][1].to_numpy(bound.stream), wv)
