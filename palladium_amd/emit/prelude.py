@@ -36,6 +36,11 @@ __device__ __forceinline__ void ph_threefry2x32(unsigned int k0, unsigned int k1
     const unsigned int k2 = k0 ^ k1 ^ 0x1BD11BDAu;
     unsigned int x0 = c0 + k0;
     unsigned int x1 = c1 + k1;
+    /* Optimisation barrier (an empty asm that emits no instruction): without
+       it LLVM re-associates each key injection into the following rounds'
+       adds and keeps injected and un-injected copies of the state live,
+       about 30% more VALU work per block (fold_in chains twice that). */
+    asm volatile("" : "+v"(x0), "+v"(x1));
 #define PH_TF_ROUND(r) x0 += x1; x1 = ph_rotl32(x1, r); x1 ^= x0;
     PH_TF_ROUND(13) PH_TF_ROUND(15) PH_TF_ROUND(26) PH_TF_ROUND(6)
     x0 += k1; x1 += k2 + 1u;
@@ -55,11 +60,13 @@ __device__ __forceinline__ void ph_threefry2x32(unsigned int k0, unsigned int k1
 #if PH_MATH_MODE == 2
 /* FAST: hardware sine/cosine (v_sin_f32/v_cos_f32 take revolutions, so
    cos(2*pi*u) needs no range reduction after reassociation). */
-__device__ __forceinline__ float ph_sin(float x) { return __sinf(x); }
-__device__ __forceinline__ float ph_cos(float x) { return __cosf(x); }
+__device__ __forceinline__ float ph_sin(float x) { return __builtin_amdgcn_sinf(x * 0.15915494309189535f); }
+__device__ __forceinline__ float ph_cos(float x) { return __builtin_amdgcn_cosf(x * 0.15915494309189535f); }
+__device__ __forceinline__ float ph_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 #else
 __device__ __forceinline__ float ph_sin(float x) { return sinf(x); }
 __device__ __forceinline__ float ph_cos(float x) { return cosf(x); }
+__device__ __forceinline__ float ph_exp(float x) { return expf(x); }
 #endif
 
 __device__ __forceinline__ float ph_fmin(float a, float b) { return fminf(a, b); }

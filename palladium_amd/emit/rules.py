@@ -90,7 +90,7 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
     if opname == "sign":
         return "(({a} > 0.0f) ? 1.0f : (({a} < 0.0f) ? -1.0f : {a}))" if f else "(({a} > 0) - ({a} < 0))"
     unary_f = {
-        "exp": "expf({a})",
+        "exp": "ph_exp({a})",
         "exp2": "exp2f({a})",
         "log": "logf({a})",
         "log1p": "log1pf({a})",
@@ -104,7 +104,7 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
         "floor": "floorf({a})",
         "ceil": "ceilf({a})",
         "round": "roundf({a})",
-        "logistic": "(1.0f / (1.0f + expf(-{a})))",
+        "logistic": "(1.0f / (1.0f + ph_exp(-{a})))",
         "atan2": "atan2f({a}, {b})",
     }
     if opname in unary_f:
