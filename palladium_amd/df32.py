@@ -59,6 +59,19 @@ __device__ __forceinline__ df32 df_mul(df32 x, df32 y) {
     float cl3 = cl1 + cl2;
     return df_fast2sum(ch, cl3);
 }
+/* x * c for a float c (a df32 whose lo word is +0): DWTimesDW with y.lo = 0
+   reduces exactly to this, bit for bit, for nonzero finite operands (the
+   dropped terms are x.lo * 0 and fma(x.hi, 0, that), signed zeros only). */
+__device__ __forceinline__ df32 df_mul_f(df32 x, float c) {
+    float ch = x.hi * c;
+    float cl1 = __builtin_fmaf(x.hi, c, -ch);
+    float cl2 = x.lo * c;
+    float cl3 = cl1 + cl2;
+    return df_fast2sum(ch, cl3);
+}
+/* 2 * x is exact in both words (barring overflow), and equals
+   DWTimesDW(x, 2) bit for bit. */
+__device__ __forceinline__ df32 df_twice(df32 x) { df32 r; r.hi = 2.0f * x.hi; r.lo = 2.0f * x.lo; return r; }
 __device__ __forceinline__ df32 operator+(df32 a, df32 b) { return df_add(a, b); }
 __device__ __forceinline__ df32 operator-(df32 a, df32 b) { return df_sub(a, b); }
 __device__ __forceinline__ df32 operator*(df32 a, df32 b) { return df_mul(a, b); }
@@ -67,12 +80,14 @@ __device__ __forceinline__ df32 operator*(df32 a, df32 b) { return df_mul(a, b);
 LV_DF32_SOURCE = DF32_PRELUDE + r"""
 struct LVState { df32 x, y; };
 
-__device__ __forceinline__ LVState lv_rhs(LVState s, df32 a, df32 b, df32 c, df32 d) {
+/* The parameters and step sizes are floats (df32 with lo = 0): their
+   products use df_mul_f, which equals the general df_mul on them exactly. */
+__device__ __forceinline__ LVState lv_rhs(LVState s, float a, float b, float c, float d) {
     df32 xy = s.x * s.y;
-    LVState r; r.x = a * s.x - b * xy; r.y = c * xy - d * s.y; return r;
+    LVState r; r.x = df_mul_f(s.x, a) - df_mul_f(xy, b); r.y = df_mul_f(xy, c) - df_mul_f(s.y, d); return r;
 }
-__device__ __forceinline__ LVState lv_adv(LVState s, LVState k, df32 h) {
-    LVState r; r.x = s.x + h * k.x; r.y = s.y + h * k.y; return r;
+__device__ __forceinline__ LVState lv_adv(LVState s, LVState k, float h) {
+    LVState r; r.x = s.x + df_mul_f(k.x, h); r.y = s.y + df_mul_f(k.y, h); return r;
 }
 
 extern "C" __global__ void __launch_bounds__(256)
@@ -85,10 +100,8 @@ lv_rk4_df32(const float* __restrict__ x0, const float* __restrict__ y0,
 {
     const unsigned int i = blockIdx.x * 256u + threadIdx.x;
     if (i >= n) return;
-    df32 a = df_from_float(a_[i]), b = df_from_float(b_[i]);
-    df32 c = df_from_float(c_[i]), d = df_from_float(d_[i]);
-    df32 half = df_from_float(0.5f * dt), full = df_from_float(dt);
-    df32 sixth = df_from_float(dt / 6.0f), two = df_from_float(2.0f);
+    const float a = a_[i], b = b_[i], c = c_[i], d = d_[i];
+    const float half = 0.5f * dt, full = dt, sixth = dt / 6.0f;
     LVState s; s.x = df_from_float(x0[i]); s.y = df_from_float(y0[i]);
     for (unsigned int k = 0; k < steps; ++k) {
         LVState k1 = lv_rhs(s, a, b, c, d);
@@ -96,8 +109,8 @@ lv_rk4_df32(const float* __restrict__ x0, const float* __restrict__ y0,
         LVState k3 = lv_rhs(lv_adv(s, k2, half), a, b, c, d);
         LVState k4 = lv_rhs(lv_adv(s, k3, full), a, b, c, d);
         LVState sum;
-        sum.x = k1.x + two * k2.x + two * k3.x + k4.x;
-        sum.y = k1.y + two * k2.y + two * k3.y + k4.y;
+        sum.x = k1.x + df_twice(k2.x) + df_twice(k3.x) + k4.x;
+        sum.y = k1.y + df_twice(k2.y) + df_twice(k3.y) + k4.y;
         s = lv_adv(s, sum, sixth);
     }
     xo_hi[i] = s.x.hi; xo_lo[i] = s.x.lo;
@@ -107,15 +120,22 @@ lv_rk4_df32(const float* __restrict__ x0, const float* __restrict__ y0,
 
 # float32 operations per df32 operation as written above (FMA = 2):
 # df_add = 2 TwoSum (6 each) + 2 adds + 2 Fast2Sum (3 each) = 20;
-# df_mul = 2 muls + 3 FMAs + 1 add + 1 Fast2Sum = 12.
+# df_mul = 2 muls + 3 FMAs + 1 add + 1 Fast2Sum = 12;
+# df_mul_f (df32 x float) = 2 muls + 1 FMA + 1 add + 1 Fast2Sum = 8;
+# df_twice = 2 muls.
 DF_ADD_FLOPS = 20
 DF_MUL_FLOPS = 12
-# One RK4 step of lv_rk4_df32: four rhs (5 muls, 2 adds: x*y is shared),
-# four stage/final updates (2 muls, 2 adds), the weighted sums (4 muls,
-# 6 adds): 32 df_mul + 22 df_add.
-LV_DF32_MULS_PER_STEP = 32
+DF_MUL_F_FLOPS = 8
+DF_TWICE_FLOPS = 2
+# One RK4 step of lv_rk4_df32: four rhs (x*y shared: 1 df_mul + 4 df_mul_f
+# + 2 df_add each), four stage/final updates (2 df_mul_f + 2 df_add each),
+# the weighted sums (4 df_twice + 6 df_add): 58 df32 operations.
+LV_DF32_MULS_PER_STEP = 4
+LV_DF32_MUL_FS_PER_STEP = 24
+LV_DF32_TWICES_PER_STEP = 4
 LV_DF32_ADDS_PER_STEP = 22
-LV_DF32_FLOPS_PER_STEP = LV_DF32_MULS_PER_STEP * DF_MUL_FLOPS + LV_DF32_ADDS_PER_STEP * DF_ADD_FLOPS
+LV_DF32_FLOPS_PER_STEP = (LV_DF32_MULS_PER_STEP * DF_MUL_FLOPS + LV_DF32_MUL_FS_PER_STEP * DF_MUL_F_FLOPS
+                          + LV_DF32_TWICES_PER_STEP * DF_TWICE_FLOPS + LV_DF32_ADDS_PER_STEP * DF_ADD_FLOPS)
 
 _kernel: rt.Kernel | None = None
 
