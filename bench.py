@@ -16,6 +16,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -281,6 +282,38 @@ def bench_gbm(steps: int, warmup: int, cpu: bool) -> dict:
         dt = time.perf_counter() - t0
         res["cpu_baseline"] = {"value": n_cpu * cfg.n_steps / dt, "unit": "path-steps/s", "cores": _cpu_cores(),
                                "kind": "port", "sample": f"all {n_cpu} paths x {cfg.n_steps} steps of config 3, C oracle, {dt:.2f} s"}
+    return res
+
+
+def bench_gbm_block(steps: int, warmup: int, cpu: bool) -> dict:
+    """Config 3 with its stated output, the discounted payoff reduced per
+    block: 256 paths per program instance spread over 256 lanes, a
+    cross-lane sum at the end. Also reports the price from the block sums
+    against the Black-Scholes closed form (standard error from the block
+    sums, which are i.i.d.)."""
+    from palladium_amd import runtime as rt
+    from palladium_amd.frontend import random
+    from palladium_amd.workloads import GBM_CFG, black_scholes_call, gbm_block_call
+
+    cfg = GBM_CFG
+    block = 256
+    key = random.key(cfg.seed)
+    call = gbm_block_call(cfg, block=block)
+    bound = call.bound(key)
+    out = rt.Buffer.empty((cfg.n_paths // block,), np.float32)
+    ops = [rt.Buffer.from_numpy(key), out]
+    ms, avg = _timed_launches(bound, ops, steps, warmup)
+    sums = out.to_numpy(bound.stream).astype(np.float64)
+    price = sums.sum() / cfg.n_paths
+    se = sums.std(ddof=1) / block / math.sqrt(sums.size)
+    exact = black_scholes_call(cfg.s0, cfg.strike, cfg.t, cfg.r, cfg.sigma)
+    ps = cfg.n_paths * cfg.n_steps
+    res = _base("GBM path-steps/s, payoff reduced per 256-path block (config 3's output)", ps / (ms / 1e3),
+                "path-steps/s", steps, warmup, ms,
+                {"workload": "GBM Monte Carlo, config 3, per-block sums", "paths": cfg.n_paths, "steps": cfg.n_steps,
+                 "block": block, "math_mode": "fast"})
+    res["price"] = {"mc": price, "black_scholes": exact, "se": se, "within_3se": bool(abs(price - exact) < 3 * se)}
+    res["roofline"] = {"bound": "valu", "avg_launch_ms": avg}
     return res
 
 
@@ -809,7 +842,7 @@ def main() -> int:
         )
         return 2
     rank = int(os.environ.get("RANK", "0"))
-    fns = {"lv": bench_lv, "lv0": bench_lv0, "gbm": bench_gbm, "gbm_fold_in": bench_gbm_fold_in, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
+    fns = {"lv": bench_lv, "lv0": bench_lv0, "gbm": bench_gbm, "gbm_block": bench_gbm_block, "gbm_fold_in": bench_gbm_fold_in, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
            "bs3_lockstep": bench_bs3_lockstep, "bs3_sorted": bench_bs3_sorted, "copy": bench_copy, "df32": bench_df32, "dispatch": bench_dispatch,
            "valu_rates": bench_valu_rates}
     if a.workload not in fns:
@@ -827,11 +860,11 @@ def main() -> int:
         # other hot kernels at their configurations, are reported beside the
         # first (GPU only, no CPU baselines: a few seconds in all).
         res["secondary"] = {}
-        for key, fn in (("gray_scott_4096", bench_gs), ("gbm_paths", bench_gbm), ("bs3_vdp", bench_bs3),
-                        ("lv_rk4_df32", bench_df32)):
+        for key, fn in (("gray_scott_4096", bench_gs), ("gbm_paths", bench_gbm), ("gbm_block_sums", bench_gbm_block),
+                        ("bs3_vdp", bench_bs3), ("lv_rk4_df32", bench_df32)):
             r = fn(a.steps, a.warmup, cpu=False)
             res["secondary"][key] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline",
-                                                        "accuracy", "accepted_steps_per_s") if k in r}
+                                                        "accuracy", "accepted_steps_per_s", "price") if k in r}
     if rank == 0:
         print(json.dumps(res), flush=True)
     return 0
