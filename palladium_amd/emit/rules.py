@@ -33,7 +33,7 @@ from palladium_amd.emit.core import (
     ref_view,
     rule,
 )
-from palladium_amd.ir import JaxprEqn, KeyAval, Literal, Var
+from palladium_amd.ir import JaxprEqn, KeyAval, Var
 
 F32 = "float"
 F16 = "_Float16"

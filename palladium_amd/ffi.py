@@ -22,8 +22,6 @@ from collections.abc import Callable
 from pathlib import Path
 from typing import Any
 
-import numpy as np
-
 from palladium_amd.dtypes import name as _dtype_name
 
 from palladium_amd.diagnostics import KernelDiagnostics, explain_spec, log_compile

@@ -27,7 +27,6 @@ from palladium_amd.frontend.core import (
     current_builder,
     default_dtype,
     literal,
-    scalar_kind,
 )
 from palladium_amd.dtypes import bfloat16_type as _bfloat16_type
 from palladium_amd.dtypes import kind as _kind

@@ -4,7 +4,6 @@ and the error taxonomy."""
 import numpy as np
 import pytest
 
-import palladium_amd as pa
 from palladium_amd import runtime as rt
 from palladium_amd.emit import emit_hip, rule
 from palladium_amd.errors import EmitError, UnsupportedPrimitiveError

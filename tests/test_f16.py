@@ -5,7 +5,7 @@ import numpy as np
 from f16_cases import arithmetic, inputs, transcendental
 from palladium_amd import runtime as rt
 from palladium_amd.emit import emit_hip
-from palladium_amd.frontend import jnp, pl
+from palladium_amd.frontend import pl
 from palladium_amd.trace import trace
 
 

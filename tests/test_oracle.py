@@ -14,7 +14,6 @@ import oracle
 from oracle.ref64 import lv_rk4_f64
 from palladium_amd.workloads import (
     BS3_CFG,
-    GBM_CFG,
     GS_CFG,
     BS3Config,
     GBMConfig,
