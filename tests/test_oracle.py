@@ -326,3 +326,39 @@ def test_df32_lv_tracks_float64():
     assert err_df < 1e-10
     assert err_df < err_32 / 1e4
     np.testing.assert_allclose(yh.astype(np.float64) + yl, Y, rtol=1e-10)
+
+
+def _df_mul_f_numpy(hi, lo, c):
+    """df32 x float as the device's df_mul_f computes it: ch = fl(hi*c),
+    cl1 = the exact product error (TwoProd: hi*c - ch is representable, so
+    float64 gives it exactly), cl2 = fl(lo*c), cl3 = fl(cl1 + cl2), then
+    Fast2Sum(ch, cl3), all in float32."""
+    f = np.float32
+    ch = (hi * c).astype(f)
+    cl1 = (hi.astype(np.float64) * c.astype(np.float64) - ch.astype(np.float64)).astype(f)
+    cl2 = (lo * c).astype(f)
+    cl3 = (cl1 + cl2).astype(f)
+    s = (ch + cl3).astype(f)
+    z = (s - ch).astype(f)
+    return s, (cl3 - z).astype(f)
+
+
+def test_df32_times_float_equals_general_product():
+    """The device's df_mul_f(x, c) equals DWTimesDW(x, (c, +0)), the C
+    oracle's general product, bit for bit (nonzero finite operands): the
+    kernel uses the first, the oracle the second."""
+    rng = np.random.default_rng(7)
+    n = 200_000
+    hi = (rng.standard_normal(n) * np.exp2(rng.integers(-20, 20, n))).astype(np.float32)
+    lo = (hi.astype(np.float64) * rng.uniform(-2**-25, 2**-25, n)).astype(np.float32)  # |lo| <= ulp(hi)/2
+    c = (rng.standard_normal(n) * np.exp2(rng.integers(-10, 10, n))).astype(np.float32)
+    ok = (hi != 0) & (lo != 0) & (c != 0)
+    hi, lo, c = hi[ok], lo[ok], c[ok]
+    wh, wl = oracle.df32_mul(hi, lo, c, np.zeros_like(c))
+    gh, gl = _df_mul_f_numpy(hi, lo, c)
+    np.testing.assert_array_equal(gh.view(np.uint32), wh.view(np.uint32))
+    np.testing.assert_array_equal(gl.view(np.uint32), wl.view(np.uint32))
+    # doubling is exact in both words
+    th, tl = oracle.df32_mul(hi, lo, np.full_like(hi, 2.0), np.zeros_like(hi))
+    np.testing.assert_array_equal(th, 2 * hi)
+    np.testing.assert_array_equal(tl, 2 * lo)
