@@ -21,6 +21,7 @@ from typing import Any, Callable, Sequence
 
 import numpy as np
 
+from palladium_amd.dtypes import name as _dtype_name
 from palladium_amd.errors import TraceError
 from palladium_amd.frontend import jnp
 from palladium_amd.frontend.core import (
@@ -215,7 +216,7 @@ class Ref:
                     value = jnp.convert_element_type(value, self.dtype)
                 else:
                     raise TraceError(
-                        f"storing {value.dtype} into a {self.dtype} ref; cast explicitly"
+                        f"storing {_dtype_name(value.dtype)} into a {_dtype_name(self.dtype)} ref; cast explicitly"
                     )
             if value.shape != shape:
                 if math.prod(value.shape) == math.prod(shape):

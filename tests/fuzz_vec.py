@@ -9,12 +9,16 @@ reductions (max/min exact in any order; sums over values quantised to
 matrix, a `cond` on a data-dependent row predicate, `iota`, integer
 hashing (multiply wrap, xor, shifts) and a fori_loop, so every result is
 exactly determined and the GPU must match the interpreter bit for bit
-under SAFE math.
+under SAFE math. The same programs run with bfloat16 blocks (each
+operation evaluated in float32 and rounded; the quantised sums and dot
+products are exact in float32 before their one rounding, so the lane-
+parallel butterfly order cannot change them either).
 """
 
 import numpy as np
 
 import palladium_amd as pa
+from palladium_amd import dtypes
 from palladium_amd.frontend import jnp, lax, pl
 
 F = np.float32
@@ -50,8 +54,10 @@ def _expr(rng, leaves, depth):
     return a * 0.75 - b
 
 
-def _tame(v, shape=None):
+def _tame(v, shape=None, dt=None):
     v = jnp.clip(v, -50.0, 50.0)
+    if dt is not None and v.dtype != dt:  # a lone literal leaf traces as a strong float32
+        v = v.astype(dt)
     return v if shape is None else jnp.broadcast_to(v, shape)
 
 
@@ -63,15 +69,16 @@ def make_kernel(seed, lanes=False):
     def kernel(x_ref, y_ref, k_ref, o_ref, s_ref, h_ref):
         rng = np.random.default_rng(seed)
         x, y = x_ref[...], y_ref[...]  # (R, 4)
+        dt = x.dtype
         k = k_ref[...]  # (R, 1) int32
-        col = lax.broadcasted_iota(jnp.int32, x.shape, 1).astype(jnp.float32)
-        v = _tame(_expr(rng, [x, y, col * 0.5], 4), x.shape)
+        col = lax.broadcasted_iota(jnp.int32, x.shape, 1).astype(dt)
+        v = _tame(_expr(rng, [x, y, col * 0.5], 4), x.shape, dt)
         rmax = jnp.broadcast_to(jnp.max(v, axis=1).reshape(v.shape[0], 1), v.shape)
         rmin = jnp.broadcast_to(jnp.min(v, axis=1).reshape(v.shape[0], 1), v.shape)
-        v = _tame(_expr(rng, [v, rmax, rmin, x], 3), x.shape)
+        v = _tame(_expr(rng, [v, rmax, rmin, x], 3), x.shape, dt)
         # A constant 4x4 matrix with small dyadic entries.
         wi = lax.broadcasted_iota(jnp.int32, (W, W), 0) * 3 + lax.broadcasted_iota(jnp.int32, (W, W), 1)
-        wm = ((wi * (seed % 5 + 1)) % 5 - 2).astype(jnp.float32) * 0.5
+        wm = ((wi * (seed % 5 + 1)) % 5 - 2).astype(dt) * 0.5
         d = jnp.dot(_quant(v), wm)
         if seed % 3 == 0 and not lanes:
             d = jnp.dot(wm, _quant(v).T).T  # transposes that move the row dim
@@ -82,7 +89,7 @@ def make_kernel(seed, lanes=False):
         out = lax.cond(pred, lambda t: t * 0.5 + 1.0, lambda t: jnp.abs(t) - 2.0, d)
 
         def body(i, c):
-            return _tame(c * 0.5 + jnp.minimum(c, x) - i.astype(jnp.float32) * 0.25)
+            return _tame(c * 0.5 + jnp.minimum(c, x) - i.astype(dt) * 0.25, dt=dt)
 
         out = lax.fori_loop(0, 2 + seed % 4, body, out)
         o_ref[...] = out
@@ -95,19 +102,21 @@ def make_kernel(seed, lanes=False):
     return kernel
 
 
-def make_call(seed, rows=512, lanes=False, **kw):
+def make_call(seed, rows=512, lanes=False, dtype=F, **kw):
     r = 64 if lanes else 1
     blk = pl.BlockSpec((r, W), lambda i: (i, 0))
     col = pl.BlockSpec((r, 1), lambda i: (i, 0))
     return pa.hip_call(make_kernel(seed, lanes), grid=(rows // r,), in_specs=[blk, blk, col],
                        out_specs=(blk, col, col),
-                       out_shape=(pl.ShapeDtypeStruct((rows, W), F), pl.ShapeDtypeStruct((rows, 1), F),
+                       out_shape=(pl.ShapeDtypeStruct((rows, W), dtype), pl.ShapeDtypeStruct((rows, 1), dtype),
                                   pl.ShapeDtypeStruct((rows, 1), np.int32)), **kw)
 
 
-def make_inputs(seed, rows=512):
+def make_inputs(seed, rows=512, dtype=F):
     rng = np.random.default_rng(1000 + seed)
     x = rng.uniform(-3, 3, (rows, W)).astype(F)
     y = rng.uniform(-3, 3, (rows, W)).astype(F)
     k = rng.integers(-(2**31), 2**31 - 1, (rows, 1)).astype(np.int32)
+    if dtype is not F:
+        x, y = dtypes.from_float(x), dtypes.from_float(y)
     return x, y, k

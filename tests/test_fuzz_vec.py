@@ -22,3 +22,18 @@ def test_program_traces_and_interprets(seed, lanes):
     o, s, h = call.interpret(*args)
     assert np.all(np.isfinite(o)) and np.all(np.abs(o) <= 50.0)
     assert np.all(s * 8 == np.round(s * 8))  # sums of 1/8-quantised values stay exact
+
+
+@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("lanes", [False, True])
+def test_bf16_program_traces_and_interprets(seed, lanes):
+    from palladium_amd import dtypes
+
+    call = make_call(seed, rows=128, lanes=lanes, dtype=dtypes.bfloat16)
+    args = make_inputs(seed, rows=128, dtype=dtypes.bfloat16)
+    spec = trace(call._staged, *args)
+    assert (lane_transform(spec) is not None) == lanes
+    assert "__bf16" in emit_hip(spec, math_mode="safe")
+    o, s, h = call.interpret(*args)
+    o = dtypes.to_float(o)
+    assert np.all(np.isfinite(o)) and np.all(np.abs(o) <= 50.0)

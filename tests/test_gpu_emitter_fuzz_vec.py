@@ -1,6 +1,6 @@
 """Differential test of the emitter on vector programs (tests/fuzz_vec.py):
-per-instance and lane-parallel launches under SAFE math, bit for bit
-against the NumPy interpreter."""
+per-instance and lane-parallel launches under SAFE math, float32 and
+bfloat16, bit for bit against the NumPy interpreter."""
 
 import os
 
@@ -8,6 +8,8 @@ import numpy as np
 import pytest
 
 from fuzz_vec import make_call, make_inputs
+
+from palladium_amd import dtypes
 
 pytestmark = pytest.mark.gpu
 
@@ -21,4 +23,18 @@ def test_vector_program_bit_exact_vs_interpreter(seed, lanes):
     got = call(*args)
     want = call.interpret(*args)
     for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
+
+
+@pytest.mark.parametrize("lanes", [False, True], ids=["instance", "lanes"])
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+def test_vector_program_bf16_bit_exact_vs_interpreter(seed, lanes):
+    print(f"fuzz_vec bf16 seed={seed} lanes={lanes}", flush=True)
+    call = make_call(seed, lanes=lanes, dtype=dtypes.bfloat16, math_mode="safe")
+    args = make_inputs(seed, dtype=dtypes.bfloat16)
+    got = call(*args)
+    want = call.interpret(*args)
+    for g, w in zip(got, want):
+        if dtypes.is_bf16(w.dtype):
+            g, w = dtypes.as_bits(g), dtypes.as_bits(w)
         np.testing.assert_array_equal(g, w)
