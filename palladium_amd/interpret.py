@@ -13,7 +13,8 @@ in lockstep; `while` masks finished instances (their stores are
 suppressed), `cond` evaluates each branch under its instance mask.
 Arithmetic is NumPy's, in the kernel's dtypes (fp32 ops are IEEE; libm-style
 functions may differ from the device by an ulp); `min`/`max` on floats are
-NaN-suppressing `fmin`/`fmax`, matching the emitted code. bfloat16 values
+NaN-suppressing `fmin`/`fmax` with -0 ordered below +0, matching what the
+emitted code computes on gfx950. bfloat16 values
 are carried as float32 arrays: each operation is evaluated in float32 and
 rounded to bfloat16 (ties to even), and bfloat16 sums and contractions
 accumulate in float32 and round once. Float sums add one element at a time
@@ -133,6 +134,46 @@ def _align(x: Any, rank: int, n: int) -> Any:
     return x
 
 
+def _fmin(a: Any, b: Any) -> np.ndarray:
+    """NaN-suppressing minimum with -0 ordered below +0 (IEEE 754-2019
+    minimumNumber): what gfx950's v_min_f32 returns for `fminf`. NumPy's
+    fmin returns its second operand when the two compare equal, so it
+    differs on zeros of opposite sign."""
+    r = np.fmin(a, b)
+    zeros = (np.asarray(a) == 0) & (np.asarray(b) == 0)
+    if np.any(zeros):
+        neg = np.signbit(a) | np.signbit(b)
+        r = np.where(zeros, np.where(neg, -np.zeros_like(r), np.zeros_like(r)), r)
+    return r
+
+
+def _fmax(a: Any, b: Any) -> np.ndarray:
+    """NaN-suppressing maximum with +0 ordered above -0 (maximumNumber),
+    as gfx950's v_max_f32 returns for `fmaxf`."""
+    r = np.fmax(a, b)
+    zeros = (np.asarray(a) == 0) & (np.asarray(b) == 0)
+    if np.any(zeros):
+        neg = np.signbit(a) & np.signbit(b)
+        r = np.where(zeros, np.where(neg, -np.zeros_like(r), np.zeros_like(r)), r)
+    return r
+
+
+def _fold(op: Any, src: np.ndarray, axes: tuple[int, ...]) -> np.ndarray:
+    """Reduce `src` over `axes` with a binary `op` (order-free here: the
+    signed-zero ordering makes min/max a total order on non-NaN values).
+    An empty reduction gives the identity, -inf for max and +inf for min."""
+    src = np.asarray(src)
+    kept = [d for d in range(src.ndim) if d not in axes]
+    moved = np.transpose(src, kept + list(axes))
+    flat = moved.reshape(moved.shape[: len(kept)] + (-1,))
+    if flat.shape[-1] == 0:
+        return np.full(flat.shape[:-1], -np.inf if op is _fmax else np.inf, src.dtype)
+    acc = flat[..., 0]
+    for r in range(1, flat.shape[-1]):
+        acc = op(acc, flat[..., r])
+    return acc
+
+
 def _round_half_away(x):
     return np.sign(x) * np.floor(np.abs(x) + np.asarray(0.5, x.dtype))
 
@@ -158,9 +199,9 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
         elif name == "rem":
             r = np.fmod(a, b)
         elif name == "min":
-            r = np.fmin(a, b) if isf else np.minimum(a, b)
+            r = _fmin(a, b) if isf else np.minimum(a, b)
         elif name == "max":
-            r = np.fmax(a, b) if isf else np.maximum(a, b)
+            r = _fmax(a, b) if isf else np.maximum(a, b)
         elif name == "pow":
             r = np.power(a, b)
         elif name == "neg":
@@ -202,7 +243,7 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
             r = np.where(sb < 32, np.asarray(a) << np.minimum(sb, 31), 0).astype(dt)
         elif name == "clamp":
             lo, x, hi = ops
-            r = (np.fmin(np.fmax(x, lo), hi) if np.asarray(x).dtype.kind == "f" else np.minimum(np.maximum(x, lo), hi))
+            r = (_fmin(_fmax(x, lo), hi) if np.asarray(x).dtype.kind == "f" else np.minimum(np.maximum(x, lo), hi))
         elif name == "select_n":
             pred, cases = ops[0], ops[1:]
             if np.asarray(pred).dtype == np.bool_:
@@ -321,9 +362,9 @@ def _eval(jaxpr: Jaxpr, env: _Env, invals: list[Any], mask: np.ndarray) -> list[
             f = {"reduce_sum": np.sum, "reduce_or": np.any, "reduce_and": np.all}.get(name)
             bf = is_bf16(eqn.outvars[0].aval.dtype)
             if name == "reduce_max":
-                r = np.fmax.reduce(src, axis=axes) if src.dtype.kind == "f" else np.max(src, axis=axes)
+                r = _fold(_fmax, src, axes) if src.dtype.kind == "f" else np.max(src, axis=axes)
             elif name == "reduce_min":
-                r = np.fmin.reduce(src, axis=axes) if src.dtype.kind == "f" else np.min(src, axis=axes)
+                r = _fold(_fmin, src, axes) if src.dtype.kind == "f" else np.min(src, axis=axes)
             elif name == "reduce_sum" and (bf or src.dtype.kind == "f"):
                 r = _ordered_sum(src, axes, np.float32 if bf else src.dtype)
             else:

@@ -90,3 +90,18 @@ def test_indexed_refs_and_blocks_2d():
                           out_specs=pl.BlockSpec((None, 4), lambda i: (i, 0)),
                           out_shape=pl.ShapeDtypeStruct((3, 4), np.float32), interpret=True)
     np.testing.assert_array_equal(call(x), x * 2.0 + 1.0)
+
+
+def test_min_max_order_negative_zero_below_positive_zero():
+    """Float min/max, clamp and the max/min reductions order -0 below +0,
+    as gfx950's v_min_f32/v_max_f32 do for fminf/fmaxf (NumPy's own
+    fmin/fmax return the second operand on equal inputs)."""
+    import signed_zero_cases as zc
+    from palladium_amd import dtypes
+
+    for dt in (np.float32, dtypes.bfloat16):
+        got = zc.call(dt).interpret(*zc.inputs(dt))
+        for g, w in zip(got, zc.expected()):
+            g = dtypes.to_float(g) if dtypes.is_bf16(g.dtype) else g
+            np.testing.assert_array_equal(np.signbit(g), np.signbit(w))
+            np.testing.assert_array_equal(g, w)
