@@ -171,6 +171,12 @@ def _emit_elementwise_loops(cursor: Cursor, dst: CVal, body: Callable[[list[str]
     go(0)
 
 
+def _round_to_even(eqn: JaxprEqn) -> bool:
+    """lax.round's `rounding_method`: 0 = AWAY_FROM_ZERO (the default,
+    C roundf), 1 = TO_NEAREST_EVEN (jnp.round, C rintf)."""
+    return int(eqn.params.get("rounding_method", 0)) == 1
+
+
 def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     """All pure element-wise primitives (reference: `_rule_elementwise`,
     `src/palladium/emit/rules.py:274-351`). integer_pow expands to repeated
@@ -196,6 +202,8 @@ def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
             template = f"(({BF16})(float){{a}})"
     elif opname == "bitcast_convert_type":
         template = f"__builtin_bit_cast({dst_ctype}, {{a}})"
+    elif opname == "round" and _round_to_even(eqn):
+        template = "rintf({a})"  # the default rounding mode: nearest, ties to even
     elif opname == "select_n":
         if len(ops) == 3 and ops[0].ctype == "bool":
             template = "({a} ? {c} : {b})"

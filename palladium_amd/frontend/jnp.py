@@ -376,6 +376,14 @@ def tan(x): return _unary("tan", x, True)
 def tanh(x): return _unary("tanh", x, True)
 def sqrt(x): return _unary("sqrt", x, True)
 def rsqrt(x): return _unary("rsqrt", x, True)
+def round(x, decimals: int = 0):  # noqa: A001
+    """Nearest integer, ties to even (numpy's and JAX's jnp.round)."""
+    if decimals:
+        raise TraceError("jnp.round with decimals != 0 is not supported in kernels")
+    return _unary("round", x, True, rounding_method=1)
+
+
+def rint(x): return round(x)
 def floor(x): return _unary("floor", x, True)
 def ceil(x): return _unary("ceil", x, True)
 def logistic(x): return _unary("logistic", x, True)

@@ -78,6 +78,11 @@ def dot(lhs: Any, rhs: Any, precision: Any = None, preferred_element_type: Any =
     return jnp.dot(lhs, rhs, precision=precision, preferred_element_type=preferred_element_type)
 
 
+def round(x: Any, rounding_method: int = 0) -> Tracer:  # noqa: A001
+    """lax.round: 0 = away from zero (default), 1 = to nearest even."""
+    return jnp._unary("round", x, True, rounding_method=int(rounding_method))
+
+
 def iota(dtype: Any, size: int) -> Tracer:
     return jnp.broadcasted_iota(dtype, (int(size),), 0)
 

@@ -175,7 +175,21 @@ def _fold(op: Any, src: np.ndarray, axes: tuple[int, ...]) -> np.ndarray:
 
 
 def _round_half_away(x):
-    return np.sign(x) * np.floor(np.abs(x) + np.asarray(0.5, x.dtype))
+    """C roundf: nearest integer, halves away from zero, zeros keep their
+    sign. Exact: x - trunc(x) is representable, so nothing rounds on the way
+    (the shortcut floor(|x| + 0.5) does: 0.49999997 + 0.5 rounds up to 1,
+    as does 2^23 + 1 + 0.5 to 2^23 + 2)."""
+    x = np.asarray(x)
+    t = np.trunc(x)
+    step = (np.abs(x - t) >= np.asarray(0.5, x.dtype)).astype(x.dtype)
+    return t + np.copysign(step, x)
+
+
+def _sign(x):
+    """sign with zeros (and NaN) returned unchanged, as the emitted
+    `(a > 0) ? 1 : ((a < 0) ? -1 : a)` does (NumPy turns -0 into +0)."""
+    x = np.asarray(x)
+    return np.where((x == 0) | np.isnan(x), x, np.sign(x))
 
 
 def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
@@ -209,13 +223,13 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
         elif name == "abs":
             r = np.abs(a)
         elif name == "sign":
-            r = np.sign(a)
+            r = _sign(a) if isf else np.sign(a)
         elif name in ("exp", "exp2", "log", "log1p", "expm1", "sin", "cos", "tan", "tanh", "sqrt", "floor", "ceil"):
             r = getattr(np, name)(a)
         elif name == "rsqrt":
             r = np.asarray(1.0, a.dtype) / np.sqrt(a)
         elif name == "round":
-            r = _round_half_away(a)
+            r = np.rint(a) if int(eqn.params.get("rounding_method", 0)) == 1 else _round_half_away(a)
         elif name == "logistic":
             r = np.asarray(1.0, a.dtype) / (np.asarray(1.0, a.dtype) + np.exp(-a))
         elif name == "atan2":

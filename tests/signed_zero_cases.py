@@ -58,3 +58,62 @@ def expected():
     hi = np.array([mx(x, y) for x, y in zip(A, B)], np.float32)
     cl = np.array([mn(mx(x, y), y) for x, y in zip(A, B)], np.float32)
     return lo, hi, cl, np.array([0.0], np.float32), np.array([-0.0], np.float32)
+
+
+# zeros, halves, the largest float below 0.5, odd integers past 2^23,
+# infinities and NaN
+R = np.array([-0.0, 0.0, -0.3, 0.3, -2.5, 2.5, 0.49999997, -0.49999997, 8388609.0, -8388609.0, 1.5, -1.5,
+              np.inf, -np.inf, np.nan, 1e-40], np.float32)
+
+
+def rounding_inputs(dtype=np.float32):
+    return dtypes.from_float(R) if dtypes.is_bf16(dtype) else R.copy()
+
+
+def rounding_call(dtype=np.float32):
+    def kernel(x_ref, r_ref, e_ref, s_ref, f_ref, c_ref):
+        x = x_ref[...]
+        r_ref[...] = lax.round(x)  # away from zero
+        e_ref[...] = jnp.round(x)  # ties to even
+        s_ref[...] = jnp.sign(x)
+        f_ref[...] = jnp.floor(x)
+        c_ref[...] = jnp.ceil(x)
+
+    shp = pl.ShapeDtypeStruct((N,), dtype)
+    return pa.hip_call(kernel, out_shape=(shp,) * 5, math_mode="safe")
+
+
+def rounding_expected():
+    """C roundf (halves away from zero, signed zeros kept), rintf (ties to
+    even), sign keeping
+    zeros and NaN, floorf/ceilf: written out with Python's exact math."""
+    import math
+
+    def rnd(v):
+        if not math.isfinite(v) or v == 0:
+            return v
+        t = math.trunc(v)
+        r = t + (math.copysign(1.0, v) if abs(v - t) >= 0.5 else 0.0)
+        return math.copysign(r, v) if r == 0 else r
+
+    def even(v):
+        if not math.isfinite(v) or v == 0:
+            return v
+        t = math.floor(v)
+        d = v - t
+        r = t + 1 if (d > 0.5 or (d == 0.5 and t % 2 == 1)) else t
+        return math.copysign(float(r), v) if r == 0 else float(r)
+
+    def sgn(v):
+        return v if (v == 0 or math.isnan(v)) else math.copysign(1.0, v)
+
+    def fl(v, f):
+        if not math.isfinite(v):
+            return v
+        r = float(f(v))
+        return math.copysign(r, v) if r == 0 else r
+
+    xs = [float(v) for v in R]
+    return (np.array([rnd(v) for v in xs], np.float32), np.array([even(v) for v in xs], np.float32),
+            np.array([sgn(v) for v in xs], np.float32),
+            np.array([fl(v, math.floor) for v in xs], np.float32), np.array([fl(v, math.ceil) for v in xs], np.float32))

@@ -18,3 +18,11 @@ def test_signed_zero_min_max_bit_exact(dt):
     args = zc.inputs(dt)
     for g, w in zip(f(*args), f.interpret(*args)):
         np.testing.assert_array_equal(np.ascontiguousarray(g).view(np.uint8), np.ascontiguousarray(w).view(np.uint8))
+
+
+@pytest.mark.parametrize("dt", [np.float32, dtypes.bfloat16], ids=["f32", "bf16"])
+def test_round_sign_floor_ceil_bit_exact(dt):
+    f = zc.rounding_call(dt)
+    x = zc.rounding_inputs(dt)
+    for g, w in zip(f(x), f.interpret(x)):
+        np.testing.assert_array_equal(np.ascontiguousarray(g).view(np.uint8), np.ascontiguousarray(w).view(np.uint8))

@@ -105,3 +105,14 @@ def test_min_max_order_negative_zero_below_positive_zero():
             g = dtypes.to_float(g) if dtypes.is_bf16(g.dtype) else g
             np.testing.assert_array_equal(np.signbit(g), np.signbit(w))
             np.testing.assert_array_equal(g, w)
+
+
+def test_round_sign_floor_ceil_edge_values():
+    """roundf (away), rintf (even), sign with signed zeros and NaN kept,
+    floorf/ceilf: zeros, halves, 0.49999997, odd integers past 2^23, inf."""
+    import signed_zero_cases as zc
+
+    got = zc.rounding_call().interpret(zc.rounding_inputs())
+    for g, w in zip(got, zc.rounding_expected()):
+        np.testing.assert_array_equal(g, w)
+        np.testing.assert_array_equal(np.signbit(g), np.signbit(w))
