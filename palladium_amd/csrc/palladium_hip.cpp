@@ -56,6 +56,9 @@ std::vector<std::string> build_options(int math_mode, const char *arch) {
   o.push_back(std::string("--offload-arch=") + (arch && *arch ? arch : "gfx950"));
   o.push_back("-O3");
   o.push_back("-std=c++17");
+  // Signed integer arithmetic wraps (two's complement), as jnp int32 does;
+  // without this an overflowing hash multiply would be undefined behaviour.
+  o.push_back("-fwrapv");
   // Packed FP32 VALU forms are kept out of every code object.
   o.push_back("-Xclang");
   o.push_back("-target-feature");

@@ -69,6 +69,24 @@ __device__ __forceinline__ float ph_cos(float x) { return cosf(x); }
 __device__ __forceinline__ float ph_exp(float x) { return expf(x); }
 #endif
 
+/* Integer division and float->integer conversion with every input defined,
+   as XLA's elemental emitter defines them: x / 0 = -1 (all ones unsigned),
+   x % 0 = x, INT_MIN / -1 = INT_MIN, INT_MIN % -1 = 0; conversions
+   saturate and send NaN to 0. (C leaves all of these undefined.) */
+__device__ __forceinline__ int ph_idiv(int a, int b) {
+    return b == 0 ? -1 : (b == -1 ? (int)(0u - (unsigned int)a) : a / b);
+}
+__device__ __forceinline__ int ph_irem(int a, int b) { return (b == 0) ? a : (b == -1 ? 0 : a % b); }
+__device__ __forceinline__ unsigned int ph_udiv(unsigned int a, unsigned int b) { return b == 0u ? 0xFFFFFFFFu : a / b; }
+__device__ __forceinline__ unsigned int ph_urem(unsigned int a, unsigned int b) { return b == 0u ? a : a % b; }
+__device__ __forceinline__ int ph_f2i(float x) {
+    return x != x ? 0 : (x >= 2147483648.0f ? 2147483647 : (x <= -2147483648.0f ? (-2147483647 - 1) : (int)x));
+}
+__device__ __forceinline__ unsigned int ph_f2u(float x) {
+    return x != x ? 0u : (x >= 4294967296.0f ? 0xFFFFFFFFu : (x <= 0.0f ? 0u : (unsigned int)x));
+}
+__device__ __forceinline__ int ph_iabs(int a) { return a < 0 ? (int)(0u - (unsigned int)a) : a; }
+
 __device__ __forceinline__ float ph_fmin(float a, float b) { return fminf(a, b); }
 __device__ __forceinline__ float ph_fmax(float a, float b) { return fmaxf(a, b); }
 

@@ -74,9 +74,13 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
     if opname == "mul":
         return "({a} * {b})"
     if opname == "div":
-        return "({a} / {b})"
+        if f:
+            return "({a} / {b})"
+        return "ph_udiv({a}, {b})" if out_ctype == "unsigned int" else "ph_idiv({a}, {b})"
     if opname == "rem":
-        return "fmodf({a}, {b})" if f else "({a} % {b})"
+        if f:
+            return "fmodf({a}, {b})"
+        return "ph_urem({a}, {b})" if out_ctype == "unsigned int" else "ph_irem({a}, {b})"
     if opname == "min":
         return "ph_fmin({a}, {b})" if f else "(({a} < {b}) ? {a} : {b})"
     if opname == "max":
@@ -86,7 +90,9 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
     if opname == "neg":
         return "(-{a})"
     if opname == "abs":
-        return "fabsf({a})" if f else "abs({a})"
+        if f:
+            return "fabsf({a})"
+        return "({a})" if out_ctype == "unsigned int" else "ph_iabs({a})"
     if opname == "sign":
         return "(({a} > 0.0f) ? 1.0f : (({a} < 0.0f) ? -1.0f : {a}))" if f else "(({a} > 0) - ({a} < 0))"
     unary_f = {
@@ -196,6 +202,9 @@ def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
         template = f"(({dst_ctype}){{a}})"
         if dst_ctype == "bool":
             template = "({a} != 0)"
+        elif dst_ctype in ("int", "unsigned int") and ops[0].ctype in FLOAT_CTYPES:
+            # saturating, NaN -> 0 (a plain cast is undefined out of range)
+            template = ("ph_f2u" if dst_ctype == "unsigned int" else "ph_f2i") + "((float){a})"
         elif dst_ctype == BF16 and ops[0].ctype not in (F32, BF16):
             # integers and float16 reach bfloat16 through float32 (one rule
             # for device and interpreter)

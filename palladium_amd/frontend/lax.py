@@ -36,7 +36,6 @@ from palladium_amd.ir import ClosedJaxpr, Jaxpr, ShapedArray
 add = jnp.add
 sub = jnp.subtract
 mul = jnp.multiply
-div = jnp.divide
 max = jnp.maximum  # noqa: A001
 min = jnp.minimum  # noqa: A001
 neg = jnp.negative
@@ -76,6 +75,17 @@ transpose = jnp.transpose
 
 def dot(lhs: Any, rhs: Any, precision: Any = None, preferred_element_type: Any = None) -> Tracer:
     return jnp.dot(lhs, rhs, precision=precision, preferred_element_type=preferred_element_type)
+
+
+def div(a: Any, b: Any) -> Tracer:
+    """lax.div: dtype-preserving; integers truncate toward zero (x / 0 and
+    INT_MIN / -1 are defined as XLA defines them), floats divide."""
+    return jnp._nary("div", a, b)
+
+
+def rem(a: Any, b: Any) -> Tracer:
+    """lax.rem: remainder with the dividend's sign (C fmod for floats)."""
+    return jnp._nary("rem", a, b)
 
 
 def round(x: Any, rounding_method: int = 0) -> Tracer:  # noqa: A001

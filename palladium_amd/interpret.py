@@ -174,6 +174,38 @@ def _fold(op: Any, src: np.ndarray, axes: tuple[int, ...]) -> np.ndarray:
     return acc
 
 
+def _int_div(a: Any, b: Any, dt: np.dtype) -> np.ndarray:
+    """Integer division truncating toward zero, defined everywhere as XLA
+    defines it: x / 0 = -1 (all ones unsigned), INT_MIN / -1 = INT_MIN."""
+    a64 = np.asarray(a).astype(np.int64)
+    b64 = np.asarray(b).astype(np.int64)
+    safe = np.where(b64 == 0, 1, b64)
+    q = np.abs(a64) // np.abs(safe) * np.sign(a64) * np.sign(safe)
+    q = np.where(b64 == 0, -1, q)
+    return (q & 0xFFFFFFFF).astype(np.uint32).view(np.int32).astype(dt) if dt.kind == "i" else \
+        (q & 0xFFFFFFFF).astype(np.uint32).astype(dt)
+
+
+def _int_rem(a: Any, b: Any, dt: np.dtype) -> np.ndarray:
+    """Remainder with the sign of the dividend; x % 0 = x and
+    INT_MIN % -1 = 0."""
+    a64 = np.asarray(a).astype(np.int64)
+    b64 = np.asarray(b).astype(np.int64)
+    safe = np.where(b64 == 0, 1, b64)
+    r = np.abs(a64) % np.abs(safe) * np.sign(a64)
+    r = np.where(b64 == 0, a64, r)
+    return r.astype(dt)
+
+
+def _float_to_int(a: Any, dt: np.dtype) -> np.ndarray:
+    """Truncating float -> int32/uint32 conversion that saturates and maps
+    NaN to 0 (C leaves out-of-range values undefined)."""
+    x = np.asarray(a).astype(np.float64)
+    info = np.iinfo(dt)
+    x = np.where(np.isnan(x), 0.0, np.clip(np.trunc(x), info.min, info.max))
+    return x.astype(dt)
+
+
 def _round_half_away(x):
     """C roundf: nearest integer, halves away from zero, zeros keep their
     sign. Exact: x - trunc(x) is representable, so nothing rounds on the way
@@ -209,9 +241,9 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
         elif name == "mul":
             r = a * b
         elif name == "div":
-            r = a / b if isf else np.trunc(a.astype(np.float64) / b).astype(dt)
+            r = a / b if isf else _int_div(a, b, dt)
         elif name == "rem":
-            r = np.fmod(a, b)
+            r = np.fmod(a, b) if isf else _int_rem(a, b, dt)
         elif name == "min":
             r = _fmin(a, b) if isf else np.minimum(a, b)
         elif name == "max":
@@ -250,7 +282,8 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
             sb = np.asarray(b).astype(np.uint32)
             r = np.where(sb < 32, ua >> np.minimum(sb, 31), 0).astype(dt)
         elif name == "shift_right_arithmetic":
-            sb = np.asarray(b).astype(np.int64)
+            # the amount is taken as unsigned: negative or >= 32 fills with the sign
+            sb = np.asarray(b).astype(np.uint32).astype(np.int64)
             r = (np.asarray(a) >> np.minimum(sb, 31)).astype(dt)
         elif name == "shift_left":
             sb = np.asarray(b).astype(np.uint32)
@@ -278,7 +311,12 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
                 if y < 0:
                     r = np.asarray(1.0, r.dtype) / r
         elif name == "convert_element_type":
-            r = (np.asarray(a) != 0) if dt == np.bool_ else np.asarray(a).astype(dt)
+            if dt == np.bool_:
+                r = np.asarray(a) != 0
+            elif dt.kind in "iu" and np.asarray(a).dtype.kind == "f":
+                r = _float_to_int(a, dt)
+            else:
+                r = np.asarray(a).astype(dt)
         elif name == "bitcast_convert_type":
             if bf_out:  # float16 bits -> bfloat16
                 r = f32_from_bits(np.ascontiguousarray(np.asarray(a)).view(np.uint16))

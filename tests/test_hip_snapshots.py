@@ -140,7 +140,7 @@ def test_emitted_hip_matches_golden(name):
     spec = build()
     hip = _body(emit_hip(spec, math_mode=mode))
     path = GOLDEN / f"{name}.hip.golden"
-    if os.environ.get("PALLADIUM_REGEN_GOLDEN"):
+    if os.environ.get("PALLADIUM_REGEN_GOLDEN") == "1":
         path.write_text(hip)
         pytest.skip(f"regenerated {path.name}")
     assert path.exists(), f"missing snapshot {path.name}; bless it with PALLADIUM_REGEN_GOLDEN=1"
