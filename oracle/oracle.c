@@ -230,7 +230,7 @@ float oracle_pow(float x, float y) {
     if (ax == 1.0f) return 1.0f;
     return ((ax > 1.0f) == (y > 0.0f)) ? INFINITY : 0.0f;
   }
-  float sign = (x < 0.0f && y_odd) ? -1.0f : 1.0f;
+  float sign = (signbit(x) && y_odd) ? -1.0f : 1.0f; /* -0 too: pow(-0, 3) = -0 */
   if (ax == 0.0f) return (y < 0.0f) ? sign * INFINITY : sign * 0.0f;
   if (ax == INFINITY) return (y < 0.0f) ? sign * 0.0f : sign * INFINITY;
   double z = (double)y * ph_ln_pos((double)ax);

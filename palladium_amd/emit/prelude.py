@@ -87,6 +87,9 @@ __device__ __forceinline__ unsigned int ph_f2u(float x) {
 }
 __device__ __forceinline__ int ph_iabs(int a) { return a < 0 ? (int)(0u - (unsigned int)a) : a; }
 
+/* expm1 with C99's expm1(-0) = -0 (the device library returns +0). */
+__device__ __forceinline__ float ph_expm1(float x) { return x == 0.0f ? x : expm1f(x); }
+
 __device__ __forceinline__ float ph_fmin(float a, float b) { return fminf(a, b); }
 __device__ __forceinline__ float ph_fmax(float a, float b) { return fmaxf(a, b); }
 
@@ -152,7 +155,7 @@ __device__ __noinline__ float ph_pow(float x, float y) {
         if (ax == 1.0f) return 1.0f;
         return ((ax > 1.0f) == (y > 0.0f)) ? __builtin_inff() : 0.0f;
     }
-    float sign = (x < 0.0f && y_odd) ? -1.0f : 1.0f;
+    float sign = (__builtin_signbit(x) && y_odd) ? -1.0f : 1.0f; /* -0 too: pow(-0, 3) = -0 */
     if (ax == 0.0f) return (y < 0.0f) ? sign * __builtin_inff() : sign * 0.0f;
     if (ax == __builtin_inff()) return (y < 0.0f) ? sign * 0.0f : sign * __builtin_inff();
     double z = (double)y * ph_ln_pos((double)ax);

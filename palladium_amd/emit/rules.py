@@ -100,7 +100,7 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
         "exp2": "exp2f({a})",
         "log": "logf({a})",
         "log1p": "log1pf({a})",
-        "expm1": "expm1f({a})",
+        "expm1": "ph_expm1({a})",
         "sin": "ph_sin({a})",
         "cos": "ph_cos({a})",
         "tan": "tanf({a})",

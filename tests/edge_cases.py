@@ -128,3 +128,51 @@ def same(g, w):
             return False
         g, w = g[~nan], w[~nan]
     return np.array_equal(np.ascontiguousarray(g).view(np.uint8), np.ascontiguousarray(w).view(np.uint8))
+
+
+TRANSCENDENTAL = {
+    "exp": lambda x, y: jnp.exp(x),
+    "exp2": lambda x, y: jnp.exp2(x),
+    "expm1": lambda x, y: jnp.expm1(x),
+    "log": lambda x, y: jnp.log(x),
+    "log1p": lambda x, y: jnp.log1p(x),
+    "sin": lambda x, y: jnp.sin(x),
+    "cos": lambda x, y: jnp.cos(x),
+    "tan": lambda x, y: jnp.tan(x),
+    "tanh": lambda x, y: jnp.tanh(x),
+    "rsqrt": lambda x, y: lax.rsqrt(x),
+    "logistic": lambda x, y: jax_logistic(x),
+    "atan2": lambda x, y: jnp.arctan2(x, y),
+    "pow": lambda x, y: x ** y,
+}
+
+
+def jax_logistic(x):
+    return jnp.logistic(x) if hasattr(jnp, "logistic") else 1.0 / (1.0 + jnp.exp(-x))
+
+
+def transcendental_call(n):
+    names = list(TRANSCENDENTAL)
+
+    def kernel(x_ref, y_ref, *outs):
+        x, y = x_ref[...], y_ref[...]
+        for o, f in zip(outs, TRANSCENDENTAL.values()):
+            o[...] = f(x, y)
+
+    return names, _gridless(kernel, n, [np.float32] * len(names))
+
+
+def close(g, w, ulps=4):
+    """Special results (NaN, infinities, zeros with their sign) equal;
+    finite nonzero results within `ulps` float32 ulps."""
+    g = np.asarray(g, np.float32)
+    w = np.asarray(w, np.float32)
+    if not np.array_equal(np.isnan(g), np.isnan(w)):
+        return False
+    m = ~np.isnan(w)
+    g, w = g[m], w[m]
+    special = np.isinf(w) | (w == 0) | np.isinf(g) | (g == 0)
+    if not np.array_equal(g[special].view(np.uint32), w[special].view(np.uint32)):
+        return False
+    g, w = g[~special].astype(np.float64), w[~special].astype(np.float64)
+    return bool(np.all(np.abs(g - w) <= ulps * np.spacing(np.abs(w).astype(np.float32)).astype(np.float64)))

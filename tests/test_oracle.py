@@ -131,10 +131,15 @@ def test_pow_within_one_ulp_of_libm():
 @pytest.mark.parametrize(
     "x,y,want",
     [(2.0, 10.0, 1024.0), (4.0, 0.5, 2.0), (0.0, 2.0, 0.0), (0.0, -1.0, np.inf), (-2.0, 3.0, -8.0),
-     (1.0, np.nan, 1.0), (5.0, 0.0, 1.0), (np.inf, -1.0, 0.0), (0.5, np.inf, 0.0)],
+     (1.0, np.nan, 1.0), (5.0, 0.0, 1.0), (np.inf, -1.0, 0.0), (0.5, np.inf, 0.0),
+     # signed zeros and infinities with odd/even/non-integer exponents (C99 F.9.4.4)
+     (-0.0, 3.0, -0.0), (-0.0, -1.0, -np.inf), (-0.0, 2.0, 0.0), (-0.0, -2.0, np.inf), (-0.0, 0.5, 0.0),
+     (-0.0, -0.5, np.inf), (-np.inf, 3.0, -np.inf), (-np.inf, -3.0, -0.0), (-np.inf, 2.0, np.inf),
+     (0.0, -np.inf, np.inf), (-1.0, np.inf, 1.0)],
 )
 def test_pow_special_cases(x, y, want):
-    assert oracle.pow32(x, y) == np.float32(want)
+    got = oracle.pow32(x, y)
+    assert got == np.float32(want) and np.signbit(got) == np.signbit(want), (x, y, got, want)
 
 
 def test_pow_negative_base_fraction_is_nan():
