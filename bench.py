@@ -581,6 +581,16 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
                        "ops_note": "elementwise eqns of the while condition + body per attempt (pow = 1)",
                        "avg_launch_ms": avg, "active_lane_fraction": active, "total_attempts": total,
                        "accepted": int(acc.sum()), "rejected": int(rej.sum())}
+    # SAFE: the mode whose accepted/rejected counts equal the oracle's exactly
+    # (IEEE order, deterministic pow); FAST above is the throughput mode.
+    safe_bound = bs3_vdp_call(cfg.n, math_mode="safe").bound(*host)
+    safe_outs = [rt.Buffer.empty((cfg.n,), np.float32) for _ in range(3)] + \
+        [rt.Buffer.empty((cfg.n,), np.int32) for _ in range(2)]
+    sms, savg = _timed_launches(safe_bound, ins + safe_outs, steps, warmup)
+    sacc = safe_outs[3].to_numpy().astype(np.int64)
+    srej = safe_outs[4].to_numpy().astype(np.int64)
+    res["safe"] = {"ms_per_step": sms, "attempts_per_s": float((sacc + srej).sum()) / (sms / 1e3),
+                   "accepted": int(sacc.sum()), "rejected": int(srej.sum())}
     if cpu:
         import oracle
 
@@ -590,6 +600,11 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
         dt = time.perf_counter() - t0
         res["cpu_baseline"] = {"value": float((a2[3].astype(np.int64) + a2[4]).sum() / dt), "unit": "attempts/s",
                                "cores": _cpu_cores(), "kind": "port", "sample": f"first {n_cpu} trajectories, C oracle, {dt:.2f} s"}
+        res["safe"]["counts_equal_oracle"] = {
+            "sample": f"first {n_cpu} trajectories",
+            "accepted": bool(np.array_equal(sacc[:n_cpu], a2[3])),
+            "rejected": bool(np.array_equal(srej[:n_cpu], a2[4])),
+        }
     return res
 
 
@@ -864,7 +879,7 @@ def main() -> int:
                         ("bs3_vdp", bench_bs3), ("lv_rk4_df32", bench_df32)):
             r = fn(a.steps, a.warmup, cpu=False)
             res["secondary"][key] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline",
-                                                        "accuracy", "accepted_steps_per_s", "price") if k in r}
+                                                        "accuracy", "accepted_steps_per_s", "price", "safe") if k in r}
     if rank == 0:
         print(json.dumps(res), flush=True)
     return 0

@@ -94,7 +94,7 @@ __device__ __forceinline__ float ph_fmin(float a, float b) { return fminf(a, b);
 __device__ __forceinline__ float ph_fmax(float a, float b) { return fmaxf(a, b); }
 
 #if PH_MATH_MODE == 0
-__device__ __noinline__ double ph_ln_pos(double x) {
+__device__ __forceinline__ double ph_ln_pos(double x) {
     int e;
     double m = frexp(x, &e);          /* x = m 2^e, m in [0.5, 1) */
     if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
@@ -119,7 +119,7 @@ __device__ __noinline__ double ph_ln_pos(double x) {
     return fma(de, ln2_hi, fma(de, ln2_lo, lnm));
 }
 
-__device__ __noinline__ double ph_exp_dbl(double z) {
+__device__ __forceinline__ double ph_exp_dbl(double z) {
     const double inv_ln2 = 1.44269504088896338700e+00;
     const double ln2_hi = 6.93147180369123816490e-01;
     const double ln2_lo = 1.90821492927058770002e-10;
@@ -143,7 +143,7 @@ __device__ __noinline__ double ph_exp_dbl(double z) {
     return ldexp(p, (int)kd);
 }
 
-__device__ __noinline__ float ph_pow(float x, float y) {
+__device__ __forceinline__ float ph_pow(float x, float y) {
     if (y == 0.0f || x == 1.0f) return 1.0f;
     if (x != x || y != y) return x + y;
     float ax = fabsf(x);
