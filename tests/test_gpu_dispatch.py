@@ -120,6 +120,47 @@ def test_ph_dispatch_c_abi_host_buffers(rng):
     rt.lib().ph_free_error(err)
 
 
+def test_ph_dispatch_concurrent_callers():
+    """XLA:CPU calls the handler from its thread pool: 8 threads dispatch
+    through ph_dispatch at once, each with its own inputs and sizes (the
+    per-thread staging grows), 20 calls each; every result is its own."""
+    sizes = [257, 1000, 4096, 64, 3000, 777, 12345, 511]
+    srcs = {}
+    for n in set(sizes):
+        f = _inc(n)
+        spec = pa.trace(f._staged, np.zeros(n, F))
+        srcs[n] = (emit_hip(spec).encode(), spec.name.encode())
+    errors = []
+
+    def worker(t):
+        try:
+            r = np.random.default_rng(t)
+            for k in range(20):
+                n = sizes[(t + k) % len(sizes)]
+                src, name = srcs[n]
+                x = r.standard_normal(n).astype(F)
+                out = np.empty(n, F)
+                ins = (ctypes.c_void_p * 1)(x.ctypes.data)
+                in_b = (ctypes.c_size_t * 1)(x.nbytes)
+                outs = (ctypes.c_void_p * 1)(out.ctypes.data)
+                out_b = (ctypes.c_size_t * 1)(out.nbytes)
+                err = ctypes.c_void_p()
+                rc = rt.lib().ph_dispatch(src, len(src), name, n, 1, 1, 256, 1, 0, ins, in_b, 1, outs, out_b, 1,
+                                          ctypes.byref(err))
+                if rc != 0 or not np.array_equal(out, x + 1.0):
+                    errors.append((t, k, n, rc))
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append((t, repr(e)))
+
+    ts = [threading.Thread(target=worker, args=(t,)) for t in range(8)]
+    for th in ts:
+        th.start()
+    for th in ts:
+        th.join(timeout=60)
+    assert not any(th.is_alive() for th in ts)
+    assert not errors, errors[:5]
+
+
 def _lane_kernel_attrs(rng):
     """A lane-parallel kernel ((128, 8) @ (8, 4) blocks, one row per lane)
     and the FFI attributes hip_call_jit would bake into the HLO."""
