@@ -212,12 +212,13 @@ def reshape(x: Tracer, new_sizes: Sequence[int]) -> Tracer:
 
 def dot_general(lhs: Any, rhs: Any, dimension_numbers: Any, precision: Any = None,
                 preferred_element_type: Any = None) -> Tracer:
-    """Stage `dot_general` as JAX does: output dims are the lhs free dims,
-    then the rhs free dims (batch dims are not supported)."""
+    """Stage `dot_general` as JAX does: output dims are the batch dims, then
+    the lhs free dims, then the rhs free dims. (Batch dims stage like JAX's
+    and are rejected by the emitter, as the reference's emitter does.)"""
     (lc, rc), (lb, rb) = dimension_numbers
     lc, rc, lb, rb = (tuple(int(d) for d in t) for t in (lc, rc, lb, rb))
-    if lb or rb:
-        raise TraceError("dot_general: batch dimensions are not supported")
+    if len(lb) != len(rb):
+        raise TraceError("dot_general: lhs and rhs batch dims differ in number")
     if not isinstance(lhs, Tracer):
         lhs = asarray(lhs)
     if not isinstance(rhs, Tracer):
@@ -230,10 +231,10 @@ def dot_general(lhs: Any, rhs: Any, dimension_numbers: Any, precision: Any = Non
     if rhs.dtype != dt:
         rhs = convert_element_type(rhs, dt)
     out_dt = np.dtype(preferred_element_type) if preferred_element_type is not None else dt
-    shape = tuple(d for k, d in enumerate(lhs.shape) if k not in lc) + tuple(
-        d for k, d in enumerate(rhs.shape) if k not in rc)
+    shape = tuple(lhs.shape[k] for k in lb) + tuple(d for k, d in enumerate(lhs.shape) if k not in lc + lb) + tuple(
+        d for k, d in enumerate(rhs.shape) if k not in rc + rb)
     return _stage("dot_general", [lhs, rhs], shape, out_dt, False,
-                  dimension_numbers=((lc, rc), ((), ())), precision=precision,
+                  dimension_numbers=((lc, rc), (lb, rb)), precision=precision,
                   preferred_element_type=out_dt, out_sharding=None)
 
 

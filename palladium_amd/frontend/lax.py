@@ -269,41 +269,56 @@ def fori_loop(lower: Any, upper: Any, body_fun: Callable, init_val: Any, *, unro
 
 
 def scan(f: Callable, init: Any, xs: Any = None, length: int | None = None, reverse: bool = False, unroll: int = 1) -> tuple[Any, Any]:
-    """Pure-carry `lax.scan` (`xs=None`, no stacked ys), the only form
-    the emitter lowers (`src/palladium/emit/rules.py:717-738`)."""
-    if xs is not None:
-        raise TraceError("lax.scan with scanned xs not supported, use lax.fori_loop")
+    """`lax.scan`, staged as JAX stages it: consts, carries, then scanned
+    xs as invars; carries then stacked ys as outvars. The emitter lowers
+    the pure-carry form (`xs=None`, no ys) and rejects the others with the
+    reference's messages (`src/palladium/emit/rules.py:717-738`)."""
     if reverse:
         raise TraceError("no reverse-mode scan support, use lax.fori_loop")
+    x_leaves, x_struct = _flatten(xs) if xs is not None else ([], None)
+    x_leaves = [_to_tracer(x) for x in x_leaves]
+    if x_leaves:
+        n = x_leaves[0].shape[0] if x_leaves[0].shape else None
+        if n is None or any(not x.shape or x.shape[0] != n for x in x_leaves):
+            raise TraceError("lax.scan xs must share a leading dim")
+        if length is not None and int(length) != n:
+            raise TraceError(f"lax.scan length={length} disagrees with xs leading dim {n}")
+        length = n
     if length is None:
         raise TraceError("lax.scan without xs needs length=")
     leaves, struct = _flatten(init)
     leaves = [_to_tracer(x) for x in leaves]
     avals = _avals(leaves)
+    x_avals = [ShapedArray(tuple(x.shape[1:]), x.dtype, x.weak_type) for x in x_leaves]
     for _ in range(3):
         b = Builder(current_builder())
         with building(b):
             args = [b.arg(a) for a in avals]
-            res = f(_unflatten(struct, args), None)
+            xargs = [b.arg(a) for a in x_avals]
+            res = f(_unflatten(struct, args), _unflatten(x_struct, xargs) if x_leaves else None)
             if not (isinstance(res, tuple) and len(res) == 2):
                 raise TraceError("scan body must return (carry, y)")
             carry, y = res
-            if y is not None:
-                raise TraceError("lax.scan with stacked ys not supported, use lax.fori_loop")
             new_leaves, _ = _flatten(carry)
+            y_leaves, y_struct = _flatten(y) if y is not None else ([], None)
+            y_leaves = [_to_tracer(v) for v in y_leaves]
         avals2, changed = _match_carry(new_leaves, avals, "scan")
         if not changed:
             break
         avals = avals2
     new_leaves = _coerce_out(b, new_leaves, avals)
-    body = closed(b, new_leaves)
+    body = closed(b, new_leaves + y_leaves)
+    # closed() puts captured consts first; the scanned xs follow the carries
     consts = b.captured_outer()
     params = dict(
         reverse=False, length=int(length), jaxpr=body, num_consts=len(consts), num_carry=len(avals),
-        linear=tuple([False] * (len(consts) + len(avals))), unroll=int(unroll), _split_transpose=False,
+        linear=tuple([False] * (len(consts) + len(avals) + len(x_leaves))), unroll=int(unroll),
+        _split_transpose=False,
     )
-    outs = current_builder().add("scan", [*consts, *_coerce_init(leaves, avals)], avals, **params)
-    return _unflatten(struct, outs), None
+    y_avals = [ShapedArray((int(length),) + tuple(v.shape), v.dtype, False) for v in y_leaves]
+    outs = current_builder().add("scan", [*consts, *_coerce_init(leaves, avals), *x_leaves], avals + y_avals, **params)
+    ys = _unflatten(y_struct, outs[len(avals):]) if y_leaves else None
+    return _unflatten(struct, outs[: len(avals)]), ys
 
 
 def while_loop(cond_fun: Callable, body_fun: Callable, init_val: Any) -> Any:

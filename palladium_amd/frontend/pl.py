@@ -16,6 +16,7 @@ from __future__ import annotations
 import dataclasses
 import math
 import threading
+from builtins import max as builtins_max
 from builtins import min as builtins_min
 from typing import Any, Callable, Sequence
 
@@ -172,8 +173,10 @@ class Ref:
         b = current_builder()
         for d, (i, n) in enumerate(zip(idx, shape)):
             if isinstance(i, slice):
-                if i.step not in (None, 1):
-                    raise TraceError(f"ref access dim {d}: stride {i.step} != 1 is unimplemented")
+                step = 1 if i.step is None else i.step
+                if isinstance(step, Tracer) or int(step) < 1:
+                    raise TraceError(f"ref access dim {d}: step {i.step} must be a positive int")
+                step = int(step)
                 start = 0 if i.start is None else i.start
                 stop = n if i.stop is None else i.stop
                 if isinstance(start, Tracer) or isinstance(stop, Tracer):
@@ -181,7 +184,8 @@ class Ref:
                 start, stop = int(start), int(stop)
                 start = start + n if start < 0 else start
                 stop = stop + n if stop < 0 else builtins_min(stop, n)
-                out.append(Slice(start, stop - start, 1))
+                # a strided window stages as JAX's does; the emitter rejects it
+                out.append(Slice(start, builtins_max(0, -(-(stop - start) // step)), step))
             elif isinstance(i, Slice):
                 st = i.start
                 if isinstance(st, Tracer):

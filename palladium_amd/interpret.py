@@ -481,7 +481,9 @@ def _dot_general(eqn: JaxprEqn, lhs: Any, rhs: Any, n: int) -> np.ndarray:
     """Contraction accumulated in k order from zero in the output dtype,
     `acc = acc + a*b`, the operation sequence the emitter produces
     (bfloat16: accumulated in float32, rounded once)."""
-    (lc, rc), _ = eqn.params["dimension_numbers"]
+    (lc, rc), (lb, rb) = eqn.params["dimension_numbers"]
+    if tuple(lb) or tuple(rb):
+        raise EmitError("dot_general: batch dims are unimplemented")
     bf = is_bf16(eqn.outvars[0].aval.dtype)
     out_dt = np.dtype(np.float32) if bf else np.dtype(eqn.outvars[0].aval.dtype)
     la, ra = eqn.invars[0].aval, eqn.invars[1].aval
@@ -516,6 +518,11 @@ def _scan(eqn: JaxprEqn, env: _Env, mask: np.ndarray) -> None:
     nconst = len(eqn.invars) - nc
     if eqn.params.get("reverse", False):
         raise EmitError("no reverse-mode scan support, use lax.fori_loop")
+    n_carry = int(eqn.params.get("num_carry", nc))
+    if nc != n_carry:
+        raise EmitError("lax.scan with stacked ys not supported, use lax.fori_loop")
+    if int(eqn.params.get("num_consts", nconst)) != nconst:
+        raise EmitError("lax.scan with scanned xs not supported, use lax.fori_loop")
     consts = [env.read(a) for a in eqn.invars[:nconst]]
     carries = [_full(env.read(a), ov.aval, env.n) for a, ov in zip(eqn.invars[nconst:], eqn.outvars)]
     for _ in range(int(eqn.params["length"])):
