@@ -175,4 +175,6 @@ def close(g, w, ulps=4):
     if not np.array_equal(g[special].view(np.uint32), w[special].view(np.uint32)):
         return False
     g, w = g[~special].astype(np.float64), w[~special].astype(np.float64)
-    return bool(np.all(np.abs(g - w) <= ulps * np.spacing(np.abs(w).astype(np.float32)).astype(np.float64)))
+    with np.errstate(over="ignore"):  # spacing of the largest finite float
+        ulp = np.spacing(np.abs(w).astype(np.float32)).astype(np.float64)
+    return bool(np.all(np.abs(g - w) <= ulps * ulp))
