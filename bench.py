@@ -128,6 +128,14 @@ def bench_lv(steps: int, warmup: int, cpu: bool, cfg=None, block: int = 1, track
             "avg_launch_ms": avg_launch_s * 1e3,
         },
     }
+    # SAFE (IEEE op order, no contraction): the mode that reproduces the C
+    # oracle bit for bit; FAST above is the throughput mode.
+    safe_outs = None
+    if cfg is LV_CFG1:
+        safe_bound = lv_rk4_call(n, cfg.dt, cfg.steps, track_max=track_max, block=block, math_mode="safe").bound(*host)
+        safe_outs = [rt.Buffer.empty((n,), np.float32) for _ in outs]
+        sms, _ = _timed_launches(safe_bound, [*ins, *safe_outs], max(1, steps // 4), 1)
+        result["safe"] = {"ms_per_step": sms, "value": traj_steps / (sms / 1e3), "unit": "trajectory-steps/s"}
     if cpu:
         import oracle
 
@@ -137,8 +145,14 @@ def bench_lv(steps: int, warmup: int, cpu: bool, cfg=None, block: int = 1, track
         sample = tuple(a[:n_cpu] for a in host)
         oracle.lv_rk4(*(a[:64] for a in host), cfg.dt, 10, track_max=track_max)  # load + warm
         t0 = time.perf_counter()
-        oracle.lv_rk4(*sample, cfg.dt, cfg.steps, track_max=track_max)
+        want = oracle.lv_rk4(*sample, cfg.dt, cfg.steps, track_max=track_max)
         dt_cpu = time.perf_counter() - t0
+        if safe_outs is not None:
+            got = [b.to_numpy() for b in safe_outs]
+            result["safe"]["bit_exact_vs_oracle"] = {
+                "trajectories": n_cpu,
+                "equal": bool(all(np.array_equal(g[:n_cpu], w) for g, w in zip(got, want))),
+            }
         result["cpu_baseline"] = {
             "value": n_cpu * cfg.steps / dt_cpu,
             "unit": "trajectory-steps/s",
