@@ -782,15 +782,13 @@ def _predicable(jaxpr: Any) -> bool:
     """A loop body that may run on lanes whose loop has already ended:
     no ref access (an index built from a finished lane's carries could
     leave its block; a store must not happen), no nested while (its trip
-    count could depend on those carries), no integer division (undefined
-    for a zero divisor in C++). Pure arithmetic, counted loops, conds and
-    RNG qualify."""
+    count could depend on those carries). Pure arithmetic (integer
+    division included: ph_idiv/ph_irem are defined for every input and do
+    not trap), counted loops, conds and RNG qualify."""
     j = getattr(jaxpr, "jaxpr", jaxpr)
     for e in j.eqns:
         name = e.primitive.name
         if name in ("get", "swap", "while", "lane_index", "lane_reduce"):
-            return False
-        if name in ("div", "rem") and np.dtype(e.outvars[0].aval.dtype).kind in "iub":
             return False
         for v in e.params.values():
             for sub in (v if isinstance(v, tuple) else (v,)):

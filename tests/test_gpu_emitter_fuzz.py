@@ -66,10 +66,14 @@ def _make_kernel(seed):
 
         a, b, c = lax.fori_loop(0, 5 + seed % 7, body, (v, x, y))
         k = lax.switch(pl.program_id(0) % 3, [lambda t: t * 2.0, lambda t: t - 1.0, lambda t: jnp.abs(t)], a)
-        n, w = lax.while_loop(lambda s: jnp.logical_and(s[0] < 3 + pl.program_id(0) % 4, s[1] < 50.0),
-                              lambda s: (s[0] + 1, s[1] * 1.5 + 1.0), (0, jnp.abs(b)))
+        # an integer carry hashed with division and remainder whose divisor
+        # passes through zero (n - 2 at n = 2): defined, so still predicated
+        n, w, h = lax.while_loop(lambda s: jnp.logical_and(s[0] < 3 + pl.program_id(0) % 4, s[1] < 50.0),
+                                 lambda s: (s[0] + 1, s[1] * 1.5 + 1.0,
+                                            (s[2] * 7 + s[0]) // (s[0] - 2) + lax.rem(s[2], s[0] - 2)),
+                                 (0, jnp.abs(b), pl.program_id(0) * 13 + 5))
         o_ref[...] = _tame(k + c * 0.5, dt)
-        p_ref[...] = w + n.astype(x.dtype)
+        p_ref[...] = w + n.astype(x.dtype) + (h % 16).astype(x.dtype) * 0.0625
 
     return kernel
 
