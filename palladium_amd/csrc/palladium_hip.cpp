@@ -59,6 +59,11 @@ std::vector<std::string> build_options(int math_mode, const char *arch) {
   // Signed integer arithmetic wraps (two's complement), as jnp int32 does;
   // without this an overflowing hash multiply would be undefined behaviour.
   o.push_back("-fwrapv");
+  // No SLP vectorisation: with packed FP32 disabled, SLP-packed float16
+  // code can reach an instruction-selection failure in the gfx950 backend
+  // ("Cannot select: v2f32 = bitcast", an abort inside hiprtc). The hot
+  // kernels compile to identical code either way.
+  o.push_back("-fno-slp-vectorize");
   // Packed FP32 VALU forms are kept out of every code object.
   o.push_back("-Xclang");
   o.push_back("-target-feature");

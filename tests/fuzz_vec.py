@@ -117,6 +117,8 @@ def make_inputs(seed, rows=512, dtype=F):
     x = rng.uniform(-3, 3, (rows, W)).astype(F)
     y = rng.uniform(-3, 3, (rows, W)).astype(F)
     k = rng.integers(-(2**31), 2**31 - 1, (rows, 1)).astype(np.int32)
-    if dtype is not F:
+    if dtypes.is_bf16(dtype):
         x, y = dtypes.from_float(x), dtypes.from_float(y)
+    elif np.dtype(dtype) != F:
+        x, y = x.astype(dtype), y.astype(dtype)
     return x, y, k

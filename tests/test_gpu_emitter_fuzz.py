@@ -93,16 +93,17 @@ def test_random_program_bit_exact_vs_interpreter(seed):
         np.testing.assert_array_equal(g, w)
 
 
+@pytest.mark.parametrize("dt", [dtypes.bfloat16, np.dtype(np.float16)], ids=["bf16", "f16"])
 @pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
-def test_random_program_bf16_bit_exact_vs_interpreter(seed):
+def test_random_program_narrow_float_bit_exact_vs_interpreter(seed, dt):
     n = 300
     rng = np.random.default_rng(200 + seed)
-    x = dtypes.from_float(rng.uniform(-3, 3, n).astype(F))
-    y = dtypes.from_float(rng.uniform(-3, 3, n).astype(F))
+    x, y = rng.uniform(-3, 3, n).astype(F), rng.uniform(-3, 3, n).astype(F)
+    x, y = (dtypes.from_float(x), dtypes.from_float(y)) if dtypes.is_bf16(dt) else (x.astype(dt), y.astype(dt))
     spec = pl.BlockSpec((1,), lambda i: (i,))
     call = pa.hip_call(_make_kernel(seed), grid=(n,), in_specs=[spec, spec], out_specs=(spec, spec),
-                       out_shape=(pl.ShapeDtypeStruct((n,), dtypes.bfloat16),) * 2, math_mode="safe")
+                       out_shape=(pl.ShapeDtypeStruct((n,), dt),) * 2, math_mode="safe")
     got = call(x, y)
     want = call.interpret(x, y)
     for g, w in zip(got, want):
-        np.testing.assert_array_equal(dtypes.as_bits(g), dtypes.as_bits(w))
+        np.testing.assert_array_equal(np.ascontiguousarray(g).view(np.uint16), np.ascontiguousarray(w).view(np.uint16))

@@ -26,15 +26,16 @@ def test_vector_program_bit_exact_vs_interpreter(seed, lanes):
         np.testing.assert_array_equal(g, w)
 
 
+@pytest.mark.parametrize("dt", [dtypes.bfloat16, np.dtype(np.float16)], ids=["bf16", "f16"])
 @pytest.mark.parametrize("lanes", [False, True], ids=["instance", "lanes"])
 @pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
-def test_vector_program_bf16_bit_exact_vs_interpreter(seed, lanes):
-    print(f"fuzz_vec bf16 seed={seed} lanes={lanes}", flush=True)
-    call = make_call(seed, lanes=lanes, dtype=dtypes.bfloat16, math_mode="safe")
-    args = make_inputs(seed, dtype=dtypes.bfloat16)
+def test_vector_program_narrow_float_bit_exact_vs_interpreter(seed, lanes, dt):
+    print(f"fuzz_vec {dtypes.name(dt)} seed={seed} lanes={lanes}", flush=True)
+    call = make_call(seed, lanes=lanes, dtype=dt, math_mode="safe")
+    args = make_inputs(seed, dtype=dt)
     got = call(*args)
     want = call.interpret(*args)
     for g, w in zip(got, want):
-        if dtypes.is_bf16(w.dtype):
-            g, w = dtypes.as_bits(g), dtypes.as_bits(w)
+        if w.dtype.itemsize == 2:
+            g, w = np.ascontiguousarray(g).view(np.uint16), np.ascontiguousarray(w).view(np.uint16)
         np.testing.assert_array_equal(g, w)
