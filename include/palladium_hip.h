@@ -50,7 +50,9 @@ int ph_compile_code_object(const char *src, size_t src_len, const char *name,
                            size_t *code_size, char **err);
 void ph_free_code_object(void *code);
 
-/* The hiprtc option string used for a math mode (static storage). */
+/* The math-mode-specific hiprtc options (static storage). Every compile
+ * also passes --offload-arch, -O3, -std=c++17, -fwrapv, -fno-slp-vectorize,
+ * -DPH_MATH_MODE=<mode> and disables the packed FP32 target feature. */
 const char *ph_compile_options(int math_mode);
 
 /* Compile (outside the cache lock), load on the current device and look up
