@@ -144,7 +144,13 @@ class FfiCallable:
         )
 
     def __call__(self, *args: Any) -> Any:
-        import jax
+        try:
+            import jax
+        except ImportError as e:
+            raise ImportError(
+                "hip_call_jit dispatches through jax.ffi and needs jax installed; "
+                "without jax, use palladium_amd.hip_call (same kernel, NumPy in/out)"
+            ) from e
 
         _register()
         spec, _ = self.spec_and_source(args)

@@ -184,3 +184,12 @@ def test_debug_hip_matches_what_hip_call_compiles():
         assert pa.debug_hip(kernel, x, x, out_shape=out, math_mode=mode) == pa.emit_hip(spec, math_mode=mode)
     assert pa.debug_hip(kernel, x, x, out_shape=out) == pa.emit_hip(spec, math_mode="fast")
     assert pa.debug_hip(kernel, x, x, out_shape=out, math_mode="safe") != pa.debug_hip(kernel, x, x, out_shape=out)
+
+
+def test_hip_call_jit_without_jax_names_the_alternative(monkeypatch):
+    import sys
+
+    monkeypatch.setitem(sys.modules, "jax", None)  # import jax -> ImportError
+    f = pa.hip_call_jit(lambda x, o: o.__setitem__(Ellipsis, x[...]), out_shape=pl.ShapeDtypeStruct((8,), F))
+    with pytest.raises(ImportError, match="hip_call"):
+        f(np.zeros(8, F))
