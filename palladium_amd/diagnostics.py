@@ -71,6 +71,9 @@ class KernelDiagnostics:
     blocks: int = 0
     block: int = 0
     resources: ResourceUsage | None = None
+    # threads per program instance: 1, or the block rows a lane-parallel
+    # kernel spreads across lanes
+    lanes: int = 1
 
     @property
     def msl_lines(self) -> int:
@@ -83,6 +86,8 @@ class KernelDiagnostics:
             parts.append(f"threadgroup={self.threadgroup}")
         parts.append(f"hip_lines={self.hip_lines}")
         parts.append(f"launch={self.blocks}x{self.block}")
+        if self.lanes > 1:
+            parts.append(f"lanes/instance={self.lanes}")
         r = self.resources
         if r is not None:
             parts.append(
@@ -183,6 +188,7 @@ def explain_spec(spec: KernelSpec, threadgroup: Any = None, math_mode: Any = Non
         blocks=geo.blocks,
         block=geo.block,
         resources=res,
+        lanes=geo.lanes,
     )
 
 

@@ -193,3 +193,15 @@ def test_hip_call_jit_without_jax_names_the_alternative(monkeypatch):
     f = pa.hip_call_jit(lambda x, o: o.__setitem__(Ellipsis, x[...]), out_shape=pl.ShapeDtypeStruct((8,), F))
     with pytest.raises(ImportError, match="hip_call"):
         f(np.zeros(8, F))
+
+
+def test_explain_reports_lane_parallel_lowering():
+    spec = pl.BlockSpec((256,), lambda i: (i,))
+
+    def kernel(x_ref, o_ref):
+        o_ref[...] = x_ref[...] * 2.0
+
+    f = pa.hip_call(kernel, grid=(4,), in_specs=[spec], out_specs=spec, out_shape=pl.ShapeDtypeStruct((1024,), F))
+    diag = f.explain(np.zeros(1024, F), compile=False)
+    assert diag.lanes == 256 and "lanes/instance=256" in str(diag)
+    assert "lanes/instance" not in str(_double(64).explain(np.zeros(64, F), compile=False))
