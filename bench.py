@@ -121,7 +121,7 @@ def bench_lv(steps: int, warmup: int, cpu: bool, cfg=None, block: int = 1, track
             "unit": "TFLOP/s",
             "frac": achieved / FP32_PEAK,
             # HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE passes,
-            # scaled by the copy-kernel calibration (profiles/hbm_traffic_lv_rk4_n1e6.md).
+            # scaled by what the same counters read for a copy kernel of known size.
             "traffic": LV_MEASURED_TRAFFIC_BYTES if cfg is LV_CFG1 else None,
             "traffic_algorithmic": (36 if track_max else 32) * n,
             "flop_per_traj_step": LV_FLOP_PER_STEP,
