@@ -63,6 +63,14 @@ const char *ph_compile_options(int math_mode);
 int ph_get_kernel(const char *src, size_t src_len, const char *name,
                   int math_mode, ph_kernel **out, char **err);
 
+/* Load a code object made by ph_compile_code_object (possibly in another
+ * process) on the current device and look up `name`. The kernel lives for
+ * the rest of the process; callers cache it. No reference counterpart:
+ * metal-runtime compiles and loads in one step. It lets a host compile in a
+ * helper process, where a compiler crash cannot end the caller. */
+int ph_load_code_object(const void *code, size_t code_size, const char *name,
+                        ph_kernel **out, char **err);
+
 /* Number of distinct kernels in the cache (for tests). */
 size_t ph_kernel_cache_size(void);
 

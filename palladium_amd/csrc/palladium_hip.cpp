@@ -222,6 +222,26 @@ int ph_get_kernel(const char *src, size_t src_len, const char *name,
   return KernelCache::instance().get(src, src_len, name, math_mode, out, err);
 }
 
+int ph_load_code_object(const void *code, size_t code_size, const char *name,
+                        ph_kernel **out, char **err) {
+  if (!code || !code_size || !name || !out)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_load_code_object: null argument");
+  int device = 0;
+  hipError_t he = hipGetDevice(&device);
+  if (he != hipSuccess) return hip_fail(err, he, "hipGetDevice");
+  auto k = std::make_unique<ph_kernel>();
+  k->device = device;
+  he = hipModuleLoadData(&k->module, code);
+  if (he != hipSuccess) return hip_fail(err, he, "hipModuleLoadData");
+  he = hipModuleGetFunction(&k->function, k->module, name);
+  if (he != hipSuccess) {
+    (void)hipModuleUnload(k->module);  // best effort: the lookup error is reported
+    return hip_fail(err, he, (std::string("hipModuleGetFunction(") + name + ")").c_str());
+  }
+  *out = k.release();  // kept for the life of the process, like cached kernels
+  return PH_OK;
+}
+
 size_t ph_kernel_cache_size(void) { return KernelCache::instance().size(); }
 
 int ph_launch(ph_kernel *k, unsigned int gx, unsigned int gy, unsigned int gz,

@@ -107,6 +107,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "ph_compile_options": (c.c_char_p, [c.c_int]),
         "ph_get_kernel": (c.c_int, [c.c_char_p, c.c_size_t, c.c_char_p, c.c_int, _PP, _PP]),
         "ph_kernel_cache_size": (c.c_size_t, []),
+        "ph_load_code_object": (c.c_int, [c.c_void_p, c.c_size_t, c.c_char_p, _PP, _PP]),
         "ph_launch": (c.c_int, [_P, c.c_uint, c.c_uint, c.c_uint, c.c_uint, c.c_uint, c.c_uint, c.c_uint, _P, _PP, _PP]),
         "ph_launch_ptrs": (c.c_int, [_P, c.c_uint, c.c_uint, _P, _PP, c.c_size_t, _PP]),
         "ph_dispatch": (c.c_int, [c.c_char_p, c.c_size_t, c.c_char_p, c.c_int64, c.c_int64, c.c_int64, c.c_int64, c.c_int64,
@@ -419,9 +420,18 @@ class Kernel:
         if self._handle is None:
             with self._lock:
                 if self._handle is None:
-                    src = self.source.encode()
+                    from palladium_amd import compile_worker
+
                     h = ctypes.c_void_p()
-                    _call("ph_get_kernel", src, len(src), self.name.encode(), self.math_mode.ordinal, ctypes.byref(h))
+                    if compile_worker.isolation_enabled():
+                        # compile in the helper process; a compiler crash
+                        # there is a CompileError here
+                        code = compile_worker.compile_isolated(self.source, self.name, self.math_mode.ordinal)
+                        _call("ph_load_code_object", code, len(code), self.name.encode(), ctypes.byref(h))
+                    else:
+                        src = self.source.encode()
+                        _call("ph_get_kernel", src, len(src), self.name.encode(), self.math_mode.ordinal,
+                              ctypes.byref(h))
                     self._handle = h.value
         return self._handle
 

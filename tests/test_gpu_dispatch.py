@@ -273,3 +273,17 @@ def test_torch_device_tensors_zero_copy():
     r = subprocess.run([sys.executable, "-c", _TORCH_INTEROP, root], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "torch interop ok" in r.stdout
+
+
+def test_isolated_compile_path_runs_kernels(monkeypatch, rng):
+    """PALLADIUM_COMPILE_ISOLATED=1: the code object comes from the helper
+    process and loads through ph_load_code_object; results equal the
+    in-process path's."""
+    from palladium_amd.workloads import lv_inputs, lv_rk4_call
+
+    args = lv_inputs(2048, 5)
+    want = lv_rk4_call(2048, 0.01, 100, track_max=True, math_mode="safe")(*args)
+    monkeypatch.setenv("PALLADIUM_COMPILE_ISOLATED", "1")
+    got = lv_rk4_call(2048, 0.01, 100, track_max=True, math_mode="safe")(*args)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
