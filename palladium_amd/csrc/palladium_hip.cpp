@@ -424,7 +424,8 @@ int ph_device_name(char *buf, size_t len) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess)
     return PH_ERR_RUNTIME;
-  std::snprintf(buf, len, "%s (%s)", prop.name, prop.gcnArchName);
+  // Some drivers leave the marketing name empty: fall back to the arch.
+  std::snprintf(buf, len, "%s (%s)", prop.name[0] ? prop.name : "AMD GPU", prop.gcnArchName);
   return PH_OK;
 }
 
