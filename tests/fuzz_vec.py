@@ -7,7 +7,8 @@ lane). The grammar mixes element-wise trees with broadcasting, row
 reductions (max/min exact in any order; sums over values quantised to
 1/8 so that they are exact too), small dot products with a constant
 matrix, a `cond` on a data-dependent row predicate, `iota`, integer
-hashing (multiply wrap, xor, shifts) and a fori_loop, so every result is
+hashing (multiply wrap, xor, shifts), a fori_loop and a lockstep
+while_loop over `jnp.any` of the rows, so every result is
 exactly determined and the GPU must match the interpreter bit for bit
 under SAFE math. The same programs run with bfloat16 blocks (each
 operation evaluated in float32 and rounded; the quantised sums and dot
@@ -92,6 +93,17 @@ def make_kernel(seed, lanes=False):
             return _tame(c * 0.5 + jnp.minimum(c, x) - i.astype(dt) * 0.25, dt=dt)
 
         out = lax.fori_loop(0, 2 + seed % 4, body, out)
+
+        # lockstep while (examples/02's pattern): iterate until no row of the
+        # instance is below a threshold; across lanes this is a cross-lane
+        # reduction in the loop condition
+        def wcond(s):
+            return jnp.logical_and(s[0] < 5, jnp.any(s[1] < 4.0 - (seed % 3)))
+
+        def wbody(s):
+            return s[0] + 1, _tame(jnp.abs(s[1]) * 0.75 + 1.25, dt=dt)
+
+        out = lax.while_loop(wcond, wbody, (0, out))[1]
         o_ref[...] = out
         s_ref[...] = q
         h = k * 1103515245 + 12345
