@@ -100,15 +100,14 @@ __device__ __forceinline__ double ph_ln_pos(double x) {
     if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
     double t = (m - 1.0) / (m + 1.0);
     double t2 = t * t;
-    /* sum_{k=0..11} t2^k / (2k+1) by Estrin's scheme (depth 4, not 11) */
+    /* sum_{k=0..7} t2^k / (2k+1) by Estrin's scheme. |t| <= 0.1716, so the
+       first omitted term is below 1.3e-13 of the sum: ample for a result
+       rounded to float. */
     double q0 = fma(1.0 / 3.0, t2, 1.0), q1 = fma(1.0 / 7.0, t2, 1.0 / 5.0);
     double q2 = fma(1.0 / 11.0, t2, 1.0 / 9.0), q3 = fma(1.0 / 15.0, t2, 1.0 / 13.0);
-    double q4 = fma(1.0 / 19.0, t2, 1.0 / 17.0), q5 = fma(1.0 / 23.0, t2, 1.0 / 21.0);
     double u2 = t2 * t2;
-    double r0 = fma(q1, u2, q0), r1 = fma(q3, u2, q2), r2 = fma(q5, u2, q4);
-    double u4 = u2 * u2;
-    double s0 = fma(r1, u4, r0);
-    double p = fma(r2, u4 * u4, s0);
+    double r0 = fma(q1, u2, q0), r1 = fma(q3, u2, q2);
+    double p = fma(r1, u2 * u2, r0);
     double lnm = 2.0 * t * p;
     const double ln2_hi = 6.93147180369123816490e-01;
     const double ln2_lo = 1.90821492927058770002e-10;
@@ -123,16 +122,16 @@ __device__ __forceinline__ double ph_exp_dbl(double z) {
     double kd = rint(z * inv_ln2);
     double r = fma(-kd, ln2_hi, z);
     r = fma(-kd, ln2_lo, r);
-    /* sum_{k=0..13} r^k / k! by Estrin's scheme (depth 4, not 13) */
+    /* sum_{k=0..10} r^k / k! by Estrin's scheme. |r| <= ln2 / 2, so the
+       first omitted term is below 2.2e-13: ample for a float result. */
     double a0 = fma(1.0, r, 1.0), a1 = fma(1.0 / 6.0, r, 0.5);
     double a2 = fma(1.0 / 120.0, r, 1.0 / 24.0), a3 = fma(1.0 / 5040.0, r, 1.0 / 720.0);
-    double a4 = fma(1.0 / 362880.0, r, 1.0 / 40320.0), a5 = fma(1.0 / 39916800.0, r, 1.0 / 3628800.0);
-    double a6 = fma(1.0 / 6227020800.0, r, 1.0 / 479001600.0);
+    double a4 = fma(1.0 / 362880.0, r, 1.0 / 40320.0);
     double w2 = r * r;
-    double b0 = fma(a1, w2, a0), b1 = fma(a3, w2, a2), b2 = fma(a5, w2, a4);
+    double b0 = fma(a1, w2, a0), b1 = fma(a3, w2, a2), b2 = fma(1.0 / 3628800.0, w2, a4);
     double w4 = w2 * w2;
-    double c0 = fma(b1, w4, b0), c1 = fma(a6, w4, b2);
-    double p = fma(c1, w4 * w4, c0);
+    double c0 = fma(b1, w4, b0);
+    double p = fma(b2, w4 * w4, c0);
     return ldexp(p, (int)kd);
 }
 

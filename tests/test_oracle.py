@@ -128,6 +128,24 @@ def test_pow_within_one_ulp_of_libm():
         assert ulps <= 1, (x, y, got, want)
 
 
+def test_pow_correctly_rounded_over_a_wide_sweep():
+    """Stronger than the 1-ulp pin: over x in 10^(+-30) and y in [-3, 3]
+    (results inside the normal float range), the deterministic pow returns
+    the float nearest to the exact power (libm's double pow rounded once),
+    so its shortened log/exp polynomials lose nothing a float can hold."""
+    rng = np.random.default_rng(1)
+    xs = (10.0 ** rng.uniform(-30, 30, 20000)).astype(np.float32)
+    ys = rng.uniform(-3.0, 3.0, 20000).astype(np.float32)
+    checked = 0
+    for x, y in zip(xs, ys):
+        w = math.pow(float(x), float(y))
+        if not 1e-37 < w < 1e37:
+            continue
+        checked += 1
+        assert oracle.pow32(x, y) == np.float32(w), (x, y)
+    assert checked > 15000
+
+
 @pytest.mark.parametrize(
     "x,y,want",
     [(2.0, 10.0, 1024.0), (4.0, 0.5, 2.0), (0.0, 2.0, 0.0), (0.0, -1.0, np.inf), (-2.0, 3.0, -8.0),
