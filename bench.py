@@ -608,7 +608,7 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     if cpu:
         import oracle
 
-        n_cpu = 131072
+        n_cpu = cfg.n  # all of config 2: the exact-count check covers every trajectory
         t0 = time.perf_counter()
         a2 = oracle.bs3_vdp(*(h[:n_cpu] for h in host), cfg)
         dt = time.perf_counter() - t0
