@@ -452,10 +452,13 @@ def bench_gs(steps: int, warmup: int, cpu: bool) -> dict:
 
         size, cs = cfg.size, 200
         t0 = time.perf_counter()
-        oracle.gray_scott(u0, v0, cfg, cs)
+        wu, wv = oracle.gray_scott(u0, v0, cfg, cs)
         dt = time.perf_counter() - t0
         res["cpu_baseline"] = {"value": size * size * cs / dt, "unit": "cell-steps/s", "cores": _cpu_cores(),
                                "kind": "port", "sample": f"config-4 grid ({size}^2) x first {cs} of {cfg.steps} steps, C oracle, {dt:.2f} s"}
+        # the same 200 steps under SAFE on the GPU, compared with the oracle's fields
+        su, sv, _ = gray_scott_run(gray_scott_call(size=size, math_mode="safe"), u0, v0, cs)
+        res["safe_bit_exact_vs_oracle"] = {"steps": cs, "equal": bool(np.array_equal(su, wu) and np.array_equal(sv, wv))}
     return res
 
 
