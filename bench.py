@@ -296,6 +296,16 @@ def bench_gbm(steps: int, warmup: int, cpu: bool) -> dict:
         dt = time.perf_counter() - t0
         res["cpu_baseline"] = {"value": n_cpu * cfg.n_steps / dt, "unit": "path-steps/s", "cores": _cpu_cores(),
                                "kind": "port", "sample": f"all {n_cpu} paths x {cfg.n_steps} steps of config 3, C oracle, {dt:.2f} s"}
+        # the kernel's own .interpret() (the reference's interpret=True path)
+        from palladium_amd.workloads import gbm_call as _gbm_call
+
+        ni = 262144
+        t0 = time.perf_counter()
+        _gbm_call(cfg, n_paths=ni).interpret(key)
+        di = time.perf_counter() - t0
+        res["cpu_baselines_more"] = {"interpret": {
+            "value": ni * cfg.n_steps / di, "unit": "path-steps/s", "cores": 1, "kind": "port",
+            "sample": f"{ni} paths x {cfg.n_steps} steps, hip_call(...).interpret() (NumPy), {di:.2f} s"}}
     return res
 
 
@@ -617,6 +627,14 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
         dt = time.perf_counter() - t0
         res["cpu_baseline"] = {"value": float((a2[3].astype(np.int64) + a2[4]).sum() / dt), "unit": "attempts/s",
                                "cores": _cpu_cores(), "kind": "port", "sample": f"first {n_cpu} trajectories, C oracle, {dt:.2f} s"}
+        # the kernel's own .interpret() (the reference's interpret=True path)
+        ni = 4096
+        t0 = time.perf_counter()
+        ia = bs3_vdp_call(ni).interpret(*(h[:ni] for h in host))
+        di = time.perf_counter() - t0
+        res["cpu_baselines_more"] = {"interpret": {
+            "value": float((ia[3].astype(np.int64) + ia[4]).sum() / di), "unit": "attempts/s", "cores": 1,
+            "kind": "port", "sample": f"first {ni} trajectories, hip_call(...).interpret() (NumPy), {di:.2f} s"}}
         res["safe"]["counts_equal_oracle"] = {
             "sample": f"first {n_cpu} trajectories",
             "accepted": bool(np.array_equal(sacc[:n_cpu], a2[3])),
