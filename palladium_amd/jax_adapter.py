@@ -17,6 +17,7 @@ from typing import Any
 import numpy as np
 
 from palladium_amd import ir
+from palladium_amd.dtypes import is_bf16, to_float
 from palladium_amd.errors import TraceError
 from palladium_amd.trace import BlockInfo, KernelSpec
 
@@ -64,7 +65,10 @@ class _Converter:
         from jax.extend.core import Literal
 
         if isinstance(a, Literal):
-            return ir.Literal(np.asarray(a.val).item(), _aval(a.aval))
+            val = np.asarray(a.val)
+            if is_bf16(val.dtype):  # an ml_dtypes (or surrogate) bfloat16 scalar
+                return ir.Literal(float(to_float(val).reshape(())), _aval(a.aval))
+            return ir.Literal(val.item(), _aval(a.aval))
         v = self.vars.get(a)
         if v is None:
             v = self.vars[a] = ir.Var(_aval(a.aval))

@@ -12,7 +12,7 @@ import types
 import numpy as np
 import pytest
 
-from palladium_amd import ir
+from palladium_amd import dtypes, ir
 from palladium_amd.emit import emit_hip
 from palladium_amd.frontend import random
 from palladium_amd.trace import trace
@@ -117,6 +117,8 @@ class _Jaxify:
 
     def atom(self, x):
         if isinstance(x, ir.Literal):
+            if dtypes.is_bf16(x.aval.dtype):  # JAX holds bf16 literals as ml_dtypes scalars
+                return FakeLiteral(dtypes.from_float(np.float32(x.val)).reshape(()), _fake_aval(x.aval))
             return FakeLiteral(np.asarray(x.val, dtype=x.aval.dtype), _fake_aval(x.aval))
         if x not in self.vars:
             self.vars[x] = FakeVar(_fake_aval(x.aval))
@@ -171,6 +173,10 @@ def _specs():
     yield "gray_scott", trace(gray_scott_call(size=64)._staged, *gray_scott_initial(64))
     yield "fuzz_vec_lanes", trace(make_call(3, rows=128, lanes=True)._staged, *make_inputs(3, rows=128))
     yield "fuzz_vec_instance", trace(make_call(4, rows=128)._staged, *make_inputs(4, rows=128))
+    for dt, tag in ((dtypes.bfloat16, "bf16"), (np.float16, "f16")):
+        yield f"fuzz_vec_lanes_{tag}", trace(make_call(5, rows=128, lanes=True, dtype=dt)._staged,
+                                              *make_inputs(5, rows=128, dtype=dt))
+        yield f"fuzz_vec_instance_{tag}", trace(make_call(6, rows=128, dtype=dt)._staged, *make_inputs(6, rows=128, dtype=dt))
 
 
 @pytest.mark.parametrize("name,spec", list(_specs()), ids=lambda x: x if isinstance(x, str) else "")
