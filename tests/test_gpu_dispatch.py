@@ -254,6 +254,23 @@ torch.cuda.synchronize()
 bound.launch_device(x, o)
 bound.stream.synchronize()
 assert torch.equal(o, x + 1.0)
+# bfloat16 tensors wrap as bfloat16 buffers: x * 2 + 1 in bf16, against the
+# interpreter on the same values
+from palladium_amd import dtypes
+g = pa.hip_call(lambda x_ref, o_ref: o_ref.__setitem__(Ellipsis, x_ref[...] * 2.0 + 1.0),
+                grid=(2,), in_specs=[pl.BlockSpec((256,), lambda i: (i,))],
+                out_specs=pl.BlockSpec((256,), lambda i: (i,)),
+                out_shape=pl.ShapeDtypeStruct((512,), dtypes.bfloat16), math_mode="safe")
+xb = torch.linspace(-3, 3, 512, device="cuda").to(torch.bfloat16)
+ob = torch.empty_like(xb)
+host = dtypes.from_float(xb.float().cpu().numpy())
+gb = g.bound(host)
+torch.cuda.synchronize()
+gb.launch_device(xb, ob)
+gb.stream.synchronize()
+want = dtypes.as_bits(g.interpret(host))
+got = ob.cpu().view(torch.int16).numpy().view(np.uint16)
+assert np.array_equal(got, want), (got[:8], want[:8])
 print("torch interop ok")
 """
 
