@@ -132,7 +132,9 @@ def bench_lv(steps: int, warmup: int, cpu: bool, cfg=None, block: int = 1, track
     # oracle bit for bit; FAST above is the throughput mode.
     safe_outs = None
     if cfg is LV_CFG1:
-        safe_bound = lv_rk4_call(n, cfg.dt, cfg.steps, track_max=track_max, block=block, math_mode="safe").bound(*host)
+        # its own kernel name, so a profiler keeps its launches apart from FAST's
+        safe_bound = lv_rk4_call(n, cfg.dt, cfg.steps, track_max=track_max, block=block, math_mode="safe",
+                                 name="lv_rk4_safe").bound(*host)
         safe_outs = [rt.Buffer.empty((n,), np.float32) for _ in outs]
         sms, _ = _timed_launches(safe_bound, [*ins, *safe_outs], max(1, steps // 4), 1)
         result["safe"] = {"ms_per_step": sms, "value": traj_steps / (sms / 1e3), "unit": "trajectory-steps/s"}
@@ -610,7 +612,7 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
                        "accepted": int(acc.sum()), "rejected": int(rej.sum())}
     # SAFE: the mode whose accepted/rejected counts equal the oracle's exactly
     # (IEEE order, deterministic pow); FAST above is the throughput mode.
-    safe_bound = bs3_vdp_call(cfg.n, math_mode="safe").bound(*host)
+    safe_bound = bs3_vdp_call(cfg.n, math_mode="safe", name="bs3_vdp_safe").bound(*host)
     safe_outs = [rt.Buffer.empty((cfg.n,), np.float32) for _ in range(3)] + \
         [rt.Buffer.empty((cfg.n,), np.int32) for _ in range(2)]
     sms, savg = _timed_launches(safe_bound, ins + safe_outs, steps, warmup)

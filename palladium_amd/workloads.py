@@ -81,7 +81,8 @@ def lv_rk4_kernel(dt: float, steps: int, track_max: bool = False):
     return kernel
 
 
-def lv_rk4_call(n: int, dt: float, steps: int, track_max: bool = False, block: int = 1, **kw: Any):
+def lv_rk4_call(n: int, dt: float, steps: int, track_max: bool = False, block: int = 1, name: str = "lv_rk4",
+                **kw: Any):
     """`hip_call` of the LV ensemble over `n` trajectories; `block`
     trajectories per program instance (1 = one lane each). The grid is
     ceil(n / block), as config 0 states it (N = 100,000 in blocks of 256):
@@ -96,7 +97,7 @@ def lv_rk4_call(n: int, dt: float, steps: int, track_max: bool = False, block: i
         in_specs=[spec] * 6,
         out_specs=tuple([spec] * n_out),
         out_shape=tuple(pl.ShapeDtypeStruct((n,), F32) for _ in range(n_out)),
-        name="lv_rk4",
+        name=name,
         **kw,
     )
 
@@ -278,7 +279,7 @@ def bs3_vdp_lockstep_kernel(cfg: BS3Config, max_steps: int):
     return kernel
 
 
-def bs3_vdp_call(n: int, cfg: BS3Config = BS3_CFG, **kw: Any):
+def bs3_vdp_call(n: int, cfg: BS3Config = BS3_CFG, name: str = "bs3_vdp", **kw: Any):
     import palladium_amd as pa
 
     spec = pl.BlockSpec((1,), lambda i: (i,))
@@ -291,7 +292,7 @@ def bs3_vdp_call(n: int, cfg: BS3Config = BS3_CFG, **kw: Any):
             pl.ShapeDtypeStruct((n,), F32), pl.ShapeDtypeStruct((n,), F32), pl.ShapeDtypeStruct((n,), F32),
             pl.ShapeDtypeStruct((n,), np.int32), pl.ShapeDtypeStruct((n,), np.int32),
         ),
-        name="bs3_vdp",
+        name=name,
         **kw,
     )
 
