@@ -125,6 +125,10 @@ int ph_device_count(int *count);
 int ph_device_name(char *buf, size_t len);
 int ph_malloc(size_t bytes, void **ptr, char **err);
 int ph_free(void *ptr);
+/* Pinned (page-locked) host memory, the staging a device->host copy can run
+ * into asynchronously (metal-runtime needs none: unified memory). */
+int ph_host_alloc(size_t bytes, void **ptr, char **err);
+int ph_host_free(void *ptr);
 int ph_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream, char **err);
 int ph_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream, char **err);
 /* Device -> host copy ordered on `stream`, returning once `dst` holds the

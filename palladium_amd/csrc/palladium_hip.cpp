@@ -436,6 +436,13 @@ int ph_malloc(size_t bytes, void **ptr, char **err) {
 
 int ph_free(void *ptr) { return hipFree(ptr) == hipSuccess ? PH_OK : PH_ERR_RUNTIME; }
 
+int ph_host_alloc(size_t bytes, void **ptr, char **err) {
+  hipError_t e = hipHostMalloc(ptr, bytes ? bytes : 4, hipHostMallocDefault);
+  return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipHostMalloc");
+}
+
+int ph_host_free(void *ptr) { return hipHostFree(ptr) == hipSuccess ? PH_OK : PH_ERR_RUNTIME; }
+
 int ph_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream, char **err) {
   hipError_t e = hipMemcpyHtoDAsync(dst, const_cast<void *>(src), bytes, (hipStream_t)stream);
   return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipMemcpyHtoDAsync");

@@ -66,7 +66,9 @@ class PendingResult:
     event : runtime.Event
         Recorded after the launch on the kernel's stream.
     out_bufs : list of runtime.Buffer
-        This launch's outputs, read back by `wait()`.
+        This launch's device outputs. For `launch()` they belong to one of
+        the kernel's IN_FLIGHT buffer sets and are reused by a later launch;
+        `wait()` returns host copies that stay valid.
     stream : runtime.Stream
     """
 
@@ -75,15 +77,33 @@ class PendingResult:
     stream: Any
     # Host arrays an asynchronous upload may still be reading.
     host_inputs: tuple = dataclasses.field(default=(), repr=False)
+    # Pinned host copies of the outputs, filled by copies queued right after
+    # the launch (None: read the device buffers back on wait()).
+    staged: list[rt.PinnedBuffer] | None = dataclasses.field(default=None, repr=False)
+    _results: tuple | None = dataclasses.field(default=None, repr=False)
+    _lock: threading.Lock = dataclasses.field(default_factory=threading.Lock, repr=False)
 
     def done(self) -> bool:
         return self.event.query()
 
+    def _settle(self) -> tuple:
+        """Wait for the launch and its queued readbacks once, and keep the
+        outputs as fresh host arrays (the staging may then be reused)."""
+        with self._lock:
+            if self._results is None:
+                self.event.synchronize()
+                self.host_inputs = ()
+                if self.staged is not None:
+                    self._results = tuple(np.array(p.view(b.shape, b.dtype)) for p, b in zip(self.staged, self.out_bufs))
+                    self.staged = None
+                else:
+                    self._results = tuple(b.to_numpy(self.stream) for b in self.out_bufs)
+            return self._results
+
     def wait(self) -> np.ndarray | tuple[np.ndarray, ...]:
-        """Block until the GPU is done, then return the outputs."""
-        self.event.synchronize()
-        self.host_inputs = ()
-        outs = tuple(b.to_numpy(self.stream) for b in self.out_bufs)
+        """Block until the GPU is done, then return the outputs (fresh
+        arrays, the same ones on every call)."""
+        outs = self._settle()
         return outs[0] if len(outs) == 1 else outs
 
 
@@ -107,10 +127,12 @@ class BoundKernel:
     hip_source: str
     threadgroup: int | tuple[int, ...] | None = None
     geometry: LaunchGeometry | None = None
-    # Input buffer sets for launches in flight: set k serves launches
-    # k, k + IN_FLIGHT, ...; a launch waits only for the last launch that
-    # used its set, so uploads for the next call overlap the running kernel.
-    _ring: list[list[rt.Buffer]] = dataclasses.field(default_factory=list, compare=False, repr=False)
+    # Buffer sets for launches in flight: set k (inputs, device outputs and
+    # pinned host staging for the outputs) serves launches k, k + IN_FLIGHT,
+    # ...; a launch waits only for the last launch that used its set, so
+    # uploads, kernels and readbacks of successive calls overlap.
+    _ring: list[tuple[list[rt.Buffer], list[rt.Buffer], list[rt.PinnedBuffer]]] = dataclasses.field(
+        default_factory=list, compare=False, repr=False)
     _ring_pending: list[PendingResult | None] = dataclasses.field(default_factory=list, compare=False, repr=False)
     _ring_next: list[int] = dataclasses.field(default_factory=lambda: [0], compare=False, repr=False)
     _launch_lock: threading.Lock = dataclasses.field(default_factory=threading.Lock, compare=False, repr=False)
@@ -163,17 +185,23 @@ class BoundKernel:
             k = self._ring_next[0]
             self._ring_next[0] = (k + 1) % IN_FLIGHT
             if len(self._ring) <= k:
-                self._ring.append([rt.Buffer.empty(a.shape, a.dtype) for a in arrs])
+                outs = self._new_outputs()
+                self._ring.append(([rt.Buffer.empty(a.shape, a.dtype) for a in arrs], outs,
+                                   [rt.PinnedBuffer(b.nbytes) for b in outs]))
                 self._ring_pending.append(None)
             previous = self._ring_pending[k]
             if previous is not None:
-                previous.event.synchronize()
-            bufs = self._ring[k]
+                previous._settle()  # its outputs leave the set's staging first
+            in_bufs, out_bufs, staging = self._ring[k]
             stream = self.stream
-            for buf, a in zip(bufs, arrs):
+            for buf, a in zip(in_bufs, arrs):
                 buf.copy_from(a, stream)
-            pending = self._dispatch(bufs, self._new_outputs())
-            pending.host_inputs = tuple(arrs)
+            geo = self._geo()
+            self.kernel.launch_ptrs(geo.blocks, geo.block, [b.ptr for b in in_bufs] + [b.ptr for b in out_bufs], stream)
+            for pin, buf in zip(staging, out_bufs):
+                pin.copy_from_device(buf, stream)
+            pending = PendingResult(rt.Event().record(stream), out_bufs, stream, host_inputs=tuple(arrs),
+                                    staged=list(staging))
             self._ring_pending[k] = pending
             return pending
 

@@ -119,6 +119,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "ph_device_name": (c.c_int, [c.c_char_p, c.c_size_t]),
         "ph_malloc": (c.c_int, [c.c_size_t, _PP, _PP]),
         "ph_free": (c.c_int, [_P]),
+        "ph_host_alloc": (c.c_int, [c.c_size_t, _PP, _PP]),
+        "ph_host_free": (c.c_int, [_P]),
         "ph_memcpy_h2d": (c.c_int, [_P, _P, c.c_size_t, _P, _PP]),
         "ph_memcpy_d2h": (c.c_int, [_P, _P, c.c_size_t, _P, _PP]),
         "ph_memcpy_d2h_wait": (c.c_int, [_P, _P, c.c_size_t, _P, _PP]),
@@ -385,6 +387,34 @@ class Buffer:
 
     def __repr__(self) -> str:
         return f"Buffer(shape={self.shape}, dtype={self.dtype.name})"
+
+
+class PinnedBuffer:
+    """Page-locked host memory (`hipHostMalloc`): the target of an
+    asynchronous device -> host copy."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = ctypes.c_void_p()
+        _call("ph_host_alloc", ctypes.c_size_t(self.nbytes), ctypes.byref(p))
+        self.ptr = int(p.value)
+
+    def view(self, shape: Sequence[int], dtype: Any) -> np.ndarray:
+        """A NumPy view of the memory (valid while this object lives)."""
+        raw = (ctypes.c_char * max(self.nbytes, 1)).from_address(self.ptr)
+        return np.frombuffer(raw, dtype=np.uint8, count=self.nbytes).view(np.dtype(dtype)).reshape(tuple(shape))
+
+    def copy_from_device(self, buf: "Buffer", stream: Any = None) -> None:
+        """Enqueue buf -> this memory on `stream` (returns at once)."""
+        if buf.nbytes > self.nbytes:
+            raise ValueError("copy_from_device: pinned buffer too small")
+        if buf.nbytes:
+            _call("ph_memcpy_d2h", ctypes.c_void_p(self.ptr), ctypes.c_void_p(buf.ptr), ctypes.c_size_t(buf.nbytes),
+                  _stream_handle(stream))
+
+    def __del__(self) -> None:
+        if getattr(self, "ptr", None) and _lib is not None:
+            _lib.ph_host_free(ctypes.c_void_p(self.ptr))
 
 
 def synchronize_stream(stream: Any) -> None:

@@ -304,3 +304,17 @@ def test_isolated_compile_path_runs_kernels(monkeypatch, rng):
     got = lv_rk4_call(2048, 0.01, 100, track_max=True, math_mode="safe")(*args)
     for g, w in zip(got, want):
         np.testing.assert_array_equal(g, w)
+
+
+def test_more_launches_than_buffer_sets_before_any_wait(rng):
+    """10 launches (the ring has 4 buffer sets) before the first wait, waited
+    in reverse order: a set is only reused after its earlier result has been
+    copied out, so every wait returns its own launch's outputs, twice."""
+    n = 300
+    f = _inc(n)
+    xs = [rng.standard_normal(n).astype(F) for _ in range(10)]
+    b = f.bound(xs[0])
+    pend = [b.launch(x) for x in xs]
+    for x, p in reversed(list(zip(xs, pend))):
+        np.testing.assert_array_equal(p.wait(), x + 1.0)
+        np.testing.assert_array_equal(p.wait(), x + 1.0)
