@@ -749,6 +749,14 @@ def bench_dispatch(steps: int, warmup: int, cpu: bool) -> dict:
             p.wait()
     out["in_flight_16_us"] = (time.perf_counter() - t0) / (reps // 16 * 16) * 1e6
 
+    call = bound.pinned(x)  # inputs uploaded once (the reference's pin())
+    for _ in range(20):
+        call()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        call()
+    out["pinned_call_us"] = (time.perf_counter() - t0) / reps * 1e6
+
     for nbytes in (16 * 1024, 1024 * 1024):
         n = nbytes // 4
         blk = pl.BlockSpec((256,), lambda i: (i,))
