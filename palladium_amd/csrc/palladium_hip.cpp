@@ -307,6 +307,25 @@ struct DispatchStaging {
   hipStream_t stream = nullptr;
   std::vector<void *> bufs;
   std::vector<size_t> caps;
+  // Pinned host memory small outputs are read back into before the final
+  // memcpy: for 16 KB that takes 28 us against 41 us straight into pageable
+  // memory; at 1 MB the extra memcpy loses (130 against 117 us), so only
+  // outputs up to 64 KiB in total take this way.
+  void *bounce = nullptr;
+  size_t bounce_cap = 0;
+  static constexpr size_t kBounceMax = 64u << 10;
+
+  int reserve_bounce(size_t bytes, char **err) {
+    if (bytes <= bounce_cap) return PH_OK;
+    if (bounce) (void)hipHostFree(bounce);  // idle: every dispatch ends synchronized
+    bounce = nullptr;
+    bounce_cap = 0;
+    size_t cap = bytes < 65536 ? 65536 : bytes;
+    hipError_t e = hipHostMalloc(&bounce, cap, hipHostMallocDefault);
+    if (e != hipSuccess) return hip_fail(err, e, "hipHostMalloc");
+    bounce_cap = cap;
+    return PH_OK;
+  }
 
   int reserve(size_t slot, size_t bytes, char **err) {
     if (slot >= bufs.size()) {
@@ -402,12 +421,29 @@ int ph_dispatch(const char *src, size_t src_len, const char *name,
   }
   rc = ph_launch_ptrs(k, blocks, block, st->stream, dev.data(), dev.size(), err);
   if (rc != PH_OK) return drain_and(rc);
+  size_t out_total = 0;
+  for (size_t i = 0; i < n_outputs; ++i) out_total += output_bytes[i];
+  const bool bounce = out_total <= DispatchStaging::kBounceMax;
+  if (bounce) {
+    rc = st->reserve_bounce(out_total, err);
+    if (rc != PH_OK) return drain_and(rc);
+  }
+  size_t off = 0;
   for (size_t i = 0; i < n_outputs; ++i) {
     if (!output_bytes[i]) continue;
-    e = hipMemcpyDtoHAsync(outputs[i], dev[n_inputs + i], output_bytes[i], st->stream);
+    void *dst = bounce ? static_cast<char *>(st->bounce) + off : outputs[i];
+    e = hipMemcpyDtoHAsync(dst, dev[n_inputs + i], output_bytes[i], st->stream);
     if (e != hipSuccess) return drain_and(hip_fail(err, e, "hipMemcpyDtoHAsync"));
+    off += output_bytes[i];
   }
   e = hipStreamSynchronize(st->stream);
+  if (e == hipSuccess && bounce) {
+    off = 0;
+    for (size_t i = 0; i < n_outputs; ++i) {
+      if (output_bytes[i]) std::memcpy(outputs[i], static_cast<char *>(st->bounce) + off, output_bytes[i]);
+      off += output_bytes[i];
+    }
+  }
   if (e != hipSuccess) return hip_fail(err, e, "hipStreamSynchronize");
   return PH_OK;
 }
