@@ -5,9 +5,10 @@ backend crash (an `LLVM ERROR` abort) ends that process. With isolation on,
 `runtime.Kernel.load` sends the source to a long-lived child process, which
 compiles it with `ph_compile_code_object` (hiprtc only: the child makes no
 other HIP call), and loads the returned code object with
-`ph_load_code_object`. If the child dies, the parent raises `CompileError`
-with the compiler's last output and starts a fresh child on the next
-compile.
+`ph_load_code_object`. If the child dies, or a compile outlasts
+PALLADIUM_COMPILE_TIMEOUT seconds (default 900; the child is then
+stopped), the parent raises `CompileError` and starts a fresh child on the
+next compile.
 
 Protocol over the child's stdin/stdout: a request is a 4-byte big-endian
 length and a JSON header {"name", "mode", "arch", "size"} followed by `size`
@@ -19,6 +20,7 @@ from __future__ import annotations
 
 import json
 import os
+import select
 import struct
 import subprocess
 import sys
@@ -68,8 +70,16 @@ class _Worker:
                 self.proc = self._start()
             proc = self.proc
             src = source.encode()
+            timeout = float(os.environ.get("PALLADIUM_COMPILE_TIMEOUT", "900"))
             try:
                 _send(proc.stdin, {"name": name, "mode": int(mode), "arch": arch, "size": len(src)}, src)
+                ready, _, _ = select.select([proc.stdout], [], [], timeout)
+                if not ready:
+                    proc.kill()
+                    proc.wait()
+                    self.proc = None
+                    raise CompileError(f"compiling {name!r} took longer than {timeout:g} s "
+                                       "(PALLADIUM_COMPILE_TIMEOUT); the compiler process was stopped")
                 reply = _recv(proc.stdout)
             except (BrokenPipeError, OSError):
                 reply = None

@@ -46,3 +46,11 @@ def test_kernel_load_uses_the_helper_when_enabled(monkeypatch):
         with pytest.raises(Exception):
             k.load()  # the code object is compiled, then loading needs a device
         assert calls and np.asarray(calls[0][2]) == 2
+
+
+def test_a_compile_past_the_deadline_is_stopped(monkeypatch):
+    monkeypatch.setenv("PALLADIUM_COMPILE_TIMEOUT", "0.0001")
+    with pytest.raises(CompileError, match="PALLADIUM_COMPILE_TIMEOUT"):
+        compile_worker.compile_isolated(OK_SRC.replace("1.0f", "3.0f"), "k", 0)
+    monkeypatch.delenv("PALLADIUM_COMPILE_TIMEOUT")
+    assert compile_worker.compile_isolated(OK_SRC, "k", 0)[:4] == b"\x7fELF"
