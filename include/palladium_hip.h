@@ -117,6 +117,12 @@ int ph_dispatch_device(const char *src, size_t src_len, const char *name,
                        size_t n_inputs, void *const *outputs,
                        size_t n_outputs, char **err);
 
+/* Staging objects ph_dispatch has created so far (a stream, device buffers
+ * and a pinned bounce buffer each). A thread holds one per device while it
+ * lives and returns it to a pool at exit for the next thread, so the count
+ * grows only with the threads dispatching at once. For tests. */
+size_t ph_dispatch_staging_count(void);
+
 /* Device memory, streams, events and graphs: the role metal-runtime's
  * Buffer/Batch/gpu_time play for the reference
  * (src/palladium/dispatch.py:18,183-225). Streams are created at the

@@ -344,17 +344,57 @@ struct DispatchStaging {
   }
 };
 
+// Staging objects are owned per thread while it lives and go back to a
+// per-device pool when it exits, for the next thread that dispatches: a
+// program that keeps starting threads (thread-per-request servers) holds
+// at most as many as ran at once. Thread exit makes no HIP call (it may
+// come during process teardown); pooled objects are idle because every
+// dispatch ends with its stream synchronized.
+struct StagingPool {
+  std::mutex mutex;
+  std::unordered_map<int, std::vector<DispatchStaging *>> idle;
+  size_t created = 0;
+
+  static StagingPool &instance() {
+    static StagingPool *pool = new StagingPool();  // never destroyed: see above
+    return *pool;
+  }
+};
+
+struct ThreadStaging {
+  std::unordered_map<int, DispatchStaging *> per_device;
+  ~ThreadStaging() {
+    StagingPool &pool = StagingPool::instance();
+    std::lock_guard<std::mutex> lock(pool.mutex);
+    for (auto &kv : per_device)
+      if (kv.second) pool.idle[kv.first].push_back(kv.second);
+  }
+};
+
 int dispatch_staging(DispatchStaging **out, char **err) {
-  thread_local std::unordered_map<int, DispatchStaging *> per_device;
+  thread_local ThreadStaging mine;
   int device = 0;
   hipError_t e = hipGetDevice(&device);
   if (e != hipSuccess) return hip_fail(err, e, "hipGetDevice");
-  DispatchStaging *&st = per_device[device];
+  DispatchStaging *&st = mine.per_device[device];
   if (!st) {
-    auto fresh = std::make_unique<DispatchStaging>();
-    e = hipStreamCreate(&fresh->stream);
-    if (e != hipSuccess) return hip_fail(err, e, "hipStreamCreate");
-    st = fresh.release();
+    StagingPool &pool = StagingPool::instance();
+    {
+      std::lock_guard<std::mutex> lock(pool.mutex);
+      auto &idle = pool.idle[device];
+      if (!idle.empty()) {
+        st = idle.back();
+        idle.pop_back();
+      }
+    }
+    if (!st) {
+      auto fresh = std::make_unique<DispatchStaging>();
+      e = hipStreamCreate(&fresh->stream);
+      if (e != hipSuccess) return hip_fail(err, e, "hipStreamCreate");
+      st = fresh.release();
+      std::lock_guard<std::mutex> lock(pool.mutex);
+      ++pool.created;
+    }
   }
   *out = st;
   return PH_OK;
@@ -448,6 +488,12 @@ int ph_dispatch(const char *src, size_t src_len, const char *name,
   return PH_OK;
 }
 
+size_t ph_dispatch_staging_count(void) {
+  StagingPool &pool = StagingPool::instance();
+  std::lock_guard<std::mutex> lock(pool.mutex);
+  return pool.created;
+}
+
 int ph_device_count(int *count) {
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
@@ -489,21 +535,66 @@ int ph_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream, char *
   return e == hipSuccess ? PH_OK : hip_fail(err, e, "hipMemcpyDtoHAsync");
 }
 
-int ph_memcpy_d2h_wait(void *dst, const void *src, size_t bytes, void *stream, char **err) {
-  // Small readbacks bounce through a per-thread pinned buffer: a DMA into
-  // pinned memory plus a memcpy takes about 13 us on MI355X, a copy into
-  // pageable memory about 23 us. Kept for the life of the process.
-  constexpr size_t kBounce = 64 * 1024;
-  thread_local void *bounce = nullptr;
-  hipStream_t s = (hipStream_t)stream;
-  if (bytes <= kBounce) {
-    if (!bounce) {
-      hipError_t e = hipHostMalloc(&bounce, kBounce, hipHostMallocDefault);
+namespace {
+
+// The pinned buffer small readbacks of ph_memcpy_d2h_wait bounce through:
+// one per thread while it lives, returned to a pool at thread exit (no
+// HIP call there) for the next thread.
+constexpr size_t kReadbackBounce = 64 * 1024;
+
+struct BouncePool {
+  std::mutex mutex;
+  std::vector<void *> idle;
+  static BouncePool &instance() {
+    static BouncePool *pool = new BouncePool();  // never destroyed
+    return *pool;
+  }
+};
+
+struct ThreadBounce {
+  void *buf = nullptr;
+  ~ThreadBounce() {
+    if (!buf) return;
+    BouncePool &pool = BouncePool::instance();
+    std::lock_guard<std::mutex> lock(pool.mutex);
+    pool.idle.push_back(buf);
+  }
+};
+
+int readback_bounce(void **out, char **err) {
+  thread_local ThreadBounce mine;
+  if (!mine.buf) {
+    BouncePool &pool = BouncePool::instance();
+    {
+      std::lock_guard<std::mutex> lock(pool.mutex);
+      if (!pool.idle.empty()) {
+        mine.buf = pool.idle.back();
+        pool.idle.pop_back();
+      }
+    }
+    if (!mine.buf) {
+      hipError_t e = hipHostMalloc(&mine.buf, kReadbackBounce, hipHostMallocDefault);
       if (e != hipSuccess) {
-        bounce = nullptr;
+        mine.buf = nullptr;
         return hip_fail(err, e, "hipHostMalloc");
       }
     }
+  }
+  *out = mine.buf;
+  return PH_OK;
+}
+
+}  // namespace
+
+int ph_memcpy_d2h_wait(void *dst, const void *src, size_t bytes, void *stream, char **err) {
+  // Small readbacks bounce through a per-thread pinned buffer: a DMA into
+  // pinned memory plus a memcpy takes about 13 us on MI355X, a copy into
+  // pageable memory about 23 us.
+  hipStream_t s = (hipStream_t)stream;
+  if (bytes <= kReadbackBounce) {
+    void *bounce = nullptr;
+    int rc = readback_bounce(&bounce, err);
+    if (rc != PH_OK) return rc;
     hipError_t e = hipMemcpyDtoHAsync(bounce, const_cast<void *>(src), bytes, s);
     if (e != hipSuccess) return hip_fail(err, e, "hipMemcpyDtoHAsync");
     e = hipStreamSynchronize(s);

@@ -139,6 +139,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "ph_stream_end_capture": (c.c_int, [_P, _PP, _PP]),
         "ph_graph_launch": (c.c_int, [_P, _P, _PP]),
         "ph_graph_destroy": (c.c_int, [_P]),
+        "ph_dispatch_staging_count": (c.c_size_t, []),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)

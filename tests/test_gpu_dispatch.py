@@ -318,3 +318,70 @@ def test_more_launches_than_buffer_sets_before_any_wait(rng):
     for x, p in reversed(list(zip(xs, pend))):
         np.testing.assert_array_equal(p.wait(), x + 1.0)
         np.testing.assert_array_equal(p.wait(), x + 1.0)
+
+
+def _two_out(n):
+    def kernel(x_ref, a_ref, b_ref):
+        x = x_ref[...]
+        a_ref[...] = x + 1.0
+        b_ref[...] = x * 2.0
+
+    spec = pl.BlockSpec((1,), lambda i: (i,))
+    f = pa.hip_call(kernel, grid=(n,), in_specs=[spec], out_specs=(spec, spec),
+                    out_shape=(pl.ShapeDtypeStruct((n,), F), pl.ShapeDtypeStruct((n,), F)))
+    spec_t = pa.trace(f._staged, np.zeros(n, F))
+    return emit_hip(spec_t).encode(), spec_t.name.encode()
+
+
+def _dispatch_two_out(src, name, x):
+    n = x.size
+    a, b = np.full(n, np.nan, F), np.full(n, np.nan, F)
+    ins = (ctypes.c_void_p * 1)(x.ctypes.data)
+    in_b = (ctypes.c_size_t * 1)(x.nbytes)
+    outs = (ctypes.c_void_p * 2)(a.ctypes.data, b.ctypes.data)
+    out_b = (ctypes.c_size_t * 2)(a.nbytes, b.nbytes)
+    err = ctypes.c_void_p()
+    rc = rt.lib().ph_dispatch(src, len(src), name, n, 1, 1, 256, 1, 0, ins, in_b, 1, outs, out_b, 2,
+                              ctypes.byref(err))
+    assert rc == 0, ctypes.cast(err, ctypes.c_char_p).value
+    return a, b
+
+
+def test_ph_dispatch_bounce_then_direct_then_bounce(rng):
+    """One thread: outputs of 2 x 16 KB (read back through the pinned
+    bounce buffer), then 2 x 1 MB (straight into the caller's memory, the
+    staging buffers grow), then 2 x 16 KB again; sizes not multiples of 256."""
+    for n in (4099, 262147, 4093):
+        src, name = _two_out(n)
+        x = rng.standard_normal(n).astype(F)
+        a, b = _dispatch_two_out(src, name, x)
+        np.testing.assert_array_equal(a, x + 1.0)
+        np.testing.assert_array_equal(b, x * 2.0)
+
+
+def test_ph_dispatch_staging_is_reused_across_threads(rng):
+    """Threads that exit hand their staging (stream, device buffers, pinned
+    bounce) to the next ones: three waves of 4 threads create at most 4."""
+    src, name = _two_out(1000)
+    _dispatch_two_out(src, name, np.zeros(1000, F))  # this thread's own
+    before = rt.lib().ph_dispatch_staging_count()
+    errors = []
+
+    def worker(seed):
+        try:
+            x = np.random.default_rng(seed).standard_normal(1000).astype(F)
+            a, b = _dispatch_two_out(src, name, x)
+            if not (np.array_equal(a, x + 1.0) and np.array_equal(b, x * 2.0)):
+                errors.append(seed)
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(repr(e))
+
+    for wave in range(3):
+        ts = [threading.Thread(target=worker, args=(wave * 4 + t,)) for t in range(4)]
+        for th in ts:
+            th.start()
+        for th in ts:
+            th.join(timeout=60)
+        assert not any(th.is_alive() for th in ts)
+    assert not errors, errors
+    assert rt.lib().ph_dispatch_staging_count() - before <= 4
