@@ -123,6 +123,33 @@ int ph_dispatch_device(const char *src, size_t src_len, const char *name,
  * grows only with the threads dispatching at once. For tests. */
 size_t ph_dispatch_staging_count(void);
 
+/* Size of the fixed device scratch area of ph_dispatch_noalloc, per GPU. */
+#define PH_NOALLOC_SCRATCH_BYTES (64u << 20)
+size_t ph_noalloc_scratch_bytes(void);
+
+/* No counterpart in the reference. ph_dispatch for callers that cannot
+ * allocate: serving loops and harnesses that forbid hipMalloc/hipFree.
+ * It calls no hipMalloc, hipFree, hipHostMalloc, stream creation, compiler
+ * or module loader, and no allocating library routine:
+ *  - `k` comes from an earlier ph_get_kernel or ph_load_code_object on the
+ *    current device (emitted source carries its math mode);
+ *  - operands are staged in one fixed device array of
+ *    PH_NOALLOC_SCRATCH_BYTES (64 MiB) per GPU, held until the process
+ *    ends, each operand at a 256-byte boundary in argument order; operands
+ *    that do not fit are rejected with PH_ERR_INVALID_ARGUMENT before
+ *    anything is queued;
+ *  - output slots are cleared to zero before the launch;
+ *  - the work is ordered on `stream` (NULL = default stream) and the call
+ *    returns once the outputs are in the caller's host buffers.
+ * Launch geometry and operand order are ph_dispatch's. Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (other
+ * threads, other streams) race and must be serialised by the caller. */
+int ph_dispatch_noalloc(ph_kernel *k, int64_t grid_x, int64_t grid_y, int64_t grid_z,
+                        int64_t block_x, int64_t lanes, void *stream,
+                        const void *const *inputs, const size_t *input_bytes,
+                        size_t n_inputs, void *const *outputs,
+                        const size_t *output_bytes, size_t n_outputs, char **err);
+
 /* Device memory, streams, events and graphs: the role metal-runtime's
  * Buffer/Batch/gpu_time play for the reference
  * (src/palladium/dispatch.py:18,183-225). Streams are created at the

@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hiprtc.h>
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <memory>
@@ -492,6 +493,137 @@ size_t ph_dispatch_staging_count(void) {
   StagingPool &pool = StagingPool::instance();
   std::lock_guard<std::mutex> lock(pool.mutex);
   return pool.created;
+}
+
+}  // extern "C"
+
+namespace {
+
+// The allocation-free dispatch's staging: one fixed device array per GPU,
+// reserved when the library's code object is loaded. In host code
+// `scratch` names a host-side stand-in, never device memory; every use
+// goes through the per-device address hipGetSymbolAddress returns.
+constexpr size_t kScratchBytes = size_t(PH_NOALLOC_SCRATCH_BYTES);
+constexpr size_t kScratchAlign = 256;
+constexpr int kMaxDevices = 64;
+constexpr size_t kMaxOperands = 64;
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// Looks up this device's copy of `scratch` once, with the device current.
+int scratch_address(int device, void **out, char **err) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(err, PH_ERR_RUNTIME, "ph_dispatch_noalloc: device ordinal beyond 64");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(err, e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(err, PH_ERR_RUNTIME, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return PH_OK;
+}
+
+// Zero `words` 32-bit words from `p` (grid-stride). A kernel, not
+// hipMemsetAsync, so the clear stays an ordinary kernel node wherever the
+// caller's stream is.
+__global__ void __launch_bounds__(256) zero_words(uint32_t *p, size_t words) {
+  size_t stride = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < words; i += stride) p[i] = 0u;
+}
+
+size_t align_up(size_t x) { return (x + kScratchAlign - 1) / kScratchAlign * kScratchAlign; }
+
+}  // namespace
+
+extern "C" {
+
+size_t ph_noalloc_scratch_bytes(void) { return kScratchBytes; }
+
+int ph_dispatch_noalloc(ph_kernel *k, int64_t grid_x, int64_t grid_y, int64_t grid_z,
+                        int64_t block_x, int64_t lanes, void *stream,
+                        const void *const *inputs, const size_t *input_bytes, size_t n_inputs,
+                        void *const *outputs, const size_t *output_bytes, size_t n_outputs,
+                        char **err) {
+  if (!k) return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_dispatch_noalloc: null kernel");
+  if ((n_inputs && (!inputs || !input_bytes)) || (n_outputs && (!outputs || !output_bytes)))
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_dispatch_noalloc: null operand array");
+  const size_t n_ops = n_inputs + n_outputs;
+  if (n_inputs > kMaxOperands || n_outputs > kMaxOperands || n_ops > kMaxOperands)
+    return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_dispatch_noalloc: more than 64 operands");
+  unsigned int blocks = 0, block = 0;
+  int rc = dispatch_geometry(grid_x, grid_y, grid_z, block_x, lanes, PH_MATH_SAFE, &blocks, &block, err);
+  if (rc != PH_OK) return rc;
+  // Place every operand at a 256-byte boundary; reject what does not fit.
+  size_t offs[kMaxOperands];
+  size_t total = 0;
+  for (size_t i = 0; i < n_ops; ++i) {
+    size_t b = i < n_inputs ? input_bytes[i] : output_bytes[i - n_inputs];
+    offs[i] = total;
+    if (b > kScratchBytes || align_up(b) > kScratchBytes - total)
+      return fail(err, PH_ERR_INVALID_ARGUMENT,
+                  "ph_dispatch_noalloc: operands need more than the " +
+                      std::to_string(kScratchBytes) + "-byte scratch area (operand " +
+                      std::to_string(i) + " of " + std::to_string(b) + " bytes ends past it)");
+    total += align_up(b);
+  }
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return hip_fail(err, e, "hipGetDevice");
+  if (device != k->device)
+    return fail(err, PH_ERR_INVALID_ARGUMENT,
+                "ph_dispatch_noalloc: kernel was loaded on device " + std::to_string(k->device) +
+                    ", current device is " + std::to_string(device));
+  void *base = nullptr;
+  rc = scratch_address(device, &base, err);
+  if (rc != PH_OK) return rc;
+  char *sbase = static_cast<char *>(base);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Once work is queued, every exit waits for it: a queued copy must not
+  // touch the caller's host buffers after we return.
+  auto drain_and = [&](int code) {
+    (void)hipStreamSynchronize(s);  // best effort: `code` is the error reported
+    return code;
+  };
+  for (size_t i = 0; i < n_inputs; ++i) {
+    if (!input_bytes[i]) continue;
+    e = hipMemcpyHtoDAsync(sbase + offs[i], const_cast<void *>(inputs[i]), input_bytes[i], s);
+    if (e != hipSuccess) return drain_and(hip_fail(err, e, "hipMemcpyHtoDAsync"));
+  }
+  // Output slots start at zero (the area keeps the previous call's data).
+  if (n_outputs) {
+    size_t lo = offs[n_inputs];
+    size_t words = (total - lo) / 4;
+    unsigned int zb = (unsigned int)std::min<size_t>((words + 255) / 256, 2048);
+    if (words) {
+      hipLaunchKernelGGL(zero_words, dim3(zb), dim3(256), 0, s,
+                         reinterpret_cast<uint32_t *>(sbase + lo), words);
+      e = hipGetLastError();
+      if (e != hipSuccess) return drain_and(hip_fail(err, e, "zero_words launch"));
+    }
+  }
+  void *ptrs[kMaxOperands];
+  void *params[kMaxOperands];
+  for (size_t i = 0; i < n_ops; ++i) {
+    ptrs[i] = sbase + offs[i];
+    params[i] = &ptrs[i];
+  }
+  e = hipModuleLaunchKernel(k->function, blocks, 1, 1, block, 1, 1, 0, s,
+                            n_ops ? params : nullptr, nullptr);
+  if (e != hipSuccess) return drain_and(hip_fail(err, e, "hipModuleLaunchKernel"));
+  for (size_t i = 0; i < n_outputs; ++i) {
+    if (!output_bytes[i]) continue;
+    e = hipMemcpyDtoHAsync(outputs[i], sbase + offs[n_inputs + i], output_bytes[i], s);
+    if (e != hipSuccess) return drain_and(hip_fail(err, e, "hipMemcpyDtoHAsync"));
+  }
+  e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(err, e, "hipStreamSynchronize");
+  return PH_OK;
 }
 
 int ph_device_count(int *count) {

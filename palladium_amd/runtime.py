@@ -140,6 +140,10 @@ def _declare(L: ctypes.CDLL) -> None:
         "ph_graph_launch": (c.c_int, [_P, _P, _PP]),
         "ph_graph_destroy": (c.c_int, [_P]),
         "ph_dispatch_staging_count": (c.c_size_t, []),
+        "ph_noalloc_scratch_bytes": (c.c_size_t, []),
+        "ph_dispatch_noalloc": (c.c_int, [_P, c.c_int64, c.c_int64, c.c_int64, c.c_int64, c.c_int64, _P, _PP,
+                                          c.POINTER(c.c_size_t), c.c_size_t, _PP, c.POINTER(c.c_size_t),
+                                          c.c_size_t, _PP]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
