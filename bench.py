@@ -610,6 +610,12 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
                        "ops_note": "elementwise eqns of the while condition + body per attempt (pow = 1)",
                        "avg_launch_ms": avg, "active_lane_fraction": active, "total_attempts": total,
                        "accepted": int(acc.sum()), "rejected": int(rej.sum())}
+    # The latency floor: the slowest lane's attempts run strictly one after
+    # another, each no faster than one wavefront's in-order chain through
+    # this build's loop body.
+    lb = bs3_latency_bound(call, host, valu_latencies(), int(attempts.max()), avg)
+    res["roofline"]["latency_frac"] = lb["latency_frac"]
+    res["roofline"]["latency_bound"] = lb
     # SAFE: the mode whose accepted/rejected counts equal the oracle's exactly
     # (IEEE order, deterministic pow); FAST above is the throughput mode.
     safe_bound = bs3_vdp_call(cfg.n, math_mode="safe", name="bs3_vdp_safe").bound(*host)
@@ -884,6 +890,93 @@ def bench_valu_rates(steps: int, warmup: int, cpu: bool) -> dict:
     return res
 
 
+_LAT_OPS = {
+    "v_fma_f32": ("v_fma_f32 %0, %0, %1, %2", ': "v"(b), "v"(c)'),
+    "v_exp_f32": ("v_exp_f32 %0, %0", ""),
+    "v_log_f32": ("v_log_f32 %0, %0", ""),
+    "v_rcp_f32": ("v_rcp_f32 %0, %0", ""),
+}
+_LAT_UNROLL = 32
+_LAT_ITERS = 256
+
+
+def _latency_probe_source(op: str, chains: int) -> str:
+    text, operands = _LAT_OPS[op]
+    body = "\n".join(f'        asm volatile("{text}" : "+v"(a{k % chains}) {operands});'
+                     for k in range(_LAT_UNROLL))
+    init = "\n".join(f"    float a{i} = (float)(threadIdx.x + {i + 1});" for i in range(chains))
+    total = " + ".join(f"a{i}" for i in range(chains))
+    return f"""
+extern "C" __global__ void __launch_bounds__(64) probe(const float* __restrict__ in, float* __restrict__ out) {{
+    float b = in[0], c = in[1];
+{init}
+    for (int it = 0; it < {_LAT_ITERS}; ++it) {{
+{body}
+    }}
+    out[blockIdx.x * 64 + threadIdx.x] = {total};
+}}
+"""
+
+
+def valu_latencies() -> dict:
+    """Nanoseconds per instruction for ONE wavefront per SIMD (1,024 single-wave
+    workgroups): a dependent chain of v_fma_f32 (result latency), dependent
+    chains of v_exp/v_log/v_rcp (transcendental latency), and eight
+    independent v_fma_f32 chains (the issue interval of a lone wavefront)."""
+    from palladium_amd import runtime as rt
+
+    blocks = 1024
+    inb = rt.Buffer.from_numpy(np.array([1, 0], dtype=np.float32))
+    outb = rt.Buffer.empty((blocks * 64,), np.float32)
+    s = rt.Stream()
+
+    def ns_per_instr(op: str, chains: int) -> float:
+        k = rt.Kernel(_latency_probe_source(op, chains), "probe", "fast")
+        k.launch_ptrs(blocks, 64, [inb.ptr, outb.ptr], s)
+        s.synchronize()
+        e0, e1 = rt.Event(), rt.Event()
+        e0.record(s)
+        for _ in range(5):
+            k.launch_ptrs(blocks, 64, [inb.ptr, outb.ptr], s)
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / 5 * 1e6 / (_LAT_ITERS * _LAT_UNROLL)
+
+    out = {"fma_dependent_ns": ns_per_instr("v_fma_f32", 1),
+           "issue_ns": ns_per_instr("v_fma_f32", 8)}
+    trans = {op: ns_per_instr(op, 1) for op in ("v_exp_f32", "v_log_f32", "v_rcp_f32")}
+    out["transcendental_dependent_ns"] = float(np.mean(list(trans.values())))
+    out["per_op_dependent_ns"] = trans
+    return out
+
+
+def bs3_latency_bound(call, host, lat: dict, max_attempts: int, kernel_ms: float) -> dict:
+    """The latency floor of the adaptive loop: the slowest lane runs
+    `max_attempts` attempts back to back, and its wavefront can run one no
+    faster than the in-order chain model of this build's own loop body
+    (palladium_amd.isa) with the measured latencies."""
+    from palladium_amd import isa
+    from palladium_amd import runtime as rt
+
+    bound = call.bound(*host)
+    code = rt.compile_code_object(bound.hip_source, bound.spec.name, "fast")
+    m = isa.loop_model(code, lat["fma_dependent_ns"], lat["transcendental_dependent_ns"], lat["issue_ns"])
+    floor_ms = max_attempts * m.cycles_per_iteration / 1e6
+    return {"ns_per_attempt_chain_model": m.cycles_per_iteration, "loop_instructions": m.instructions,
+            "loop_valu": m.valu, "loop_transcendental": m.transcendental, "max_attempts_one_lane": max_attempts,
+            "measured_ns_per_attempt_slowest_wave": kernel_ms * 1e6 / max_attempts,
+            "latency_floor_ms": floor_ms, "latency_frac": floor_ms / kernel_ms, "latencies_ns": lat}
+
+
+def bench_valu_latency(steps: int, warmup: int, cpu: bool) -> dict:
+    lat = valu_latencies()
+    res = _base("dependent v_fma_f32 latency, one wavefront per SIMD (ns)", lat["fma_dependent_ns"], "ns",
+                5, 1, 0.0, {"workload": "1,024 single-wave workgroups, dependent and independent chains"})
+    res["higher_is_better"] = False
+    res["latencies_ns"] = lat
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -904,7 +997,7 @@ def main() -> int:
     rank = int(os.environ.get("RANK", "0"))
     fns = {"lv": bench_lv, "lv0": bench_lv0, "gbm": bench_gbm, "gbm_block": bench_gbm_block, "gbm_fold_in": bench_gbm_fold_in, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
            "bs3_lockstep": bench_bs3_lockstep, "bs3_sorted": bench_bs3_sorted, "copy": bench_copy, "df32": bench_df32, "dispatch": bench_dispatch,
-           "valu_rates": bench_valu_rates}
+           "valu_rates": bench_valu_rates, "valu_latency": bench_valu_latency}
     if a.workload not in fns:
         raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")
     res = fns[a.workload](a.steps, a.warmup, cpu=not a.no_cpu and rank == 0)

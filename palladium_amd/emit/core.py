@@ -547,9 +547,9 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
 
     body = plan.jaxpr if plan else spec.jaxpr
     if math_mode is not None and math_mode_ordinal(math_mode) == 2:
-        from palladium_amd.emit.optimize import factor_common_products
+        from palladium_amd.emit.optimize import fast_rewrites
 
-        body = factor_common_products(body)
+        body = fast_rewrites(body)
     emit_jaxpr(env, cursor, body, ref_vals)
 
     head = (

@@ -52,7 +52,7 @@ from palladium_amd.trace import KernelSpec
 L, U = "L", "U"
 
 _ELEMENTWISE = set(
-    "add sub mul div rem min max pow neg abs sign exp exp2 log log1p expm1 sin cos tan tanh sqrt rsqrt floor "
+    "add sub mul div rem min max pow neg abs sign exp exp2 log log2 log1p expm1 sin cos tan tanh sqrt rsqrt floor "
     "ceil round logistic atan2 lt le gt ge eq ne and or xor not shift_right_logical shift_right_arithmetic "
     "shift_left clamp select_n integer_pow convert_element_type bitcast_convert_type threefry2x32".split()
 )

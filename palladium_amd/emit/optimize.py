@@ -13,15 +13,38 @@ The compiler finds this for some terms on its own but not across the RK4
 stages; doing it on the jaxpr makes the kernel ~6 % shorter. Only
 single-use product chains are rewritten (no value is recomputed), and only
 equal-shaped float operands (no broadcasting).
+
+A second rewrite shortens power-law step-size controllers (the PI
+controller of `tests/test_08_adaptive.py:76-122`,
+`factor = safety * (1/err)**c1 * prev**c2`), whose chain of reciprocal,
+two branchy `pow` calls and multiplies lies on the serial path from one
+adaptive attempt to the next:
+
+    pow(x, c)              ->  exp2(c * log2(x))      (c a non-integer literal)
+    log2(1 / y)            ->  -log2(y)
+    exp2(a) * exp2(b)      ->  exp2(a + b)            (single-use exp2 values)
+    k * exp2(a)            ->  exp2(log2(k) + a)      (k a positive literal)
+
+so the controller costs one hardware log2 on the chain, FMAs and one
+hardware exp2. For a non-integer exponent `pow(x, c)` and `exp2(c*log2 x)`
+agree on every special operand (finite negative x gives NaN, +-0 gives 0
+or inf, +inf gives inf or 0, NaN propagates) except x = -inf, where pow
+gives +inf or +0 and log2 NaN: a base not provably non-negative from its
+producer (max with a non-negative literal, abs, exp, sqrt) has -inf read
+as +inf first, which also keeps `log2(1/y) = -log2(y)` exact at y = -0
+and y = -inf. The results differ by the rounding of the log and exp,
+within FAST's approximate-transcendental contract.
 """
 
 from __future__ import annotations
 
 from typing import Any
 
+import numpy as np
+
 from palladium_amd.ir import ClosedJaxpr, Jaxpr, JaxprEqn, Literal, ShapedArray, Var, primitive
 
-__all__ = ["factor_common_products"]
+__all__ = ["factor_common_products", "fast_rewrites", "power_laws_to_exp2"]
 
 
 def _same(a: Any, b: Any) -> bool:
@@ -30,14 +53,128 @@ def _same(a: Any, b: Any) -> bool:
     return a is b
 
 
-def _rewrite_sub(v: Any) -> Any:
+def _rewrite_sub(v: Any, fn: Any = None) -> Any:
+    fn = fn or factor_common_products
     if isinstance(v, ClosedJaxpr):
-        return ClosedJaxpr(factor_common_products(v.jaxpr), v.consts)
+        return ClosedJaxpr(fn(v.jaxpr), v.consts)
     if isinstance(v, Jaxpr):
-        return factor_common_products(v)
+        return fn(v)
     if isinstance(v, tuple) and v and all(isinstance(b, ClosedJaxpr) for b in v):
-        return tuple(ClosedJaxpr(factor_common_products(b.jaxpr), b.consts) for b in v)
+        return tuple(ClosedJaxpr(fn(b.jaxpr), b.consts) for b in v)
     return v
+
+
+def fast_rewrites(jaxpr: Jaxpr) -> Jaxpr:
+    """Every FAST-only rewrite, in order."""
+    return factor_common_products(power_laws_to_exp2(jaxpr))
+
+
+def _use_counts(jaxpr: Jaxpr) -> dict[Any, int]:
+    uses: dict[Any, int] = {}
+    for e in jaxpr.eqns:
+        for a in e.invars:
+            if isinstance(a, Var):
+                uses[a] = uses.get(a, 0) + 1
+    for o in jaxpr.outvars:
+        if isinstance(o, Var):
+            uses[o] = uses.get(o, 0) + 2
+    return uses
+
+
+def _f32_literal(v: Any) -> float | None:
+    if isinstance(v, Literal) and np.dtype(v.aval.dtype) == np.float32 and not v.aval.shape:
+        x = float(np.float32(v.val))
+        return x if np.isfinite(x) else None
+    return None
+
+
+def _non_negative(v: Any, producer: dict) -> bool:
+    """Whether `v` is provably >= 0 or NaN (never -inf) from its producer."""
+    e = producer.get(v)
+    if e is None:
+        return False
+    name = e.primitive.name
+    if name in ("abs", "exp", "exp2", "sqrt"):
+        return True
+    if name == "max":
+        return any((_f32_literal(a) or -1.0) >= 0 for a in e.invars)
+    return False
+
+
+def power_laws_to_exp2(jaxpr: Jaxpr) -> Jaxpr:
+    """Rewrite float32 `pow` by non-integer literal exponents, and products
+    of the results, into `exp2` of a linear combination of `log2`s."""
+    uses = _use_counts(jaxpr)
+    producer = {ov: e for e in jaxpr.eqns for ov in e.outvars}
+    exp2_arg: dict[Any, Any] = {}      # outvar of an exp2 made here -> its operand
+    exp2_eqn: dict[Any, JaxprEqn] = {}
+    new_eqns: list[JaxprEqn] = []
+
+    def lit(x: float) -> Literal:
+        return Literal(np.float32(x), ShapedArray((), np.float32, weak_type=True))
+
+
+    def f32(v: Any) -> bool:
+        return np.dtype(getattr(v.aval, "dtype", np.float64)) == np.float32
+
+    for e in jaxpr.eqns:
+        params = {k: _rewrite_sub(v, power_laws_to_exp2) for k, v in e.params.items()}
+        e = JaxprEqn(e.invars, e.outvars, e.primitive, params)
+        name = e.primitive.name
+        out = e.outvars[0] if len(e.outvars) == 1 else None
+        if name == "pow" and out is not None and f32(out) and isinstance(e.invars[0], Var):
+            c = _f32_literal(e.invars[1])
+            x = e.invars[0]
+            if c is not None and c != int(c) and tuple(x.aval.shape) == tuple(out.aval.shape):
+                aval = ShapedArray(out.aval.shape, np.float32)
+                src = producer.get(x)
+                if (src is not None and src.primitive.name == "div" and _f32_literal(src.invars[0]) == 1.0
+                        and isinstance(src.invars[1], Var)
+                        and tuple(src.invars[1].aval.shape) == tuple(out.aval.shape)):
+                    x, c = src.invars[1], -c      # log2(1/y) = -log2(y)
+                if not _non_negative(x, producer):
+                    # pow(-inf, c) is +inf or +0, log2(-inf) is NaN: read -inf as +inf
+                    is_ninf, xs = Var(ShapedArray(out.aval.shape, np.bool_)), Var(aval)
+                    new_eqns.append(JaxprEqn([x, lit(-np.inf)], [is_ninf], primitive("eq"), {}))
+                    new_eqns.append(JaxprEqn([is_ninf, x, lit(np.inf)], [xs], primitive("select_n"), {}))
+                    x = xs
+                lg, m = Var(aval), Var(aval)
+                new_eqns.append(JaxprEqn([x], [lg], primitive("log2"), {}))
+                new_eqns.append(JaxprEqn([lit(c), lg], [m], primitive("mul"), {}))
+                ex = JaxprEqn([m], [out], primitive("exp2"), {})
+                new_eqns.append(ex)
+                exp2_arg[out], exp2_eqn[out] = m, ex
+                continue
+        if name == "mul" and out is not None and f32(out):
+            a, b = e.invars
+            shape = tuple(out.aval.shape)
+
+            def single_exp2(v: Any) -> bool:
+                return (isinstance(v, Var) and v in exp2_arg and uses.get(v, 0) == 1
+                        and tuple(v.aval.shape) == shape)
+
+            terms = None
+            if single_exp2(a) and single_exp2(b):
+                terms = (exp2_arg[a], exp2_arg[b], (a, b))
+            else:
+                for k, v in ((a, b), (b, a)):
+                    kv = _f32_literal(k)
+                    if kv is not None and kv > 0 and single_exp2(v):
+                        terms = (lit(float(np.log2(np.float64(kv)))), exp2_arg[v], (v,))
+                        break
+            if terms is not None:
+                p, q, gone = terms
+                dead = {id(exp2_eqn[g]) for g in gone}
+                new_eqns = [x for x in new_eqns if id(x) not in dead]
+                aval = ShapedArray(shape, np.float32)
+                ssum = Var(aval)
+                new_eqns.append(JaxprEqn([p, q], [ssum], primitive("add"), {}))
+                ex = JaxprEqn([ssum], [out], primitive("exp2"), {})
+                new_eqns.append(ex)
+                exp2_arg[out], exp2_eqn[out] = ssum, ex
+                continue
+        new_eqns.append(e)
+    return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)
 
 
 def factor_common_products(jaxpr: Jaxpr) -> Jaxpr:

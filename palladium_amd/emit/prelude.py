@@ -15,6 +15,8 @@
   t = (m-1)/(m+1), as an odd series in t; exp by reduction z = k ln2 + r,
   |r| <= ln2/2, and a degree-13 Taylor polynomial; both carried in double,
   so the float result is the correctly rounded double value rounded once.
+- `ph_exp2`/`ph_log2`: under FAST the hardware base-2 exponential and
+  logarithm; libm otherwise.
 - `ph_sin`/`ph_cos`: under FAST the hardware sine/cosine (the reference's
   FAST contract allows approximate transcendentals); libm-accurate otherwise.
 - `ph_fmin`/`ph_fmax`: NaN-suppressing min/max (C fminf/fmaxf), the
@@ -63,7 +65,12 @@ __device__ __forceinline__ void ph_threefry2x32(unsigned int k0, unsigned int k1
 __device__ __forceinline__ float ph_sin(float x) { return __builtin_amdgcn_sinf(x * 0.15915494309189535f); }
 __device__ __forceinline__ float ph_cos(float x) { return __builtin_amdgcn_cosf(x * 0.15915494309189535f); }
 __device__ __forceinline__ float ph_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+/* v_exp_f32 / v_log_f32: 2^x and log2(x), 1 ulp, subnormals flushed. */
+__device__ __forceinline__ float ph_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float ph_log2(float x) { return __builtin_amdgcn_logf(x); }
 #else
+__device__ __forceinline__ float ph_exp2(float x) { return exp2f(x); }
+__device__ __forceinline__ float ph_log2(float x) { return log2f(x); }
 __device__ __forceinline__ float ph_sin(float x) { return sinf(x); }
 __device__ __forceinline__ float ph_cos(float x) { return cosf(x); }
 __device__ __forceinline__ float ph_exp(float x) { return expf(x); }

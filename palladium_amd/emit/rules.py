@@ -97,8 +97,9 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
         return "(({a} > 0.0f) ? 1.0f : (({a} < 0.0f) ? -1.0f : {a}))" if f else "(({a} > 0) - ({a} < 0))"
     unary_f = {
         "exp": "ph_exp({a})",
-        "exp2": "exp2f({a})",
+        "exp2": "ph_exp2({a})",
         "log": "logf({a})",
+        "log2": "ph_log2({a})",
         "log1p": "log1pf({a})",
         "expm1": "ph_expm1({a})",
         "sin": "ph_sin({a})",
@@ -141,7 +142,7 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
 
 # The elementwise subset, for discoverability and rule registration.
 ELEMENTWISE = (
-    "add sub mul div rem min max pow neg abs sign exp exp2 log log1p expm1 sin cos "
+    "add sub mul div rem min max pow neg abs sign exp exp2 log log2 log1p expm1 sin cos "
     "tan tanh sqrt rsqrt floor ceil round logistic atan2 lt le gt ge eq ne and or xor "
     "not shift_right_logical shift_right_arithmetic shift_left clamp"
 ).split()

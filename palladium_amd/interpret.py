@@ -256,7 +256,7 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
             r = np.abs(a)
         elif name == "sign":
             r = _sign(a) if isf else np.sign(a)
-        elif name in ("exp", "exp2", "log", "log1p", "expm1", "sin", "cos", "tan", "tanh", "sqrt", "floor", "ceil"):
+        elif name in ("exp", "exp2", "log", "log2", "log1p", "expm1", "sin", "cos", "tan", "tanh", "sqrt", "floor", "ceil"):
             r = getattr(np, name)(a)
         elif name == "rsqrt":
             r = np.asarray(1.0, a.dtype) / np.sqrt(a)
@@ -338,7 +338,7 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
 
 
 _ELEMENTWISE = set(
-    "add sub mul div rem min max pow neg abs sign exp exp2 log log1p expm1 sin cos tan tanh sqrt rsqrt floor "
+    "add sub mul div rem min max pow neg abs sign exp exp2 log log2 log1p expm1 sin cos tan tanh sqrt rsqrt floor "
     "ceil round logistic atan2 lt le gt ge eq ne and or xor not shift_right_logical shift_right_arithmetic "
     "shift_left clamp select_n integer_pow convert_element_type bitcast_convert_type".split()
 )

@@ -165,3 +165,80 @@ def test_rewrite_fuzz_is_not_vacuous():
                      *[np.zeros(64, np.float32)] * 3)
         fired += _count(_rewritten(spec).jaxpr, "mul") < _count(spec.jaxpr, "mul")
     assert fired >= 10
+
+
+# ---------------------------------------------------------------------------
+# power-law rewrite: pow by non-integer literals -> exp2 of a sum of log2s
+
+from palladium_amd.emit.optimize import power_laws_to_exp2  # noqa: E402
+
+
+def _pl(spec):
+    return dataclasses.replace(spec, jaxpr=power_laws_to_exp2(spec.jaxpr))
+
+
+def test_bs3_controller_becomes_one_exp2():
+    cfg = dataclasses.replace(BS3Config(), n=128, t1=2.0)
+    args = bs3_inputs(128)
+    spec = trace(bs3_vdp_call(128, cfg)._staged, *args)
+    opt = _pl(spec)
+    assert _count(spec.jaxpr, "pow") == 2
+    assert _count(opt.jaxpr, "pow") == 0
+    assert _count(opt.jaxpr, "exp2") == 1        # both powers and the safety factor in one exp2
+    assert _count(opt.jaxpr, "log2") == 2        # log2(err) on the chain, log2(prev) off it
+    assert _count(opt.jaxpr, "select_n") == _count(spec.jaxpr, "select_n") + 1  # only prev needs the -inf guard
+    assert _count(opt.jaxpr, "div") == _count(spec.jaxpr, "div")  # 1/err still feeds the carry
+    got = interpret_spec(opt, *args)
+    want = interpret_spec(spec, *args)
+    np.testing.assert_allclose(got[0], want[0], rtol=1e-5)
+    np.testing.assert_allclose(got[1], want[1], rtol=1e-3, atol=1e-4)
+    # accept/reject decisions near err = 1 may flip and shift a lane's
+    # count by a few attempts; the totals stay put
+    assert np.all(np.abs(got[3].astype(int) - want[3]) <= 0.1 * want[3] + 5)
+    assert abs(int(got[3].sum()) - int(want[3].sum())) <= 0.02 * want[3].sum()
+
+
+def _power_kernel(c1, c2, k):
+    def kernel(x_ref, y_ref, o_ref, p_ref):
+        x, y = x_ref[...], y_ref[...]
+        o_ref[...] = k * (1.0 / x) ** c1 * y ** c2
+        p_ref[...] = x ** c1
+    return kernel
+
+
+def test_power_law_rewrite_special_operands():
+    """pow(x, c) for non-integer c and exp2(c log2 x) agree on zeros,
+    infinities, NaN and negative bases. (Finite bases stay where no single
+    power overflows: a product whose factors overflow and underflow is
+    finite in the fused form, as reassociation allows.)"""
+    vals = np.array([0.0, -0.0, np.inf, 1.0, 2.0, 0.5, 1e-3, 3e3, -1.0, -np.inf, np.nan, 7.0], np.float32)
+    x, y = np.meshgrid(vals, vals)
+    x, y = x.ravel().copy(), y.ravel().copy()
+    n = x.size
+    for c1, c2, k in ((0.2333, -0.1333, 0.9), (1.5, 0.5, 2.0), (-0.7, 2.5, 1.0)):
+        call = pl.pallas_call(_power_kernel(c1, c2, k), out_shape=(pl.ShapeDtypeStruct((n,), np.float32),) * 2)
+        spec = trace(call, x, y)
+        opt = _pl(spec)
+        assert _count(opt.jaxpr, "pow") == 0
+        for g, w in zip(interpret_spec(opt, x, y), interpret_spec(spec, x, y)):
+            same_class = (np.isnan(g) == np.isnan(w)) & (np.isinf(g) == np.isinf(w)) & ((g == 0) == (w == 0))
+            ok = same_class
+            assert ok.all(), (c1, c2, x[~ok], y[~ok], g[~ok], w[~ok])
+            fin = np.isfinite(w) & (w != 0) & (np.abs(w) < 1e37) & (np.abs(w) > 1e-37)
+            np.testing.assert_allclose(g[fin], w[fin], rtol=5e-6)
+
+
+def test_power_law_rewrite_leaves_integer_exponents_and_shared_values():
+    def kernel(x_ref, o_ref, p_ref):
+        x = x_ref[...]
+        q = x ** 0.5
+        o_ref[...] = x ** 2.0 * q      # integer power untouched
+        p_ref[...] = q                  # q has a second use: the product keeps its own exp2
+
+    x = np.linspace(-2, 2, 64, dtype=np.float32)
+    spec = trace(pl.pallas_call(kernel, out_shape=(pl.ShapeDtypeStruct((64,), np.float32),) * 2), x)
+    opt = _pl(spec)
+    assert _count(opt.jaxpr, "pow") == 1
+    assert _count(opt.jaxpr, "exp2") == 1
+    for g, w in zip(interpret_spec(opt, x), interpret_spec(spec, x)):
+        np.testing.assert_allclose(g, w, rtol=5e-6)
