@@ -583,6 +583,22 @@ def bench_gbm_fold_in(steps: int, warmup: int, cpu: bool) -> dict:
     return res
 
 
+def _compacted_lane_fraction(attempts: np.ndarray) -> float:
+    """Useful lane-iterations over issued ones under workgroup compaction:
+    each epoch a 1,024-lane workgroup issues ceil(live / 64) wavefronts for
+    EPOCH iterations (an upper bound: a wavefront leaves an epoch early
+    when all its lanes finish)."""
+    from palladium_amd.emit.compact import EPOCH, WORKGROUP
+
+    issued = 0
+    for g in range(attempts.size // WORKGROUP):
+        a = np.sort(attempts[g * WORKGROUP:(g + 1) * WORKGROUP])
+        ends = np.arange(EPOCH, int(a[-1]) + EPOCH, EPOCH)
+        live = WORKGROUP - np.searchsorted(a, ends - EPOCH, side="right")
+        issued += int(np.sum(-(-live // 64))) * EPOCH * 64
+    return float(attempts.sum() / issued) if issued else 1.0
+
+
 def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     from palladium_amd import runtime as rt
     from palladium_amd.workloads import BS3_CFG, bs3_inputs, bs3_vdp_call
@@ -598,7 +614,12 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     rej = outs[4].to_numpy().astype(np.int64)
     attempts = acc + rej
     waves = attempts[: (cfg.n // 64) * 64].reshape(-1, 64)
+    # useful lane-attempts over issued ones if each wavefront ran to its
+    # slowest lane (no compaction), and with 1,024-lane workgroups repacked
+    # every EPOCH iterations (replayed from the returned counts)
     active = float(waves.sum() / (waves.max(axis=1).sum() * 64))
+    compacted = "__syncthreads" in bound.hip_source
+    active_c = _compacted_lane_fraction(attempts) if compacted else active
     total = int(attempts.sum())
     res = _base("BS3(2)+PI attempted steps/s (Van der Pol, N=262,144, fp32)", total / (ms / 1e3), "attempts/s",
                 steps, warmup, ms, {"workload": "adaptive BS3(2) Van der Pol, config 2", "n": cfg.n, "math_mode": "fast"})
@@ -608,7 +629,8 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     res["roofline"] = {"bound": "valu", "achieved": achieved / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TOP/s",
                        "frac": achieved / FP32_PEAK, "traffic": None, "ops_per_attempt": ops,
                        "ops_note": "elementwise eqns of the while condition + body per attempt (pow = 1)",
-                       "avg_launch_ms": avg, "active_lane_fraction": active, "total_attempts": total,
+                       "avg_launch_ms": avg, "lane_compaction": compacted, "active_lane_fraction": active_c,
+                       "active_lane_fraction_uncompacted": active, "total_attempts": total,
                        "accepted": int(acc.sum()), "rejected": int(rej.sum())}
     # The latency floor: the slowest lane's attempts run strictly one after
     # another, each no faster than one wavefront's in-order chain through

@@ -1,0 +1,208 @@
+"""Workgroup lane compaction for divergent `while_loop`s.
+
+An adaptive solver's per-lane `while_loop` keeps a wavefront issuing until
+its slowest lane finishes; on config 2 (Van der Pol, mu log-uniform) half
+the lane-attempts of a wavefront do no work. When a kernel's loop runs one
+program instance per lane with nothing lane-specific inside it, the
+instance is only its loop state: the carries and the loop's operands. Then
+the state of a live instance can move to another lane, and a 1,024-lane
+workgroup can repack its live instances into its lowest wavefronts every
+`EPOCH` iterations, so emptied wavefronts stop issuing:
+
+    epoch:  run up to EPOCH predicated iterations (a wavefront leaves the
+            epoch early once none of its lanes is live);
+            lanes whose instance finished store its carries in LDS at the
+            instance's own slot;
+            count the live lanes per wavefront (ballot, popcount);
+            if packing frees a wavefront, live lanes write their state to
+            LDS at their rank among the live (prefix over wavefronts +
+            mbcnt) and lanes [0, live) read it back;
+            stop when no lane of the workgroup is live.
+    after:  every lane reloads its own instance's final carries.
+
+Each instance runs exactly the operations it ran before, in the same
+order: results are bit-identical with and without compaction. Wavefront w
+of a 1,024-lane workgroup shares its SIMD with w ± 4, w ± 8 ... (measured
+on MI355X: consecutive wavefronts land on the CU's four SIMDs in turn), so
+packing into the lowest wavefronts keeps the four SIMDs evenly loaded.
+
+The control flow around each barrier is uniform over the workgroup (the
+epoch loop stops on a count read from LDS), and every lane of the launch
+exists (the grid is a whole number of workgroups), so every wavefront
+meets every barrier.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import os
+from typing import Any
+
+import numpy as np
+
+from palladium_amd.ir import KeyAval
+
+WORKGROUP = 1024
+EPOCH = 32
+# LDS per workgroup the compaction may use (2 workgroups per CU fit in 160 KB).
+LDS_BUDGET = 72 * 1024
+
+_LANE_SPECIFIC = {"program_id", "num_programs", "get", "swap", "lane_index", "lane_reduce", "while"}
+_STORABLE = {"float32": "f", "int32": "i", "uint32": "u", "bool": "b"}
+
+
+@dataclasses.dataclass(frozen=True)
+class CompactPlan:
+    index: int  # position of the loop among the top-level eqns
+
+
+def _jaxpr(j: Any) -> Any:
+    return getattr(j, "jaxpr", j)
+
+
+def _lane_free(jaxpr: Any) -> bool:
+    for e in _jaxpr(jaxpr).eqns:
+        if e.primitive.name in _LANE_SPECIFIC:
+            return False
+        for v in e.params.values():
+            for sub in (v if isinstance(v, tuple) else (v,)):
+                if hasattr(_jaxpr(sub), "eqns") and not _lane_free(sub):
+                    return False
+    return True
+
+
+def _storable(v: Any) -> bool:
+    aval = getattr(v, "aval", None)
+    if aval is None or isinstance(aval, KeyAval):
+        return False
+    if int(np.prod(aval.shape)) != 1:
+        return False
+    return np.dtype(aval.dtype).name in _STORABLE
+
+
+def enabled() -> bool:
+    return os.environ.get("PALLADIUM_WHILE_COMPACTION", "1") != "0"
+
+
+def plan_for(spec: Any, jaxpr: Any, lanes: int, block: int | None) -> CompactPlan | None:
+    """The loop to compact, or None. Needs: one lane per instance, a 1-D
+    grid that fills whole 1,024-lane workgroups, no explicit workgroup size
+    other than 1,024, and exactly one top-level `while` whose condition
+    and body touch no ref, program id or nested while, with scalar
+    4-byte-or-bool carries and operands."""
+    if not enabled() or lanes != 1 or len(spec.grid) != 1:
+        return None
+    if block not in (None, WORKGROUP) or spec.num_programs % WORKGROUP:
+        return None
+    whiles = [k for k, e in enumerate(jaxpr.eqns) if e.primitive.name == "while"]
+    if len(whiles) != 1:
+        return None
+    e = jaxpr.eqns[whiles[0]]
+    if getattr(e.params["cond_jaxpr"], "consts", None) or getattr(e.params["body_jaxpr"], "consts", None):
+        return None
+    if not (_lane_free(e.params["cond_jaxpr"]) and _lane_free(e.params["body_jaxpr"])):
+        return None
+    if not all(_storable(v) for v in list(e.invars) + list(e.outvars)):
+        return None
+    used = {v for x in jaxpr.eqns for v in x.invars} | set(jaxpr.outvars)
+    n_state = len(e.invars) + 1  # operands and carries, plus the slot index
+    n_kept = sum(1 for v in e.outvars if v in used)  # final carries read after the loop
+    if (n_state + n_kept) * WORKGROUP * 4 > LDS_BUDGET:
+        return None
+    return CompactPlan(whiles[0])
+
+
+def _to_bits(expr: str, ctype: str) -> str:
+    if ctype == "float":
+        return f"__float_as_uint({expr})"
+    if ctype == "bool":
+        return f"({expr} ? 1u : 0u)"
+    return f"(unsigned int)({expr})"
+
+
+def _from_bits(expr: str, ctype: str) -> str:
+    if ctype == "float":
+        return f"__uint_as_float({expr})"
+    if ctype == "bool":
+        return f"({expr} != 0u)"
+    return f"({ctype})({expr})"
+
+
+def emit_compacting_while(env: Any, cursor: Any, eqn: Any, emit_jaxpr: Any, declare_carries: Any,
+                          copy_back: Any) -> None:
+    """Emit `eqn` (a top-level `while`) with workgroup lane compaction."""
+    cn = int(eqn.params["cond_nconsts"])
+    bn = int(eqn.params["body_nconsts"])
+    cj = _jaxpr(eqn.params["cond_jaxpr"])
+    bj = _jaxpr(eqn.params["body_jaxpr"])
+    # The loop's operands move with their instance: private copies.
+    consts = []
+    for v in eqn.invars[: cn + bn]:
+        src = env.val(v)
+        name = cursor.fresh("_k")
+        cursor.emit(f"{src.ctype} {name} = {src.at('0')};")
+        consts.append(dataclasses.replace(src, expr=name, space="local", readonly=False))
+    cond_consts, body_consts = consts[:cn], consts[cn:]
+    carries = declare_carries(env, cursor, eqn.invars[cn + bn:], eqn.outvars)
+    state = consts + carries
+    kept = [(k, c) for k, (c, ov) in enumerate(zip(carries, eqn.outvars)) if env.used(ov)]
+    nw = WORKGROUP // 64
+    buf, res, cnt = cursor.fresh("_cbuf"), cursor.fresh("_cres"), cursor.fresh("_ccnt")
+    cursor.emit(f"__shared__ unsigned int {buf}[{len(state) + 1}][{WORKGROUP}];")
+    if kept:
+        cursor.emit(f"__shared__ unsigned int {res}[{len(kept)}][{WORKGROUP}];")
+    cursor.emit(f"__shared__ int {cnt}[{nw}];")
+    slot, own = cursor.fresh("_slot"), cursor.fresh("_own")
+    cursor.emit(f"int {slot} = (int)threadIdx.x;  // the instance this lane holds; -1: none")
+    wave = cursor.fresh("_wv")
+    cursor.emit(f"const int {wave} = (int)(threadIdx.x >> 6);")
+    with cursor.block("while (true)"):
+        ep = cursor.fresh("_ep")
+        with cursor.block(f"for (int {ep} = 0; {ep} < {EPOCH}; ++{ep})"):
+            (pred,) = emit_jaxpr(env, cursor, cj, cond_consts + carries)
+            live = cursor.fresh("_live")
+            cursor.emit(f"const bool {live} = ({pred.at('0')}) && {slot} >= 0;")
+            with cursor.block(f"if (!__any({live}))"):
+                cursor.emit("break;")
+            outs = emit_jaxpr(env, cursor, bj, body_consts + carries)
+            copy_back(cursor, outs, carries, predicate=live)
+        # Epoch boundary: the same condition, on the state as it stands.
+        (pred,) = emit_jaxpr(env, cursor, cj, cond_consts + carries)
+        cursor.emit(f"bool {own} = ({pred.at('0')}) && {slot} >= 0;")
+        with cursor.block(f"if (!{own} && {slot} >= 0)"):
+            for j, (_, c) in enumerate(kept):
+                cursor.emit(f"{res}[{j}][{slot}] = {_to_bits(c.expr, c.ctype)};")
+            cursor.emit(f"{slot} = -1;")
+        mask, total, before, active = (cursor.fresh(p) for p in ("_cm", "_ctot", "_cbef", "_cact"))
+        cursor.emit(f"const unsigned long long {mask} = __ballot({own});")
+        with cursor.block("if ((threadIdx.x & 63u) == 0u)"):
+            cursor.emit(f"{cnt}[{wave}] = (int)__popcll({mask});")
+        cursor.emit("__syncthreads();")
+        cursor.emit(f"int {total} = 0, {before} = 0, {active} = 0;")
+        w = cursor.fresh("_cw")
+        with cursor.block(f"for (int {w} = 0; {w} < {nw}; ++{w})"):
+            cursor.emit(f"const int _c = {cnt}[{w}];")
+            cursor.emit(f"{total} += _c; {before} += ({w} < {wave}) ? _c : 0; {active} += (_c > 0) ? 1 : 0;")
+        with cursor.block(f"if ({total} == 0)"):
+            cursor.emit("break;")
+        # Repack only when it frees a wavefront (the decision is uniform).
+        with cursor.block(f"if (({total} + 63) / 64 < {active})"):
+            with cursor.block(f"if ({own})"):
+                pos = cursor.fresh("_cpos")
+                cursor.emit(f"const int {pos} = {before} + (int)__builtin_amdgcn_mbcnt_hi("
+                            f"(unsigned int)({mask} >> 32), __builtin_amdgcn_mbcnt_lo((unsigned int){mask}, 0u));")
+                for j, c in enumerate(state):
+                    cursor.emit(f"{buf}[{j}][{pos}] = {_to_bits(c.expr, c.ctype)};")
+                cursor.emit(f"{buf}[{len(state)}][{pos}] = (unsigned int){slot};")
+            cursor.emit("__syncthreads();")
+            with cursor.block(f"if ((int)threadIdx.x < {total})"):
+                for j, c in enumerate(state):
+                    cursor.emit(f"{c.expr} = {_from_bits(f'{buf}[{j}][threadIdx.x]', c.ctype)};")
+                cursor.emit(f"{slot} = (int){buf}[{len(state)}][threadIdx.x];")
+            with cursor.block("else"):
+                cursor.emit(f"{slot} = -1;")
+        # Nothing is written to LDS again before every lane has read.
+        cursor.emit("__syncthreads();")
+    # Every instance has finished: each lane takes its own back.
+    for j, (_, c) in enumerate(kept):
+        cursor.emit(f"{c.expr} = {_from_bits(f'{res}[{j}][threadIdx.x]', c.ctype)};")

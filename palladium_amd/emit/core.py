@@ -440,6 +440,11 @@ def launch_geometry(spec: KernelSpec, block: int | None = None, lanes: int | Non
     lanes = lanes if lanes is not None else lanes_of(spec)
     if lanes > 1:
         b = workgroup_for(lanes, block)
+    else:
+        from palladium_amd.emit.compact import WORKGROUP, plan_for
+
+        if plan_for(spec, spec.jaxpr, lanes, block) is not None:
+            b = WORKGROUP  # a compacting while loop repacks 1,024-lane workgroups
     threads = n * lanes
     if threads >= 2**31:
         raise EmitError(f"grid {spec.grid} needs more than 2**31 lanes")
@@ -550,6 +555,12 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         from palladium_amd.emit.optimize import fast_rewrites
 
         body = fast_rewrites(body)
+    from palladium_amd.emit.compact import plan_for
+
+    cplan = plan_for(spec, body, lanes, block)
+    if (cplan is not None) != (plan is None and geo.block == 1024 and plan_for(spec, spec.jaxpr, lanes, block) is not None):
+        raise EmitError("internal: while-loop compaction disagrees with the launch geometry")
+    env.compact = body.eqns[cplan.index] if cplan is not None else None  # type: ignore[attr-defined]
     emit_jaxpr(env, cursor, body, ref_vals)
 
     head = (

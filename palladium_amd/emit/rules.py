@@ -818,6 +818,11 @@ def _rule_while(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     bj = eqn.params["body_jaxpr"]
     if getattr(cj, "consts", None) or getattr(bj, "consts", None):
         raise EmitError("while with jaxpr consts is unsupported")
+    if getattr(env, "compact", None) is eqn:
+        from palladium_amd.emit.compact import emit_compacting_while
+
+        emit_compacting_while(env, cursor, eqn, emit_jaxpr, _declare_carries, copy_back_carries)
+        return
     cond_consts = [env.val(v) for v in eqn.invars[:cn]]
     body_consts = [env.val(v) for v in eqn.invars[cn : cn + bn]]
     carries = _declare_carries(env, cursor, eqn.invars[cn + bn :], eqn.outvars)

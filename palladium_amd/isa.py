@@ -128,24 +128,23 @@ def parse(asm: str) -> list[Instr]:
 
 
 def loop_body(instrs: list[Instr]) -> list[Instr]:
-    """The hot loop's body: of the spans from a backward branch's target to
-    the branch, the one with the most vector instructions. (A
-    `while (true) { if (!any(live)) break; ... }` loop also compiles to a
-    short backward branch on its exit path, which is not the loop.)"""
-    best: list[Instr] | None = None
-    best_valu = -1
+    """The hot loop's body. Of the spans from a backward branch's target to
+    the branch holding at least a quarter of the vector instructions of the
+    largest such span, the shortest: an epoch loop around the hot loop is
+    longer, and the short backward branch a
+    `while (true) { if (!any(live)) break; ... }` loop compiles to on its
+    exit path holds too little."""
+    spans = []
     for k, ins in enumerate(instrs):
         if ins.target is not None and ins.target <= ins.addr:
             start = next((j for j, x in enumerate(instrs) if x.addr == ins.target), None)
-            if start is None:
-                continue
-            body = instrs[start:k + 1]
-            valu = sum(b.op.startswith("v_") for b in body)
-            if valu > best_valu:
-                best, best_valu = body, valu
-    if best is None:
+            if start is not None:
+                spans.append((start, k, sum(b.op.startswith("v_") for b in instrs[start:k + 1])))
+    if not spans:
         raise ValueError("no backward branch: the kernel has no loop")
-    return best
+    top = max(s[2] for s in spans)
+    best = min((s for s in spans if 4 * s[2] >= top), key=lambda s: s[1] - s[0])
+    return instrs[best[0]:best[1] + 1]
 
 
 def _latency(op: str, lat_valu: float, lat_trans: float, lat_salu: float) -> float:

@@ -1,0 +1,75 @@
+"""Which loops get workgroup lane compaction, and the launch geometry that
+goes with it (CPU: emission only)."""
+
+import numpy as np
+import pytest
+
+import palladium_amd as pa
+from palladium_amd.emit import emit_hip, launch_geometry
+from palladium_amd.frontend import jnp, lax, pl
+from palladium_amd.trace import trace
+from palladium_amd.workloads import bs3_inputs, bs3_vdp_call
+
+
+def _bs3_spec(n):
+    return trace(bs3_vdp_call(n)._staged, *bs3_inputs(n))
+
+
+def test_bs3_loop_is_compacted_in_1024_lane_workgroups():
+    spec = _bs3_spec(4096)
+    assert launch_geometry(spec).block == 1024
+    src = emit_hip(spec, math_mode="fast")
+    assert src.count("__syncthreads()") == 3
+    assert "__launch_bounds__(1024)" in src
+    # only the five carries read after the loop keep a result slot
+    assert "_cres" in src and "[5][1024]" in src
+
+
+@pytest.mark.parametrize("n", [1000, 1536, 512])
+def test_partial_workgroups_are_not_compacted(n):
+    spec = _bs3_spec(n)
+    assert launch_geometry(spec).block == 256
+    assert "__syncthreads" not in emit_hip(spec)
+
+
+def test_explicit_workgroup_size_and_env_switch(monkeypatch):
+    spec = _bs3_spec(4096)
+    assert launch_geometry(spec, 256).block == 256
+    assert "__syncthreads" not in emit_hip(spec, block=256)
+    assert "__syncthreads" in emit_hip(spec, block=1024)
+    monkeypatch.setenv("PALLADIUM_WHILE_COMPACTION", "0")
+    assert launch_geometry(spec).block == 256
+    assert "__syncthreads" not in emit_hip(spec)
+
+
+def _loop_kernel(use_pid=False, vector=False):
+    def kernel(x_ref, o_ref):
+        x = x_ref[...]
+        if vector:
+            x = jnp.broadcast_to(x, (1,))
+
+        def cond(c):
+            return c[0] > 1
+
+        def body(c):
+            v, k = c
+            extra = pl.program_id(0) * 0 if use_pid else 0
+            return jnp.where(v % 2 == 0, v // 2, 3 * v + 1) + extra, k + 1
+
+        _, k = lax.while_loop(cond, body, (x, jnp.zeros_like(x)))
+        o_ref[...] = k
+
+    return kernel
+
+
+def test_loops_reading_the_program_id_are_not_compacted():
+    n = 2048
+    spec_ok = trace(pl.pallas_call(_loop_kernel(), grid=(n,), in_specs=[pl.BlockSpec((1,), lambda i: (i,))],
+                                   out_specs=pl.BlockSpec((1,), lambda i: (i,)),
+                                   out_shape=pl.ShapeDtypeStruct((n,), np.int32)), np.ones(n, np.int32))
+    assert "__syncthreads" in emit_hip(spec_ok)
+    spec_pid = trace(pl.pallas_call(_loop_kernel(use_pid=True), grid=(n,),
+                                    in_specs=[pl.BlockSpec((1,), lambda i: (i,))],
+                                    out_specs=pl.BlockSpec((1,), lambda i: (i,)),
+                                    out_shape=pl.ShapeDtypeStruct((n,), np.int32)), np.ones(n, np.int32))
+    assert "__syncthreads" not in emit_hip(spec_pid)
