@@ -43,7 +43,7 @@ import numpy as np
 from palladium_amd.ir import KeyAval
 
 WORKGROUP = 1024
-EPOCH = 32
+EPOCH = 64
 # LDS per workgroup the compaction may use (2 workgroups per CU fit in 160 KB).
 LDS_BUDGET = 72 * 1024
 

@@ -142,25 +142,32 @@ __device__ __forceinline__ double ph_exp_dbl(double z) {
     return ldexp(p, (int)kd);
 }
 
+/* Branch-free: the main path runs on a harmless base for special operands
+   and the C99 special cases are selected over it, highest priority last,
+   so the loop around it carries no exec-mask branches. Same results as
+   oracle/oracle.c:oracle_pow, which tests them in order. */
 __device__ __forceinline__ float ph_pow(float x, float y) {
-    if (y == 0.0f || x == 1.0f) return 1.0f;
-    if (x != x || y != y) return x + y;
+    const float inf = __builtin_inff();
     float ax = fabsf(x);
     float ay = fabsf(y);
-    bool y_int = (ay < 16777216.0f) ? (truncf(y) == y) : true;
-    bool y_odd = y_int && (ay < 16777216.0f) && (fmodf(ay, 2.0f) == 1.0f);
-    if (x < 0.0f && !y_int && ax != __builtin_inff()) return __builtin_nanf("");
-    if (ay == __builtin_inff()) {
-        if (ax == 1.0f) return 1.0f;
-        return ((ax > 1.0f) == (y > 0.0f)) ? __builtin_inff() : 0.0f;
-    }
+    bool small = ay < 16777216.0f;
+    bool y_int = small ? (truncf(y) == y) : true;
+    /* fmodf(ay, 2) == 1 for an integral ay below 2^24, exactly */
+    bool y_odd = y_int && small && (ay - 2.0f * truncf(0.5f * ay) == 1.0f);
     float sign = (__builtin_signbit(x) && y_odd) ? -1.0f : 1.0f; /* -0 too: pow(-0, 3) = -0 */
-    if (ax == 0.0f) return (y < 0.0f) ? sign * __builtin_inff() : sign * 0.0f;
-    if (ax == __builtin_inff()) return (y < 0.0f) ? sign * 0.0f : sign * __builtin_inff();
-    double z = (double)y * ph_ln_pos((double)ax);
-    if (z > 89.0) return sign * __builtin_inff();
-    if (z < -104.0) return sign * 0.0f;
-    return sign * (float)ph_exp_dbl(z);
+    bool finite_base = ax > 0.0f && ax < inf;
+    double z = (double)y * ph_ln_pos((double)(finite_base ? ax : 1.0f));
+    double zc = fmin(fmax(z, -104.0), 89.0);
+    float r = sign * (float)ph_exp_dbl(zc);
+    r = (z > 89.0) ? sign * inf : r;
+    r = (z < -104.0) ? sign * 0.0f : r;
+    r = (ax == inf) ? ((y < 0.0f) ? sign * 0.0f : sign * inf) : r;
+    r = (ax == 0.0f) ? ((y < 0.0f) ? sign * inf : sign * 0.0f) : r;
+    r = (ay == inf) ? ((ax == 1.0f) ? 1.0f : (((ax > 1.0f) == (y > 0.0f)) ? inf : 0.0f)) : r;
+    r = (x < 0.0f && !y_int && ax != inf) ? __builtin_nanf("") : r;
+    r = (x != x || y != y) ? x + y : r;
+    r = (y == 0.0f || x == 1.0f) ? 1.0f : r;
+    return r;
 }
 #elif PH_MATH_MODE == 2
 /* FAST: x^y = 2^(y log2 x) on the hardware base-2 logarithm and
