@@ -27,7 +27,7 @@ import re
 import subprocess
 import tempfile
 
-__all__ = ["Instr", "LoopModel", "disassemble", "loop_body", "loop_model", "parse"]
+__all__ = ["Instr", "LoopModel", "disassemble", "issue_slots", "loop_body", "loop_model", "parse"]
 
 OBJDUMP = os.environ.get("PALLADIUM_OBJDUMP", "/opt/rocm/llvm/bin/llvm-objdump")
 
@@ -43,6 +43,7 @@ class Instr:
     dst: tuple[str, ...]
     src: tuple[str, ...]
     target: int | None = None  # branch target address
+    imm: int | None = None     # last operand, when it is a plain integer
 
 
 @dataclasses.dataclass(frozen=True)
@@ -123,7 +124,10 @@ def parse(asm: str) -> list[Instr]:
             src.append("scc")
         if op.startswith(("v_",)):
             src.append("exec")
-        out.append(Instr(addr, op, tuple(dst), tuple(src), target))
+        imm = None
+        if parts and re.fullmatch(r"-?\d+", parts[-1]):
+            imm = int(parts[-1])
+        out.append(Instr(addr, op, tuple(dst), tuple(src), target, imm))
     return out
 
 
@@ -190,3 +194,55 @@ def loop_model(code_or_asm: bytes | str, lat_valu: float, lat_trans: float, issu
         salu=sum(o.startswith("s_") for o in ops),
         cycles_per_iteration=per,
     )
+
+
+# Three-input integer VALU forms priced like v_add3_u32 when no probe of
+# their own exists.
+_VOP3_INT = ("v_add3_", "v_xad_", "v_lshl_add_", "v_add_lshl_", "v_lshl_or_", "v_and_or_", "v_or3_", "v_xor3_")
+
+
+def issue_slots(code_or_asm: bytes | str, costs: dict[str, float]) -> tuple[float, dict[str, int]]:
+    """FMA-equivalent issue slots of one iteration of the hot loop: each
+    vector instruction weighted by its measured cost relative to
+    v_fma_f32 (`costs`, keyed by mnemonic without encoding suffix, e.g.
+    "v_alignbit_b32", "v_exp_f32"); transcendentals without a probe cost
+    what v_exp_f32 does, three-input integer forms what v_add3_u32 does,
+    every other vector instruction 1. Scalar instructions are not counted
+    (they issue beside vector ones from other wavefronts). Returns the
+    slots and the instruction histogram, both per source iteration (a
+    machine loop unrolled k times is divided by k)."""
+    asm = code_or_asm if isinstance(code_or_asm, str) else disassemble(code_or_asm)
+    body = loop_body(parse(asm))
+    hist: dict[str, int] = {}
+    slots = 0.0
+    for ins in body:
+        if not ins.op.startswith("v_"):
+            continue
+        hist[ins.op] = hist.get(ins.op, 0) + 1
+        base = re.sub(r"_e(32|64)$", "", ins.op)
+        if base in costs:
+            slots += costs[base]
+        elif ins.op.startswith(TRANSCENDENTAL):
+            slots += costs.get("v_exp_f32", 1.0)
+        elif ins.op.startswith(_VOP3_INT):
+            slots += costs.get("v_add3_u32", 1.0)
+        else:
+            slots += 1.0
+    unroll = unroll_factor(body)
+    return slots / unroll, {k: v / unroll for k, v in hist.items()}
+
+
+_IND = re.compile(r"^\s*(s_add_i32|s_sub_i32|s_add_u32|s_sub_u32)\s+(s\d+), (s\d+), (-?\d+)\s*//")
+
+
+def unroll_factor(body: list[Instr], asm_lines: list[str] | None = None) -> int:
+    """How many source iterations one pass of the machine loop covers: the
+    step of its scalar induction update (`s_add_i32 sN, sN, -4` after
+    four-fold unrolling) when that register is also compared in the loop,
+    else 1."""
+    compared = {r for ins in body if ins.op.startswith(("s_cmp", "s_cmpk")) for r in ins.src}
+    for ins in body:
+        if ins.op in ("s_add_i32", "s_sub_i32", "s_add_u32", "s_sub_u32") and ins.dst and ins.dst[0] in compared \
+                and ins.imm is not None and ins.dst[0] in ins.src:
+            return max(1, abs(ins.imm))
+    return 1

@@ -66,3 +66,23 @@ def test_bs3_fast_loop_has_one_exp_and_no_branches_inside():
     m = isa.loop_model(code, 4.0, 12.0, 1.0)
     assert 50 < m.valu < 120
     assert m.cycles_per_iteration > m.instructions  # latency, not issue, sets it
+
+
+@pytest.mark.skipif(not os.path.exists(isa.OBJDUMP), reason="ROCm llvm-objdump absent")
+def test_issue_slots_divide_by_the_unroll_factor():
+    from palladium_amd import runtime as rt
+    from palladium_amd.emit import emit_hip
+    from palladium_amd.trace import trace
+    from palladium_amd.workloads import lv_inputs, lv_rk4_call
+
+    spec = trace(lv_rk4_call(4096, 0.005, 4000, track_max=True)._staged, *lv_inputs(8, 1))
+    code = rt.compile_code_object(emit_hip(spec, math_mode="fast"), spec.name, "fast")
+    body = isa.loop_body(isa.parse(isa.disassemble(code)))
+    k = isa.unroll_factor(body)
+    slots, hist = isa.issue_slots(code, {})
+    # one RK4 step of the 58 staged float ops is ~28 VALU instructions after
+    # contraction and factoring, however many steps the machine loop holds
+    assert 24 <= slots <= 34
+    assert sum(b.op.startswith("v_") for b in body) == pytest.approx(slots * k)
+    costs = {"v_fma_f32": 1.0, "v_mul_f32": 2.0}
+    assert isa.issue_slots(code, costs)[0] == pytest.approx(slots + hist.get("v_mul_f32_e32", 0))
