@@ -212,6 +212,25 @@ def test_bs3_against_float64_restatement():
     np.testing.assert_allclose(acc, ACC, rtol=0.05, atol=5)
 
 
+def test_bs3_stiff_against_float64_restatement():
+    """The stiff end of config 2 (mu in [50, 100], where one trajectory needs
+    over 2,000 attempts): final states within 2e-5 relative of float64 and
+    accepted counts within 3 % / 3. Rejections sit near err = 1, where float32
+    and float64 decide differently, so they are only bounded."""
+    x0, v0, mu = bs3_inputs(4096, seed=11)
+    sel = np.where(mu >= 50)[0][:12]
+    x0, v0, mu = x0[sel], v0[sel], mu[sel]
+    assert mu.min() >= 50 and mu.max() > 85
+    t, x, v, acc, rej = oracle.bs3_vdp(x0, v0, mu, BS3_CFG)
+    T, X, V, ACC, REJ = _bs3_f64(x0, v0, mu, BS3_CFG)
+    np.testing.assert_array_equal(t, np.float32(BS3_CFG.t1))
+    np.testing.assert_allclose(x, X, rtol=2e-5)
+    np.testing.assert_allclose(v, V, rtol=5e-5, atol=2e-7)
+    np.testing.assert_allclose(acc, ACC, rtol=0.03, atol=3)
+    assert acc.max() > 1500
+    assert np.all(rej <= 4 * REJ + 25)
+
+
 def test_bs3_counts_respond_to_tolerance_and_stiffness():
     x0, v0, mu = bs3_inputs(256, seed=12)
     loose = oracle.bs3_vdp(x0, v0, mu, BS3Config(rtol=1e-3, atol=1e-6))
