@@ -55,7 +55,7 @@ def test_invalid_math_mode_rejected():
         rt.compile_code_object('extern "C" __global__ void k() {}', "k", 7)
 
 
-def test_packed_fp32_forms_absent_from_code_objects():
+def test_packed_fp32_forms_absent_from_code_objects(tmp_path):
     from palladium_amd.workloads import lv_inputs, lv_rk4_call
 
     call = lv_rk4_call(1024, 0.01, 8)
@@ -67,12 +67,9 @@ def test_packed_fp32_forms_absent_from_code_objects():
     objdump = Path("/opt/rocm/llvm/bin/llvm-objdump")
     if not objdump.exists():
         pytest.skip("llvm-objdump not available")
-    p = ROOT / "_work_test_codeobj.co"
-    try:
-        p.write_bytes(code)
-        asm = subprocess.run([str(objdump), "-d", "--mcpu=gfx950", str(p)], capture_output=True, text=True, check=True).stdout
-    finally:
-        p.unlink(missing_ok=True)
+    p = tmp_path / "lv_rk4.co"
+    p.write_bytes(code)
+    asm = subprocess.run([str(objdump), "-d", "--mcpu=gfx950", str(p)], capture_output=True, text=True, check=True).stdout
     assert "v_fma" in asm
     assert "v_pk_" not in asm
 
