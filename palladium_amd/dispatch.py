@@ -65,15 +65,15 @@ class PendingResult:
     ----------
     event : runtime.Event
         Recorded after the launch on the kernel's stream.
-    out_bufs : list of runtime.Buffer
-        This launch's device outputs. For `launch()` they belong to one of
-        the kernel's IN_FLIGHT buffer sets and are reused by a later launch;
-        `wait()` returns host copies that stay valid.
     stream : runtime.Stream
+
+    The device outputs are private: they belong to one of the kernel's
+    IN_FLIGHT buffer sets, which a later launch overwrites. `wait()`
+    returns host copies that stay valid.
     """
 
     event: rt.Event
-    out_bufs: list[rt.Buffer]
+    _out_bufs: list[rt.Buffer]
     stream: Any
     # Host arrays an asynchronous upload may still be reading.
     host_inputs: tuple = dataclasses.field(default=(), repr=False)
@@ -94,10 +94,10 @@ class PendingResult:
                 self.event.synchronize()
                 self.host_inputs = ()
                 if self.staged is not None:
-                    self._results = tuple(np.array(p.view(b.shape, b.dtype)) for p, b in zip(self.staged, self.out_bufs))
+                    self._results = tuple(np.array(p.view(b.shape, b.dtype)) for p, b in zip(self.staged, self._out_bufs))
                     self.staged = None
                 else:
-                    self._results = tuple(b.to_numpy(self.stream) for b in self.out_bufs)
+                    self._results = tuple(b.to_numpy(self.stream) for b in self._out_bufs)
             return self._results
 
     def wait(self) -> np.ndarray | tuple[np.ndarray, ...]:
@@ -208,13 +208,6 @@ class BoundKernel:
     def __call__(self, *arrays: np.ndarray) -> np.ndarray | tuple[np.ndarray, ...]:
         """Launch over the grid and return the outputs (NumPy)."""
         return self.launch(*arrays).wait()
-
-    def _dispatch(self, in_bufs: list[rt.Buffer], out_bufs: list[rt.Buffer]) -> PendingResult:
-        geo = self._geo()
-        ptrs = [b.ptr for b in in_bufs] + [b.ptr for b in out_bufs]
-        self.kernel.launch_ptrs(geo.blocks, geo.block, ptrs, self.stream)
-        ev = rt.Event().record(self.stream)
-        return PendingResult(ev, out_bufs, self.stream)
 
     def pinned(self, *arrays: np.ndarray) -> Callable[[], np.ndarray | tuple[np.ndarray, ...]]:
         """Upload once; return a zero-argument callable that re-dispatches

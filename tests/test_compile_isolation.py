@@ -54,3 +54,55 @@ def test_a_compile_past_the_deadline_is_stopped(monkeypatch):
         compile_worker.compile_isolated(OK_SRC.replace("1.0f", "3.0f"), "k", 0)
     monkeypatch.delenv("PALLADIUM_COMPILE_TIMEOUT")
     assert compile_worker.compile_isolated(OK_SRC, "k", 0)[:4] == b"\x7fELF"
+
+
+def test_a_noisy_child_neither_stalls_nor_corrupts_replies(monkeypatch):
+    """200 KB on stderr (more than a pipe holds) and stray bytes written to
+    fd 1 before each reply: the compile still succeeds."""
+    monkeypatch.setenv("PALLADIUM_COMPILE_WORKER_TEST_NOISE", "200000")
+    w = compile_worker._Worker()
+    try:
+        assert w.compile(OK_SRC, "k", 0, "gfx950") == rt.compile_code_object(OK_SRC, "k", 0)
+        assert w.compile(OK_SRC, "k", 2, "gfx950")[:4] == b"\x7fELF"
+    finally:
+        w._discard(kill=True)
+
+
+@pytest.mark.parametrize("value", ["abc", "0", "-3", "nan", "inf"])
+def test_bad_timeout_values_are_compile_errors(monkeypatch, value):
+    monkeypatch.setenv("PALLADIUM_COMPILE_TIMEOUT", value)
+    with pytest.raises(CompileError, match="PALLADIUM_COMPILE_TIMEOUT"):
+        compile_worker.compile_isolated(OK_SRC, "k", 0)
+
+
+def test_partial_and_malformed_replies(tmp_path):
+    import os
+    import struct
+    import time
+
+    r, w = os.pipe()
+    try:
+        os.write(w, struct.pack(">I", 40) + b'{"ok": tr')  # a header cut off mid-way
+        with pytest.raises(TimeoutError):
+            compile_worker._recv_by(r, time.monotonic() + 0.2)
+    finally:
+        os.close(r)
+        os.close(w)
+    r, w = os.pipe()
+    try:
+        os.write(w, struct.pack(">I", 5) + b"nope!")
+        with pytest.raises(compile_worker._ReplyError):
+            compile_worker._recv_by(r, time.monotonic() + 1.0)
+        os.write(w, struct.pack(">I", 1 << 30))
+        with pytest.raises(compile_worker._ReplyError):
+            compile_worker._recv_by(r, time.monotonic() + 1.0)
+    finally:
+        os.close(r)
+        os.close(w)
+    r, w = os.pipe()
+    os.close(w)
+    try:
+        with pytest.raises(compile_worker._ReplyError):
+            compile_worker._recv_by(r, time.monotonic() + 1.0)
+    finally:
+        os.close(r)
