@@ -44,7 +44,7 @@ import numpy as np
 
 from palladium_amd.ir import ClosedJaxpr, Jaxpr, JaxprEqn, Literal, ShapedArray, Var, primitive
 
-__all__ = ["factor_common_products", "fast_rewrites", "power_laws_to_exp2"]
+__all__ = ["drop_redundant_clamps", "factor_common_products", "fast_rewrites", "power_laws_to_exp2"]
 
 
 def _same(a: Any, b: Any) -> bool:
@@ -66,7 +66,71 @@ def _rewrite_sub(v: Any, fn: Any = None) -> Any:
 
 def fast_rewrites(jaxpr: Jaxpr) -> Jaxpr:
     """Every FAST-only rewrite, in order."""
-    return factor_common_products(power_laws_to_exp2(jaxpr))
+    return factor_common_products(power_laws_to_exp2(drop_redundant_clamps(jaxpr)))
+
+
+def _lower_bound(v: Any, producer: dict) -> float | None:
+    """A float32 lower bound of `v` that holds bit for bit, from the ops
+    that made it: JAX's uniform construction (bits >> 9 | 0x3F800000,
+    bitcast: [1, 2)), then subtraction, addition of literals and
+    multiplication by a positive literal (round-to-nearest is monotonic,
+    so applying the op to the bound bounds the result)."""
+    e = producer.get(v)
+    if e is None:
+        return None
+    name = e.primitive.name
+    if name == "bitcast_convert_type" and np.dtype(v.aval.dtype) == np.float32:
+        o = producer.get(e.invars[0])
+        if o is not None and o.primitive.name == "or":
+            a, b = o.invars
+            if isinstance(a, Literal):
+                a, b = b, a
+            sh = producer.get(a)
+            if (isinstance(b, Literal) and int(b.val) == 0x3F800000 and sh is not None
+                    and sh.primitive.name == "shift_right_logical" and isinstance(sh.invars[1], Literal)
+                    and int(sh.invars[1].val) >= 9):
+                return 1.0
+        return None
+    if name in ("sub", "add", "mul") and isinstance(e.invars[1], Literal) and isinstance(e.invars[0], Var):
+        lb = _lower_bound(e.invars[0], producer)
+        c = _f32_literal(e.invars[1])
+        if lb is None or c is None:
+            return None
+        with np.errstate(all="ignore"):
+            if name == "sub":
+                return float(np.float32(lb) - np.float32(c))
+            if name == "add":
+                return float(np.float32(lb) + np.float32(c))
+            if c > 0:
+                return float(np.float32(lb) * np.float32(c))
+    return None
+
+
+def drop_redundant_clamps(jaxpr: Jaxpr) -> Jaxpr:
+    """`max(c, x)` with x provably >= c is x: the clamp `jax.random.uniform`
+    stages after mapping random bits onto [minval, maxval) can never act,
+    and the compiler cannot see it from the bit manipulation."""
+    producer = {ov: e for e in jaxpr.eqns for ov in e.outvars}
+    subst: dict[Any, Any] = {}
+    new_eqns: list[JaxprEqn] = []
+    for e in jaxpr.eqns:
+        params = {k: _rewrite_sub(v, drop_redundant_clamps) for k, v in e.params.items()}
+        invars = [subst.get(a, a) if isinstance(a, Var) else a for a in e.invars]
+        e = JaxprEqn(invars, e.outvars, e.primitive, params)
+        if e.primitive.name == "max" and len(e.outvars) == 1:
+            a, b = e.invars
+            if isinstance(a, Var) and isinstance(b, Literal):
+                a, b = b, a
+            c = _f32_literal(a)
+            if (c is not None and isinstance(b, Var) and np.dtype(b.aval.dtype) == np.float32
+                    and tuple(b.aval.shape) == tuple(e.outvars[0].aval.shape)):
+                lb = _lower_bound(b, producer)
+                if lb is not None and lb >= c:
+                    subst[e.outvars[0]] = b
+                    continue
+        new_eqns.append(e)
+    outvars = [subst.get(o, o) if isinstance(o, Var) else o for o in jaxpr.outvars]
+    return Jaxpr(jaxpr.constvars, jaxpr.invars, outvars, new_eqns)
 
 
 def _use_counts(jaxpr: Jaxpr) -> dict[Any, int]:

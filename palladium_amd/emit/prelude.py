@@ -38,13 +38,16 @@ __device__ __forceinline__ void ph_threefry2x32(unsigned int k0, unsigned int k1
     const unsigned int k2 = k0 ^ k1 ^ 0x1BD11BDAu;
     unsigned int x0 = c0 + k0;
     unsigned int x1 = c1 + k1;
+#define PH_TF_ROUND(r) x0 += x1; x1 = ph_rotl32(x1, r); x1 ^= x0;
+    PH_TF_ROUND(13)
     /* Optimisation barrier (an empty asm that emits no instruction): without
        it LLVM re-associates each key injection into the following rounds'
        adds and keeps injected and un-injected copies of the state live,
-       about 30% more VALU work per block (fold_in chains twice that). */
+       about 30% more VALU work per block (fold_in chains twice that). After
+       the first round rather than before it, so a counter word that is
+       uniform (a scalar) needs no copy into a vector register first. */
     asm volatile("" : "+v"(x0), "+v"(x1));
-#define PH_TF_ROUND(r) x0 += x1; x1 = ph_rotl32(x1, r); x1 ^= x0;
-    PH_TF_ROUND(13) PH_TF_ROUND(15) PH_TF_ROUND(26) PH_TF_ROUND(6)
+    PH_TF_ROUND(15) PH_TF_ROUND(26) PH_TF_ROUND(6)
     x0 += k1; x1 += k2 + 1u;
     PH_TF_ROUND(17) PH_TF_ROUND(29) PH_TF_ROUND(16) PH_TF_ROUND(24)
     x0 += k2; x1 += k0 + 2u;

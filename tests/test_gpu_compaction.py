@@ -2,6 +2,8 @@
 instance runs the same operations as without compaction, so results are
 bit-identical to the uncompacted kernel, the interpreter and the oracle."""
 
+import os
+
 import numpy as np
 import pytest
 
@@ -80,3 +82,48 @@ def test_bs3_compacted_equals_uncompacted(monkeypatch, mode):
         want = oracle.bs3_vdp(*args, BS3_CFG)
         for a, w in zip(got, want):
             np.testing.assert_array_equal(a, w)
+
+
+def _fuzz_kernel(seed):
+    """A data-dependent while loop over random float/int carries: each lane
+    runs until its own accumulator passes a threshold read from its input,
+    so trip counts spread from 0 to a few hundred."""
+    from test_gpu_emitter_fuzz import _expr, _tame
+
+    def kernel(x_ref, y_ref, o_ref, p_ref):
+        x, y = x_ref[...], y_ref[...]
+        lim = jnp.abs(y) * 40.0 + 1.0
+
+        def cond(c):
+            acc, k, a, b = c
+            return jnp.logical_and(acc < lim, k < 400)
+
+        def body(c):
+            acc, k, a, b = c
+            r = np.random.default_rng(seed)
+            na = _tame(_expr(r, [a, b, x], 3), np.dtype(np.float32))
+            nb = _tame(_expr(r, [b, na, y], 2), np.dtype(np.float32))
+            step = jnp.abs(na) * 0.25 + 0.05
+            return acc + step, k + 1 + (k % 3), na, nb
+
+        acc, k, a, b = lax.while_loop(cond, body, (jnp.zeros_like(x), jnp.zeros(x.shape, jnp.int32), x, y))
+        o_ref[...] = a + b * 0.5
+        p_ref[...] = acc + k.astype(jnp.float32)
+
+    return kernel
+
+
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+def test_random_compacted_loops_bit_exact_vs_interpreter(seed):
+    n = 2048
+    rng = np.random.default_rng(700 + seed)
+    x = rng.uniform(-3, 3, n).astype(np.float32)
+    y = rng.uniform(-3, 3, n).astype(np.float32)
+    spec = pl.BlockSpec((1,), lambda i: (i,))
+    call = pa.hip_call(_fuzz_kernel(seed), grid=(n,), in_specs=[spec, spec], out_specs=(spec, spec),
+                       out_shape=(pl.ShapeDtypeStruct((n,), np.float32),) * 2, math_mode="safe")
+    assert "__syncthreads" in call.bound(x, y).hip_source
+    got = call(x, y)
+    want = call.interpret(x, y)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)

@@ -242,3 +242,28 @@ def test_power_law_rewrite_leaves_integer_exponents_and_shared_values():
     assert _count(opt.jaxpr, "exp2") == 1
     for g, w in zip(interpret_spec(opt, x), interpret_spec(spec, x)):
         np.testing.assert_allclose(g, w, rtol=5e-6)
+
+
+# ---------------------------------------------------------------------------
+# redundant clamps: jax.random.uniform's max(minval, .) after the bit trick
+
+from palladium_amd.emit.optimize import drop_redundant_clamps  # noqa: E402
+from palladium_amd.frontend import random  # noqa: E402
+
+
+@pytest.mark.parametrize("lo,hi", [(0.0, 1.0), (-3.0, 5.0), (1e-7, 2.0), (2.5, 2.5000002)])
+def test_uniform_clamp_is_dropped_and_results_unchanged(lo, hi):
+    def kernel(b_ref, o_ref, p_ref):
+        b = b_ref[...]
+        o_ref[...] = random.bits_to_uniform(b, lo, hi)
+        p_ref[...] = jnp.maximum(random.bits_to_uniform(b, lo, hi), hi)  # acts on every value: kept
+
+    edge = np.array([0, 1, 511, 512, 0x7FFFFFFF, 0x80000000, 0xFFFFFE00, 0xFFFFFFFF], np.uint32)
+    b = np.concatenate([edge, np.random.default_rng(1).integers(0, 2**32, 4088, dtype=np.uint64).astype(np.uint32)])
+    call = pl.pallas_call(kernel, out_shape=(pl.ShapeDtypeStruct((b.size,), np.float32),) * 2)
+    spec = trace(call, b)
+    opt = dataclasses.replace(spec, jaxpr=drop_redundant_clamps(spec.jaxpr))
+    assert _count(spec.jaxpr, "max") == 3
+    assert _count(opt.jaxpr, "max") == 1  # both uniforms' clamps go, the one that can act stays
+    for g, w in zip(interpret_spec(opt, b), interpret_spec(spec, b)):
+        np.testing.assert_array_equal(g, w)
