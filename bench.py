@@ -713,7 +713,8 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     # The latency floor: the slowest lane's attempts run strictly one after
     # another, each no faster than one wavefront's in-order chain through
     # this build's loop body.
-    lb = bs3_latency_bound(call, host, valu_latencies(), int(attempts.max()), avg)
+    lat = valu_latencies()
+    lb = bs3_latency_bound(call, host, lat, int(attempts.max()), avg)
     res["roofline"]["latency_frac"] = lb["latency_frac"]
     res["roofline"]["latency_bound"] = lb
     # SAFE: the mode whose accepted/rejected counts equal the oracle's exactly
@@ -726,6 +727,10 @@ def bench_bs3(steps: int, warmup: int, cpu: bool) -> dict:
     srej = safe_outs[4].to_numpy().astype(np.int64)
     res["safe"] = {"ms_per_step": sms, "attempts_per_s": float((sacc + srej).sum()) / (sms / 1e3),
                    "accepted": int(sacc.sum()), "rejected": int(srej.sum())}
+    slb = bs3_latency_bound(bs3_vdp_call(cfg.n, math_mode="safe", name="bs3_vdp_safe"), host, lat,
+                            int((sacc + srej).max()), sms, mode="safe")
+    res["safe"]["latency_frac"] = slb["latency_frac"]
+    res["safe"]["latency_bound"] = {k: v for k, v in slb.items() if k != "latencies_ns"}
     if cpu:
         import oracle
 
@@ -1000,29 +1005,34 @@ def bench_valu_rates(steps: int, warmup: int, cpu: bool) -> dict:
 
 
 _LAT_OPS = {
-    "v_fma_f32": ("v_fma_f32 %0, %0, %1, %2", ': "v"(b), "v"(c)'),
-    "v_exp_f32": ("v_exp_f32 %0, %0", ""),
-    "v_log_f32": ("v_log_f32 %0, %0", ""),
-    "v_rcp_f32": ("v_rcp_f32 %0, %0", ""),
+    # mnemonic: (asm, extra operands, C type)
+    "v_fma_f32": ("v_fma_f32 %0, %0, %1, %2", ': "v"(b), "v"(c)', "float"),
+    "v_exp_f32": ("v_exp_f32 %0, %0", "", "float"),
+    "v_log_f32": ("v_log_f32 %0, %0", "", "float"),
+    "v_rcp_f32": ("v_rcp_f32 %0, %0", "", "float"),
+    "v_add_f32_e32": ("v_add_f32_e32 %0, %0, %1", ': "v"(b)', "float"),
+    "v_fmac_f32_e32": ("v_fmac_f32_e32 %0, %1, %2", ': "v"(b), "v"(c)', "float"),
+    "v_fma_f64": ("v_fma_f64 %0, %0, %1, %2", ': "v"(b), "v"(c)', "double"),
+    "v_fmac_f64_e32": ("v_fmac_f64_e32 %0, %1, %2", ': "v"(b), "v"(c)', "double"),
 }
 _LAT_UNROLL = 32
 _LAT_ITERS = 256
 
 
 def _latency_probe_source(op: str, chains: int) -> str:
-    text, operands = _LAT_OPS[op]
+    text, operands, ct = _LAT_OPS[op]
     body = "\n".join(f'        asm volatile("{text}" : "+v"(a{k % chains}) {operands});'
                      for k in range(_LAT_UNROLL))
-    init = "\n".join(f"    float a{i} = (float)(threadIdx.x + {i + 1});" for i in range(chains))
+    init = "\n".join(f"    {ct} a{i} = ({ct})(threadIdx.x + {i + 1});" for i in range(chains))
     total = " + ".join(f"a{i}" for i in range(chains))
     return f"""
 extern "C" __global__ void __launch_bounds__(64) probe(const float* __restrict__ in, float* __restrict__ out) {{
-    float b = in[0], c = in[1];
+    {ct} b = in[0], c = in[1];
 {init}
     for (int it = 0; it < {_LAT_ITERS}; ++it) {{
 {body}
     }}
-    out[blockIdx.x * 64 + threadIdx.x] = {total};
+    out[blockIdx.x * 64 + threadIdx.x] = (float)({total});
 }}
 """
 
@@ -1056,10 +1066,15 @@ def valu_latencies() -> dict:
     trans = {op: ns_per_instr(op, 1) for op in ("v_exp_f32", "v_log_f32", "v_rcp_f32")}
     out["transcendental_dependent_ns"] = float(np.mean(list(trans.values())))
     out["per_op_dependent_ns"] = trans
+    # Lone-wavefront issue interval by encoding: 4-byte VOP2 forms against
+    # the 8-byte VOP3 v_fma_f32 above, and double precision.
+    out["issue_ns_by_op"] = {op: ns_per_instr(op, 8) for op in ("v_add_f32_e32", "v_fmac_f32_e32", "v_fma_f64",
+                                                              "v_fmac_f64_e32")}
+    out["per_op_dependent_ns"].update({op: ns_per_instr(op, 1) for op in ("v_add_f32_e32", "v_fma_f64")})
     return out
 
 
-def bs3_latency_bound(call, host, lat: dict, max_attempts: int, kernel_ms: float) -> dict:
+def bs3_latency_bound(call, host, lat: dict, max_attempts: int, kernel_ms: float, mode: str = "fast") -> dict:
     """The latency floor of the adaptive loop: the slowest lane runs
     `max_attempts` attempts back to back, and its wavefront can run one no
     faster than the in-order chain model of this build's own loop body
@@ -1068,7 +1083,7 @@ def bs3_latency_bound(call, host, lat: dict, max_attempts: int, kernel_ms: float
     from palladium_amd import runtime as rt
 
     bound = call.bound(*host)
-    code = rt.compile_code_object(bound.hip_source, bound.spec.name, "fast")
+    code = rt.compile_code_object(bound.hip_source, bound.spec.name, mode)
     m = isa.loop_model(code, lat["fma_dependent_ns"], lat["transcendental_dependent_ns"], lat["issue_ns"])
     floor_ms = max_attempts * m.cycles_per_iteration / 1e6
     return {"ns_per_attempt_chain_model": m.cycles_per_iteration, "loop_instructions": m.instructions,
