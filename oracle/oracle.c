@@ -165,48 +165,45 @@ void oracle_gbm(long n_paths, long first_path, long n_steps, uint32_t k0, uint32
 
 /* ------------------------------------------------------------------------
  * Deterministic pow, the same sequence as the SAFE-mode device ph_pow
- * (palladium_amd/emit/prelude.py): double-precision ln via the atanh series
- * and exp via k ln2 + r reduction and a degree-13 Taylor polynomial, all in
- * IEEE double with explicit fma. Pinned against libm pow in tests.
+ * (palladium_amd/emit/prelude.py): double-precision log2 via the atanh
+ * series (coefficients carrying 2/ln 2) and 2^z via z = k + r reduction and a
+ * degree-10 polynomial in r, all in IEEE double with explicit fma. Pinned
+ * against libm pow in tests (correctly rounded on every sampled argument).
  * ---------------------------------------------------------------------- */
-static double ph_ln_pos(double x) {
+static double ph_log2_pos(double x) {
   int e;
   double m = frexp(x, &e);
   if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
   double t = (m - 1.0) / (m + 1.0);
   double t2 = t * t;
-  /* sum_{k=0..7} t2^k / (2k+1) by Estrin's scheme. |t| <= 0.1716, so the
-     first omitted term is below 1.3e-13 of the sum: ample for a result
-     rounded to float. */
-  double q0 = fma(1.0 / 3.0, t2, 1.0), q1 = fma(1.0 / 7.0, t2, 1.0 / 5.0);
-  double q2 = fma(1.0 / 11.0, t2, 1.0 / 9.0), q3 = fma(1.0 / 15.0, t2, 1.0 / 13.0);
-  double u2 = t2 * t2;
-  double r0 = fma(q1, u2, q0), r1 = fma(q3, u2, q2);
-  double p = fma(r1, u2 * u2, r0);
-  double lnm = 2.0 * t * p;
-  const double ln2_hi = 6.93147180369123816490e-01;
-  const double ln2_lo = 1.90821492927058770002e-10;
-  double de = (double)e;
-  return fma(de, ln2_hi, fma(de, ln2_lo, lnm));
+  /* sum_{k=0..7} 2 t2^k / ((2k+1) ln 2) by Horner's rule (one constant per
+     FMA, so no constant needs a register move first). |t| <= 0.1716, so the
+     first omitted term is below 1.3e-13 of the sum. */
+  double p = fma(0.19235933878519512, t2, 0.22195308321368667);
+  p = fma(p, t2, 0.2623081892525388);
+  p = fma(p, t2, 0.3205988979753252);
+  p = fma(p, t2, 0.4121985831111324);
+  p = fma(p, t2, 0.5770780163555853);
+  p = fma(p, t2, 0.9617966939259756);
+  p = fma(p, t2, 2.8853900817779268);
+  return fma(t, p, (double)e);
 }
 
-static double ph_exp_dbl(double z) {
-  const double inv_ln2 = 1.44269504088896338700e+00;
-  const double ln2_hi = 6.93147180369123816490e-01;
-  const double ln2_lo = 1.90821492927058770002e-10;
-  double kd = rint(z * inv_ln2);
-  double r = fma(-kd, ln2_hi, z);
-  r = fma(-kd, ln2_lo, r);
-  /* sum_{k=0..10} r^k / k! by Estrin's scheme. |r| <= ln2 / 2, so the
-     first omitted term is below 2.2e-13: ample for a float result. */
-  double a0 = fma(1.0, r, 1.0), a1 = fma(1.0 / 6.0, r, 0.5);
-  double a2 = fma(1.0 / 120.0, r, 1.0 / 24.0), a3 = fma(1.0 / 5040.0, r, 1.0 / 720.0);
-  double a4 = fma(1.0 / 362880.0, r, 1.0 / 40320.0);
-  double w2 = r * r;
-  double b0 = fma(a1, w2, a0), b1 = fma(a3, w2, a2), b2 = fma(1.0 / 3628800.0, w2, a4);
-  double w4 = w2 * w2;
-  double c0 = fma(b1, w4, b0);
-  double p = fma(b2, w4 * w4, c0);
+static double ph_exp2_dbl(double z) {
+  double kd = rint(z);
+  double r = z - kd; /* exact */
+  /* sum_{n=0..10} (ln 2)^n r^n / n! by Horner's rule. |r ln 2| <= 0.347,
+     so the first omitted term is below 2.2e-13. */
+  double p = fma(7.054911620801123e-09, r, 1.01780860092397e-07);
+  p = fma(p, r, 1.321548679014431e-06);
+  p = fma(p, r, 1.5252733804059841e-05);
+  p = fma(p, r, 0.0001540353039338161);
+  p = fma(p, r, 0.0013333558146428443);
+  p = fma(p, r, 0.009618129107628477);
+  p = fma(p, r, 0.05550410866482158);
+  p = fma(p, r, 0.24022650695910072);
+  p = fma(p, r, 0.6931471805599453);
+  p = fma(p, r, 1.0);
   return ldexp(p, (int)kd);
 }
 
@@ -225,10 +222,10 @@ float oracle_pow(float x, float y) {
   float sign = (signbit(x) && y_odd) ? -1.0f : 1.0f; /* -0 too: pow(-0, 3) = -0 */
   if (ax == 0.0f) return (y < 0.0f) ? sign * INFINITY : sign * 0.0f;
   if (ax == INFINITY) return (y < 0.0f) ? sign * 0.0f : sign * INFINITY;
-  double z = (double)y * ph_ln_pos((double)ax);
-  if (z > 89.0) return sign * INFINITY;
-  if (z < -104.0) return sign * 0.0f;
-  return sign * (float)ph_exp_dbl(z);
+  double z = (double)y * ph_log2_pos((double)ax);
+  if (z > 129.0) return sign * INFINITY;
+  if (z < -151.0) return sign * 0.0f;
+  return sign * (float)ph_exp2_dbl(z);
 }
 
 /* ------------------------------------------------------------------------

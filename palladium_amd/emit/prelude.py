@@ -11,10 +11,11 @@
   adaptive accept/reject decisions reproducible on the CPU. Under RELAXED
   it is the device `powf`; under FAST, 2^(y log2 x) on the hardware base-2
   transcendentals for positive normal bases (powf otherwise).
-  Method: x = m * 2^e with m in [sqrt(1/2), sqrt(2)); ln m = 2 atanh(t),
-  t = (m-1)/(m+1), as an odd series in t; exp by reduction z = k ln2 + r,
-  |r| <= ln2/2, and a degree-13 Taylor polynomial; both carried in double,
-  so the float result is the correctly rounded double value rounded once.
+  Method, in base 2: x = m * 2^e with m in [sqrt(1/2), sqrt(2));
+  log2 m = (2/ln 2) atanh(t), t = (m-1)/(m+1), as an odd series in t;
+  2^z by z = k + r, |r| <= 1/2, and a degree-10 polynomial in r; both
+  carried in double, so the float result is the double value rounded once
+  (correctly rounded on every sampled argument).
 - `ph_exp2`/`ph_log2`: under FAST the hardware base-2 exponential and
   logarithm; libm otherwise.
 - `ph_sin`/`ph_cos`: under FAST the hardware sine/cosine (the reference's
@@ -104,44 +105,55 @@ __device__ __forceinline__ float ph_fmin(float a, float b) { return fminf(a, b);
 __device__ __forceinline__ float ph_fmax(float a, float b) { return fmaxf(a, b); }
 
 #if PH_MATH_MODE == 0
-__device__ __forceinline__ double ph_ln_pos(double x) {
+/* a * b + c, correctly rounded (one v_fma_f64), with the constant c read
+   from scalar registers. Written out because the compiler otherwise keeps
+   polynomial coefficients in vector registers and copies each into the
+   accumulator of a v_fmac_f64 first: two instructions per term. */
+__device__ __forceinline__ double ph_fma_k(double a, double b, double c) {
+    double r;
+    asm("v_fma_f64 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "s"(c));
+    return r;
+}
+
+/* log2 of a positive finite double: x = m 2^e with m in [sqrt(1/2), sqrt(2)),
+   log2 m = (2 / ln 2) atanh(t), t = (m - 1) / (m + 1), as an odd series in t
+   whose coefficients carry the 2 / ln 2; log2 x = e + t P(t^2), one FMA. */
+__device__ __forceinline__ double ph_log2_pos(double x) {
     int e;
     double m = frexp(x, &e);          /* x = m 2^e, m in [0.5, 1) */
     if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
     double t = (m - 1.0) / (m + 1.0);
     double t2 = t * t;
-    /* sum_{k=0..7} t2^k / (2k+1) by Estrin's scheme. |t| <= 0.1716, so the
-       first omitted term is below 1.3e-13 of the sum: ample for a result
-       rounded to float. */
-    double q0 = fma(1.0 / 3.0, t2, 1.0), q1 = fma(1.0 / 7.0, t2, 1.0 / 5.0);
-    double q2 = fma(1.0 / 11.0, t2, 1.0 / 9.0), q3 = fma(1.0 / 15.0, t2, 1.0 / 13.0);
-    double u2 = t2 * t2;
-    double r0 = fma(q1, u2, q0), r1 = fma(q3, u2, q2);
-    double p = fma(r1, u2 * u2, r0);
-    double lnm = 2.0 * t * p;
-    const double ln2_hi = 6.93147180369123816490e-01;
-    const double ln2_lo = 1.90821492927058770002e-10;
-    double de = (double)e;
-    return fma(de, ln2_hi, fma(de, ln2_lo, lnm));
+    /* sum_{k=0..7} 2 t2^k / ((2k+1) ln 2) by Horner's rule (one constant per
+       FMA, so no constant needs a register move first). |t| <= 0.1716, so the
+       first omitted term is below 1.3e-13 of the sum. */
+    double p = ph_fma_k(t2, 0.19235933878519512, 0.22195308321368667);
+    p = ph_fma_k(p, t2, 0.2623081892525388);
+    p = ph_fma_k(p, t2, 0.3205988979753252);
+    p = ph_fma_k(p, t2, 0.4121985831111324);
+    p = ph_fma_k(p, t2, 0.5770780163555853);
+    p = ph_fma_k(p, t2, 0.9617966939259756);
+    p = ph_fma_k(p, t2, 2.8853900817779268);
+    return fma(t, p, (double)e);
 }
 
-__device__ __forceinline__ double ph_exp_dbl(double z) {
-    const double inv_ln2 = 1.44269504088896338700e+00;
-    const double ln2_hi = 6.93147180369123816490e-01;
-    const double ln2_lo = 1.90821492927058770002e-10;
-    double kd = rint(z * inv_ln2);
-    double r = fma(-kd, ln2_hi, z);
-    r = fma(-kd, ln2_lo, r);
-    /* sum_{k=0..10} r^k / k! by Estrin's scheme. |r| <= ln2 / 2, so the
-       first omitted term is below 2.2e-13: ample for a float result. */
-    double a0 = fma(1.0, r, 1.0), a1 = fma(1.0 / 6.0, r, 0.5);
-    double a2 = fma(1.0 / 120.0, r, 1.0 / 24.0), a3 = fma(1.0 / 5040.0, r, 1.0 / 720.0);
-    double a4 = fma(1.0 / 362880.0, r, 1.0 / 40320.0);
-    double w2 = r * r;
-    double b0 = fma(a1, w2, a0), b1 = fma(a3, w2, a2), b2 = fma(1.0 / 3628800.0, w2, a4);
-    double w4 = w2 * w2;
-    double c0 = fma(b1, w4, b0);
-    double p = fma(b2, w4 * w4, c0);
+/* 2^z for |z| <= 151: z = k + r, |r| <= 1/2, 2^r = sum (r ln 2)^n / n!
+   with the ln 2 powers folded into the coefficients. */
+__device__ __forceinline__ double ph_exp2_dbl(double z) {
+    double kd = rint(z);
+    double r = z - kd;                /* exact */
+    /* sum_{n=0..10} (ln 2)^n r^n / n! by Horner's rule. |r ln 2| <= 0.347,
+       so the first omitted term is below 2.2e-13. */
+    double p = ph_fma_k(r, 7.054911620801123e-09, 1.01780860092397e-07);
+    p = ph_fma_k(p, r, 1.321548679014431e-06);
+    p = ph_fma_k(p, r, 1.5252733804059841e-05);
+    p = ph_fma_k(p, r, 0.0001540353039338161);
+    p = ph_fma_k(p, r, 0.0013333558146428443);
+    p = ph_fma_k(p, r, 0.009618129107628477);
+    p = ph_fma_k(p, r, 0.05550410866482158);
+    p = ph_fma_k(p, r, 0.24022650695910072);
+    p = ph_fma_k(p, r, 0.6931471805599453);
+    p = ph_fma_k(p, r, 1.0);
     return ldexp(p, (int)kd);
 }
 
@@ -159,11 +171,11 @@ __device__ __forceinline__ float ph_pow(float x, float y) {
     bool y_odd = y_int && small && (ay - 2.0f * truncf(0.5f * ay) == 1.0f);
     float sign = (__builtin_signbit(x) && y_odd) ? -1.0f : 1.0f; /* -0 too: pow(-0, 3) = -0 */
     bool finite_base = ax > 0.0f && ax < inf;
-    double z = (double)y * ph_ln_pos((double)(finite_base ? ax : 1.0f));
-    double zc = fmin(fmax(z, -104.0), 89.0);
-    float r = sign * (float)ph_exp_dbl(zc);
-    r = (z > 89.0) ? sign * inf : r;
-    r = (z < -104.0) ? sign * 0.0f : r;
+    double z = (double)y * ph_log2_pos((double)(finite_base ? ax : 1.0f));
+    double zc = fmin(fmax(z, -151.0), 129.0);
+    float r = sign * (float)ph_exp2_dbl(zc);
+    r = (z > 129.0) ? sign * inf : r;
+    r = (z < -151.0) ? sign * 0.0f : r;
     r = (ax == inf) ? ((y < 0.0f) ? sign * 0.0f : sign * inf) : r;
     r = (ax == 0.0f) ? ((y < 0.0f) ? sign * inf : sign * 0.0f) : r;
     r = (ay == inf) ? ((ax == 1.0f) ? 1.0f : (((ax > 1.0f) == (y > 0.0f)) ? inf : 0.0f)) : r;
