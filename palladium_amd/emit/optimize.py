@@ -30,9 +30,10 @@ hardware exp2. For a non-integer exponent `pow(x, c)` and `exp2(c*log2 x)`
 agree on every special operand (finite negative x gives NaN, +-0 gives 0
 or inf, +inf gives inf or 0, NaN propagates) except x = -inf, where pow
 gives +inf or +0 and log2 NaN: a base not provably non-negative from its
-producer (max with a non-negative literal, abs, exp, sqrt) has -inf read
-as +inf first, which also keeps `log2(1/y) = -log2(y)` exact at y = -0
-and y = -inf. The results differ by the rounding of the log and exp,
+producer (max with a non-negative operand, abs, exp, sqrt, sums, products
+and quotients of such values, selects among them, and while-loop carries
+that start and stay so) has -inf read as +inf first, which also keeps
+`log2(1/y) = -log2(y)` exact at y = -0 and y = -inf. The results differ by the rounding of the log and exp,
 within FAST's approximate-transcendental contract.
 """
 
@@ -152,8 +153,14 @@ def _f32_literal(v: Any) -> float | None:
     return None
 
 
-def _non_negative(v: Any, producer: dict) -> bool:
-    """Whether `v` is provably >= 0 or NaN (never -inf) from its producer."""
+def _non_negative(v: Any, producer: dict, known: frozenset = frozenset()) -> bool:
+    """Whether `v` is provably >= 0 or NaN (never -inf) from the ops that
+    made it; `known` holds variables already proven so (loop carries)."""
+    if isinstance(v, Literal):
+        x = _f32_literal(v)
+        return x is not None and x >= 0
+    if v in known:
+        return True
     e = producer.get(v)
     if e is None:
         return False
@@ -161,13 +168,37 @@ def _non_negative(v: Any, producer: dict) -> bool:
     if name in ("abs", "exp", "exp2", "sqrt"):
         return True
     if name == "max":
-        return any((_f32_literal(a) or -1.0) >= 0 for a in e.invars)
+        return any(_non_negative(a, producer, known) for a in e.invars)
+    if name in ("add", "mul", "div", "min", "broadcast_in_dim", "reshape", "squeeze"):
+        return all(_non_negative(a, producer, known) for a in e.invars)
+    if name == "select_n":
+        return all(_non_negative(a, producer, known) for a in e.invars[1:])
     return False
 
 
-def power_laws_to_exp2(jaxpr: Jaxpr) -> Jaxpr:
+def _nonneg_carries(e: JaxprEqn, producer: dict, known: frozenset) -> tuple[frozenset, set]:
+    """Body invars of a `while` that are provably >= 0 or NaN on every
+    iteration: operands non-negative outside, and carries whose initial
+    value is and whose update keeps them so (largest fixed point)."""
+    cn, bn = int(e.params["cond_nconsts"]), int(e.params["body_nconsts"])
+    body = getattr(e.params["body_jaxpr"], "jaxpr", e.params["body_jaxpr"])
+    consts, carries = e.invars[cn:cn + bn], e.invars[cn + bn:]
+    bconsts, bcarries = body.invars[:bn], body.invars[bn:]
+    base = {bv for bv, ov in zip(bconsts, consts) if _non_negative(ov, producer, known)}
+    cand = {k for k, iv in enumerate(carries) if _non_negative(iv, producer, known)}
+    bprod = {ov: x for x in body.eqns for ov in x.outvars}
+    while True:
+        assumed = frozenset(base | {bcarries[k] for k in cand})
+        keep = {k for k in cand if _non_negative(body.outvars[k], bprod, assumed)}
+        if keep == cand:
+            return assumed, cand
+        cand = keep
+
+
+def power_laws_to_exp2(jaxpr: Jaxpr, known: frozenset = frozenset()) -> Jaxpr:
     """Rewrite float32 `pow` by non-integer literal exponents, and products
-    of the results, into `exp2` of a linear combination of `log2`s."""
+    of the results, into `exp2` of a linear combination of `log2`s.
+    `known`: variables proven >= 0 or NaN by the caller (while carries)."""
     uses = _use_counts(jaxpr)
     producer = {ov: e for e in jaxpr.eqns for ov in e.outvars}
     exp2_arg: dict[Any, Any] = {}      # outvar of an exp2 made here -> its operand
@@ -182,7 +213,14 @@ def power_laws_to_exp2(jaxpr: Jaxpr) -> Jaxpr:
         return np.dtype(getattr(v.aval, "dtype", np.float64)) == np.float32
 
     for e in jaxpr.eqns:
-        params = {k: _rewrite_sub(v, power_laws_to_exp2) for k, v in e.params.items()}
+        if e.primitive.name == "while":
+            inner, idx = _nonneg_carries(e, producer, known)
+            known = known | {e.outvars[k] for k in idx}   # the loop's results stay so
+            params = dict(e.params)
+            params["body_jaxpr"] = _rewrite_sub(e.params["body_jaxpr"], lambda j: power_laws_to_exp2(j, inner))
+            params["cond_jaxpr"] = _rewrite_sub(e.params["cond_jaxpr"], power_laws_to_exp2)
+        else:
+            params = {k: _rewrite_sub(v, power_laws_to_exp2) for k, v in e.params.items()}
         e = JaxprEqn(e.invars, e.outvars, e.primitive, params)
         name = e.primitive.name
         out = e.outvars[0] if len(e.outvars) == 1 else None
@@ -196,7 +234,7 @@ def power_laws_to_exp2(jaxpr: Jaxpr) -> Jaxpr:
                         and isinstance(src.invars[1], Var)
                         and tuple(src.invars[1].aval.shape) == tuple(out.aval.shape)):
                     x, c = src.invars[1], -c      # log2(1/y) = -log2(y)
-                if not _non_negative(x, producer):
+                if not _non_negative(x, producer, known):
                     # pow(-inf, c) is +inf or +0, log2(-inf) is NaN: read -inf as +inf
                     is_ninf, xs = Var(ShapedArray(out.aval.shape, np.bool_)), Var(aval)
                     new_eqns.append(JaxprEqn([x, lit(-np.inf)], [is_ninf], primitive("eq"), {}))

@@ -7,7 +7,7 @@ import pytest
 
 from palladium_amd.emit import emit_hip
 from palladium_amd.emit.optimize import factor_common_products
-from palladium_amd.frontend import jnp, pl
+from palladium_amd.frontend import jnp, lax, pl
 from palladium_amd.interpret import interpret_spec
 from palladium_amd.trace import trace
 from palladium_amd.workloads import (
@@ -186,7 +186,8 @@ def test_bs3_controller_becomes_one_exp2():
     assert _count(opt.jaxpr, "pow") == 0
     assert _count(opt.jaxpr, "exp2") == 1        # both powers and the safety factor in one exp2
     assert _count(opt.jaxpr, "log2") == 2        # log2(err) on the chain, log2(prev) off it
-    assert _count(opt.jaxpr, "select_n") == _count(spec.jaxpr, "select_n") + 1  # only prev needs the -inf guard
+    # no -inf guard: prev starts at 1 and is only ever replaced by 1/max(err, 1e-9)
+    assert _count(opt.jaxpr, "select_n") == _count(spec.jaxpr, "select_n")
     assert _count(opt.jaxpr, "div") == _count(spec.jaxpr, "div")  # 1/err still feeds the carry
     got = interpret_spec(opt, *args)
     want = interpret_spec(spec, *args)
@@ -267,3 +268,27 @@ def test_uniform_clamp_is_dropped_and_results_unchanged(lo, hi):
     assert _count(opt.jaxpr, "max") == 1  # both uniforms' clamps go, the one that can act stays
     for g, w in zip(interpret_spec(opt, b), interpret_spec(spec, b)):
         np.testing.assert_array_equal(g, w)
+
+
+def test_carry_that_can_turn_negative_keeps_the_guard():
+    def kernel(x_ref, o_ref, p_ref):
+        x = x_ref[...]
+
+        def body(c):
+            k, a, b = c
+            return k + 1, a * 0.5 + 0.25, b - 0.75     # a stays >= 0, b goes negative
+
+        _, a, b = lax.while_loop(lambda c: c[0] < 4, body, (jnp.int32(0), jnp.abs(x), jnp.abs(x)))
+        o_ref[...] = a ** 0.3 + b ** 0.7
+
+    x = np.linspace(-2, 2, 64, dtype=np.float32)
+    call = pl.pallas_call(kernel, grid=(64,), in_specs=[pl.BlockSpec((1,), lambda i: (i,))],
+                          out_specs=(pl.BlockSpec((1,), lambda i: (i,)),) * 2,
+                          out_shape=(pl.ShapeDtypeStruct((64,), np.float32),) * 2)
+    spec = trace(call, x)
+    opt = _pl(spec)
+    assert _count(opt.jaxpr, "pow") == 0
+    # only b's power gets the -inf guard (one eq + one select); a's is proven
+    assert _count(opt.jaxpr, "select_n") == _count(spec.jaxpr, "select_n") + 1
+    for g, w in zip(interpret_spec(opt, x), interpret_spec(spec, x)):
+        np.testing.assert_allclose(g, w, rtol=5e-6)
