@@ -27,9 +27,9 @@ on MI355X: consecutive wavefronts land on the CU's four SIMDs in turn), so
 packing into the lowest wavefronts keeps the four SIMDs evenly loaded.
 
 The control flow around each barrier is uniform over the workgroup (the
-epoch loop stops on a count read from LDS), and every lane of the launch
-exists (the grid is a whole number of workgroups), so every wavefront
-meets every barrier.
+epoch loop stops on a count read from LDS), and no lane returns early (a
+grid that does not fill its last workgroup keeps the extra lanes, which
+hold no instance), so every wavefront meets every barrier.
 """
 
 from __future__ import annotations
@@ -86,13 +86,14 @@ def enabled() -> bool:
 
 def plan_for(spec: Any, jaxpr: Any, lanes: int, block: int | None) -> CompactPlan | None:
     """The loop to compact, or None. Needs: one lane per instance, a 1-D
-    grid that fills whole 1,024-lane workgroups, no explicit workgroup size
-    other than 1,024, and exactly one top-level `while` whose condition
-    and body touch no ref, program id or nested while, with scalar
-    4-byte-or-bool carries and operands."""
+    grid, no explicit workgroup size other than 1,024, and exactly one
+    top-level `while` whose condition and body touch no ref, program id or
+    nested while, with scalar 4-byte-or-bool carries and operands. A grid
+    that does not fill whole workgroups keeps its extra lanes: they read
+    the last instance's data, never enter the loop and store nothing."""
     if not enabled() or lanes != 1 or len(spec.grid) != 1:
         return None
-    if block not in (None, WORKGROUP) or spec.num_programs % WORKGROUP:
+    if block not in (None, WORKGROUP):
         return None
     whiles = [k for k, e in enumerate(jaxpr.eqns) if e.primitive.name == "while"]
     if len(whiles) != 1:
@@ -153,7 +154,8 @@ def emit_compacting_while(env: Any, cursor: Any, eqn: Any, emit_jaxpr: Any, decl
         cursor.emit(f"__shared__ unsigned int {res}[{len(kept)}][{WORKGROUP}];")
     cursor.emit(f"__shared__ int {cnt}[{nw}];")
     slot, own = cursor.fresh("_slot"), cursor.fresh("_own")
-    cursor.emit(f"int {slot} = (int)threadIdx.x;  // the instance this lane holds; -1: none")
+    first = f"(_in ? (int)threadIdx.x : -1)" if getattr(env, "compact_in", None) else "(int)threadIdx.x"
+    cursor.emit(f"int {slot} = {first};  // the instance this lane holds; -1: none")
     wave = cursor.fresh("_wv")
     cursor.emit(f"const int {wave} = (int)(threadIdx.x >> 6);")
     with cursor.block("while (true)"):

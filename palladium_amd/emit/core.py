@@ -494,17 +494,39 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         qual = "const " if k < n_in else ""
         params.append(f"{qual}{ct}* __restrict__ arg{k}_base")
 
+    body = plan.jaxpr if plan else spec.jaxpr
+    if math_mode is not None and math_mode_ordinal(math_mode) == 2:
+        from palladium_amd.emit.optimize import fast_rewrites
+
+        body = fast_rewrites(body)
+    from palladium_amd.emit.compact import plan_for
+
+    cplan = plan_for(spec, body, lanes, block)
+    if (cplan is not None) != (plan is None and geo.block == 1024 and plan_for(spec, spec.jaxpr, lanes, block) is not None):
+        raise EmitError("internal: while-loop compaction disagrees with the launch geometry")
+
     for line in _xcd_remap(geo.blocks):
         cursor.emit(line)
     cursor.emit(f"const unsigned int _flat = _blk * {geo.block}u + threadIdx.x;")
-    cursor.emit(f"if (_flat >= {geo.num_programs * lanes}u) return;")
+    total = geo.num_programs * lanes
+    if cplan is not None and total % geo.block:
+        # A compacting loop needs every lane of the workgroup at its
+        # barriers: lanes past the grid stay, compute on the last instance's
+        # data (clamped index, loads in bounds), never enter the loop and
+        # store nothing.
+        cursor.emit(f"const bool _in = _flat < {total}u;")
+        cursor.emit(f"const unsigned int _flatc = _in ? _flat : {total - 1}u;")
+        env.store_guard = "_in"  # type: ignore[attr-defined]
+        env.compact_in = "_in"  # type: ignore[attr-defined]
+    else:
+        cursor.emit(f"if (_flat >= {total}u) return;")
     if lanes > 1:
         cursor.emit(f"const unsigned int _inst = _flat / {lanes}u;")
         cursor.emit(f"const int _lane = (int)(_flat % {lanes}u);")
     env.lanes = lanes  # type: ignore[attr-defined]
     env.grid = tuple(spec.grid)  # type: ignore[attr-defined]
     pid_vals = []
-    rem = "_inst" if lanes > 1 else "_flat"
+    rem = "_inst" if lanes > 1 else ("_flatc" if getattr(env, "compact_in", None) else "_flat")
     grid = tuple(spec.grid)
     tile = _tile2d(grid, geo.block) if lanes == 1 else None
     if tile is not None:
@@ -550,16 +572,6 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         cursor.emit(f"{ptr} = arg{k}_base + {offset};" if offset != "0" else f"{ptr} = arg{k}_base;")
         ref_vals.append(CVal(f"arg{k}", info.block_shape or (1,), ct, "global", k < n_in))
 
-    body = plan.jaxpr if plan else spec.jaxpr
-    if math_mode is not None and math_mode_ordinal(math_mode) == 2:
-        from palladium_amd.emit.optimize import fast_rewrites
-
-        body = fast_rewrites(body)
-    from palladium_amd.emit.compact import plan_for
-
-    cplan = plan_for(spec, body, lanes, block)
-    if (cplan is not None) != (plan is None and geo.block == 1024 and plan_for(spec, spec.jaxpr, lanes, block) is not None):
-        raise EmitError("internal: while-loop compaction disagrees with the launch geometry")
     env.compact = body.eqns[cplan.index] if cplan is not None else None  # type: ignore[attr-defined]
     emit_jaxpr(env, cursor, body, ref_vals)
 

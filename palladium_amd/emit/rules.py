@@ -313,6 +313,9 @@ def _rule_swap(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
         guard = "_lane == 0"
     elif eqn.params.get("lane_row") and getattr(env, "live", None):
         guard = env.live  # type: ignore[attr-defined]
+    if getattr(env, "store_guard", None):
+        # lanes past the grid of a compacting kernel store nothing
+        guard = env.store_guard if guard is None else f"({guard}) && {env.store_guard}"  # type: ignore[attr-defined]
     if guard:
         cursor.emit(f"if ({guard}) {{")
         cursor.indent += 1

@@ -26,10 +26,26 @@ def test_bs3_loop_is_compacted_in_1024_lane_workgroups():
 
 
 @pytest.mark.parametrize("n", [1000, 1536, 512])
-def test_partial_workgroups_are_not_compacted(n):
+def test_partial_workgroups_keep_their_extra_lanes(n):
+    """A grid that does not fill its last workgroup: no lane returns early
+    (every wavefront must meet the barriers); the extra lanes read the last
+    instance's data, hold no instance and store nothing."""
     spec = _bs3_spec(n)
-    assert launch_geometry(spec).block == 256
-    assert "__syncthreads" not in emit_hip(spec)
+    geo = launch_geometry(spec)
+    assert geo.block == 1024 and geo.blocks == -(-n // 1024)
+    src = emit_hip(spec)
+    assert "return;" not in src
+    assert f"const bool _in = _flat < {n}u;" in src
+    assert f"_in ? _flat : {n - 1}u" in src
+    assert "(_in ? (int)threadIdx.x : -1)" in src
+    # all five output stores are guarded
+    assert src.count("if (_in) {") == 5
+
+
+def test_whole_workgroups_need_no_guard():
+    src = emit_hip(_bs3_spec(2048))
+    body = src[src.index("extern \"C\""):]
+    assert "_in " not in body and "return;" in body
 
 
 def test_explicit_workgroup_size_and_env_switch(monkeypatch):

@@ -45,9 +45,11 @@ def _collatz(n):
                        math_mode="safe")
 
 
-def test_collatz_compacted_matches_interpreter_and_uncompacted(monkeypatch):
-    n = 8192
-    rng = np.random.default_rng(3)
+@pytest.mark.parametrize("n", [8192, 3000, 100])
+def test_collatz_compacted_matches_interpreter_and_uncompacted(monkeypatch, n):
+    """8,192 fills whole workgroups; 3,000 and 100 leave extra lanes in the
+    last one, which must store nothing."""
+    rng = np.random.default_rng(3 + n)
     x = rng.integers(1, 200_000, n).astype(np.int32)
     x[::97] = 1  # lanes that never enter the loop
     f = rng.standard_normal(n).astype(np.float32)

@@ -7,7 +7,7 @@ form where one exists):
 - tests/test_07_preflight.py:108-124 (-inf sentinel running max),
   145-163 (accept/reject inside a loop);
 - tests/test_15_control_flow.py:88-107 (while loop rotating its carries),
-  here also in the lane-compacted form (a grid of 2,048 instances);
+  in the lane-compacted form and the plain predicated one;
 - tests/test_09_indexed_refs.py:91-114 (periodic wraparound indices)."""
 
 import numpy as np
@@ -127,10 +127,11 @@ def test_accept_reject_inside_a_loop(rng):
     assert np.all(got <= 1.0)
 
 
-@pytest.mark.parametrize("n", [128, 2048])
-def test_while_rotating_its_carries(rng, n):
-    """n = 2,048 instances fill whole 1,024-lane workgroups, so the loop is
-    emitted with lane compaction; 128 is the plain predicated loop."""
+@pytest.mark.parametrize("n,threadgroup", [(128, None), (2048, None), (2048, 256)])
+def test_while_rotating_its_carries(rng, n, threadgroup):
+    """Default workgroups emit the loop with lane compaction (at 128
+    instances the last workgroup keeps 896 extra lanes); an explicit
+    256-lane workgroup gives the plain predicated loop."""
     def kernel(a_ref, o_ref):
         def body(c):
             a, b, k = c
@@ -142,11 +143,10 @@ def test_while_rotating_its_carries(rng, n):
 
     s = pl.BlockSpec((1,), lambda i: (i,))
     f = pa.hip_call(kernel, grid=(n,), in_specs=[s], out_specs=s, out_shape=pl.ShapeDtypeStruct((n,), F),
-                    math_mode="safe")
+                    math_mode="safe", threadgroup=threadgroup)
     a = rng.standard_normal(n).astype(F)
-    assert ("__syncthreads" in f.bound(a).hip_source) == (n == 2048)
+    assert ("__syncthreads" in f.bound(a).hip_source) == (threadgroup is None)
     (got,) = _same(f, a)
-    # fib-like: (a, a+1) -> after 5 steps a + b = 13a + 8(a+1)... in float32 order
     x, y = a.copy(), a + F(1.0)
     for _ in range(5):
         x, y = y, x + y
