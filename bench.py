@@ -32,6 +32,8 @@ LV_MEASURED_TRAFFIC_BYTES = int((23467.5 + 11718.75) * 1024)
 GS_MEASURED_TRAFFIC_BYTES = int((131612.4 + 131072.0) * 1024)
 # The same for one 4-step pass of the LDS temporal-blocking Gray-Scott kernel.
 GSF_MEASURED_TRAFFIC_BYTES = int((2 * 66687.3 + 131072.0) * 1024)
+# And for one 6-step pass of the register Gray-Scott kernel (64-row strips).
+GSR_MEASURED_TRAFFIC_BYTES = int((2 * 83003.0 + 131627.1) * 1024)
 
 
 def _cpu_cores() -> int:
@@ -602,39 +604,43 @@ gs_lds(const float* __restrict__ u, const float* __restrict__ v, float* __restri
 
 
 def bench_gs_fused(steps: int, warmup: int, cpu: bool) -> dict:
-    """Config 4 with temporal blocking: 4 steps per pass through HBM
-    (palladium_amd/stencil.py), 500 passes as one HIP graph. The per-step
-    formulation's 16 B/cell-step over this time is an effective rate, not
-    HBM traffic; the pass's own algorithmic traffic is the tile plus its
-    4-cell halo read and the tile written, per 4 steps."""
+    """Config 4 with temporal blocking (palladium_amd/stencil.py): K steps
+    per pass through HBM, all passes as one HIP graph. PALLADIUM_GS_KERNEL
+    picks the kernel: "regs" (default; each lane walks a column in
+    registers, neighbours through DPP) or "lds" (tiles staged in LDS)."""
     from palladium_amd import stencil
     from palladium_amd.workloads import GS_BYTES_PER_CELL_STEP, GS_CFG, gray_scott_initial
 
     cfg = GS_CFG
     u0, v0 = gray_scott_initial(cfg.size)
-    fused = stencil.FusedGrayScott(cfg.size)
+    kind = os.environ.get("PALLADIUM_GS_KERNEL", "regs")
+    make = {"regs": stencil.RegisterGrayScott, "lds": stencil.FusedGrayScott}[kind]
+    fused = make(cfg.size)
     stencil.gray_scott_fused_run(fused, u0, v0, 2 * fused.k)  # compile + warm
     n_steps = int(os.environ.get("PALLADIUM_GS_STEPS", cfg.steps))
     graph = os.environ.get("PALLADIUM_GS_GRAPH", "1") != "0"
     u, v, gpu_s = stencil.gray_scott_fused_run(fused, u0, v0, n_steps, graph=graph)
     cells = cfg.size * cfg.size
     ms = gpu_s * 1e3 / n_steps
-    k, th, tw = fused.k, fused.th, fused.tw
+    k = fused.k
+    passes = len(fused.launches(n_steps))
     pass_bytes = GS_BYTES_PER_CELL_STEP * cells  # each pass reads and writes both fields once
-    hbm = pass_bytes / (ms * k / 1e3)
-    res = _base("Gray-Scott cell-steps/s (4096^2, 2,000 steps, fp32), 4 steps per pass", cells / (ms / 1e3),
+    hbm = pass_bytes * passes / (gpu_s)
+    res = _base("Gray-Scott cell-steps/s (4096^2, 2,000 steps, fp32), temporal blocking", cells / (ms / 1e3),
                 "cell-steps/s", n_steps, 2 * k, ms,
-                {"workload": f"Gray-Scott 4096x4096, {n_steps} steps in {n_steps // k} passes of {k} as one HIP graph, "
-                             f"{th}x{tw} tiles, config 4", "size": cfg.size, "math_mode": "fast",
-                 "steps_per_pass": k, "tile": [th, tw]})
-    res["roofline"] = {"bound": "lds", "achieved": hbm / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                       "frac": hbm / HBM_PEAK, "traffic": GSF_MEASURED_TRAFFIC_BYTES,
-                       "bytes_per_pass_algorithmic": pass_bytes, "avg_pass_ms": ms * k,
+                {"workload": f"Gray-Scott 4096x4096, {n_steps} steps in {passes} passes ({k} steps each) as one HIP "
+                             f"graph, config 4; {fused.describe()}", "size": cfg.size, "math_mode": "fast",
+                 "kernel": kind, "steps_per_pass": k})
+    traffic = {"lds": GSF_MEASURED_TRAFFIC_BYTES, "regs": GSR_MEASURED_TRAFFIC_BYTES}[kind]
+    res["roofline"] = {"bound": "issue", "achieved": hbm / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                       "frac": hbm / HBM_PEAK, "traffic": traffic,
+                       "bytes_per_pass_algorithmic": pass_bytes, "avg_pass_ms": gpu_s * 1e3 / passes,
                        "effective_per_step_GBps": GS_BYTES_PER_CELL_STEP * cells / (ms / 1e3) / 1e9,
                        "note": ("achieved/frac: both fields read and written once per pass (16 B/cell) over the "
-                                "pass time; halo re-reads are served by L2 (traffic 1.009x algorithmic). The pass "
-                                "is bound by LDS traffic and issue, not HBM. effective_per_step_GBps prices each "
-                                "step at the per-step kernel's 16 B/cell, traffic this kernel does not make")}
+                                "pass time. The pass is bound by VALU issue and by how little of its HBM time "
+                                "overlaps its arithmetic, not by HBM bandwidth: alone, its arithmetic takes 50 us "
+                                "and its loads and stores 43 us of a 76 us pass. effective_per_step_GBps prices "
+                                "each step at the per-step kernel's 16 B/cell, traffic this kernel does not make")}
     res["pattern_energy"] = float(np.sum(v, dtype=np.float64))
     if cpu:
         import oracle
@@ -645,7 +651,7 @@ def bench_gs_fused(steps: int, warmup: int, cpu: bool) -> dict:
         dt = time.perf_counter() - t0
         res["cpu_baseline"] = {"value": cells * cs / dt, "unit": "cell-steps/s", "cores": _cpu_cores(),
                                "kind": "port", "sample": f"config-4 grid x first {cs} steps, C oracle, {dt:.2f} s"}
-        su, sv, _ = stencil.gray_scott_fused_run(stencil.FusedGrayScott(cfg.size, math_mode="safe"), u0, v0, cs)
+        su, sv, _ = stencil.gray_scott_fused_run(make(cfg.size, math_mode="safe"), u0, v0, cs)
         res["safe_bit_exact_vs_oracle"] = {"steps": cs, "equal": bool(np.array_equal(su, wu) and np.array_equal(sv, wv))}
     return res
 

@@ -31,7 +31,7 @@ import numpy as np
 from palladium_amd import runtime as rt
 from palladium_amd.emit.core import format_float
 
-__all__ = ["FusedGrayScott", "fused_source", "gray_scott_fused_run"]
+__all__ = ["FusedGrayScott", "RegisterGrayScott", "fused_source", "gray_scott_fused_run", "register_source"]
 
 WORKGROUP = 256
 NUM_XCDS = 8
@@ -157,6 +157,150 @@ def fused_source(n: int, k: int, th: int, tw: int, du: float, dv: float, f: floa
     return "\n".join(lines)
 
 
+WAVE = 64
+# DPP controls for a whole-wave rotation by one lane: after `wave_rol:1`
+# lane l holds what lane l + 1 held (its right-hand neighbour's column),
+# after `wave_ror:1` what lane l - 1 held.
+_DPP_FROM_RIGHT = 0x134
+_DPP_FROM_LEFT = 0x13C
+
+
+def _reg_update(lit: dict, up: tuple, mid: tuple, down: tuple, out: tuple, tag: str) -> list[str]:
+    """One row of the next step from three rows of this one held in this
+    lane's registers (each a (u, v) pair of names); the left and right
+    columns are rotated in from the neighbouring lanes. The op order of
+    `_update`."""
+    lines = []
+    for i, (f, d) in enumerate((("u", "DU"), ("v", "DV"))):
+        c = mid[i]
+        lines += [
+            f"float l{f}{tag} = {down[i]} + {up[i]};",
+            f"l{f}{tag} = l{f}{tag} + ph_from_right({c});",
+            f"l{f}{tag} = l{f}{tag} + ph_from_left({c});",
+            f"l{f}{tag} = l{f}{tag} - 4.0f * {c};",
+        ]
+    uc, vc = mid
+    lines += [
+        f"const float uvv{tag} = ({uc} * {vc}) * {vc};",
+        f"float a{tag} = {lit['DU']} * lu{tag};",
+        f"a{tag} = a{tag} - uvv{tag};",
+        f"a{tag} = a{tag} + {lit['F']} * (1.0f - {uc});",
+        f"float b{tag} = {lit['DV']} * lv{tag};",
+        f"b{tag} = b{tag} + uvv{tag};",
+        f"b{tag} = b{tag} - {lit['FK']} * {vc};",
+        f"const float {out[0]} = {uc} + {lit['DT']} * a{tag};",
+        f"const float {out[1]} = {vc} + {lit['DT']} * b{tag};",
+    ]
+    return lines
+
+
+def register_geometry(n: int, k: int, rows: int) -> tuple[int, int]:
+    """(waves, workgroups) of a register pass: one wave per strip of `rows`
+    rows by 64 - 2K columns (the last strip of each kind may reach past the
+    grid), four waves per workgroup."""
+    waves = -(-n // rows) * -(-n // (WAVE - 2 * k))
+    return waves, -(-waves // (WORKGROUP // WAVE))
+
+
+def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, fk: float, dt: float,
+                    group: int = 8) -> str:
+    """HIP source of a K-step Gray-Scott pass with no LDS: each wave owns a
+    strip of `rows` grid rows by 64 - 2K columns. Lane l walks down column
+    j0 - K + l from row i0 - K to row i0 + rows + K - 1, one input row at a
+    time. For each step t it keeps the last two rows of step t - 1 in
+    registers (the up and down neighbours) and takes the left and right
+    neighbours from the adjacent lanes through DPP wave rotations: input row
+    r yields step-t row r - t, so step K's row r - K leaves the pipeline as
+    row r comes in. Edge lanes and the first rows of each step read values
+    that are not yet (or no longer) valid; each step moves that region in by
+    one lane and one row per side, so after K steps lanes K .. 63 - K and
+    rows K .. K + rows - 1 are exact, and only those are stored. Rows come
+    in `group` at a time, the next group's loads issued before the current
+    group's arithmetic. Row indices wrap around the grid, so every load is
+    in bounds; the last strip of a row (and of a column) may reach past the
+    grid, and its lanes (rows) outside it store nothing."""
+    w = WAVE - 2 * k
+    if k < 1 or w < 1:
+        raise ValueError(f"steps per pass {k} out of range for a {WAVE}-lane wave")
+    if rows < 1:
+        raise ValueError(f"strip height {rows} must be positive")
+    if n * n * 4 >= 1 << 31:
+        raise ValueError(f"grid {n}x{n} exceeds the 2 GiB a buffer descriptor addresses")
+    if rows + 2 * k > n or n < WAVE:
+        raise ValueError(f"grid {n}x{n} too small for {rows}-row strips with a {k}-row halo (and one {WAVE}-lane wave)")
+    h = rows + 2 * k
+    groups = -(-h // group)
+    strips_j = -(-n // w)
+    waves, blocks = register_geometry(n, k, rows)
+    per, rem = divmod(blocks, NUM_XCDS)
+    lit = {name: format_float(v) for name, v in (("DU", du), ("DV", dv), ("F", f), ("FK", fk), ("DT", dt))}
+    lines = [
+        f"// Gray-Scott, {k} steps per pass in registers, {rows}x{w} strips, {n}x{n} periodic grid.",
+        "#define PH_RSRC_WORD3 0x00020000  /* gfx9 buffer descriptor word 3: 32-bit elements, raw */",
+        "#define PH_DROP ((int)0x80000000)  /* an offset past every field: the store is dropped */",
+        "static __device__ __forceinline__ float ph_from_right(float x) {",
+        f"    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), {_DPP_FROM_RIGHT:#x}, 0xf, 0xf, true));",
+        "}",
+        "static __device__ __forceinline__ float ph_from_left(float x) {",
+        f"    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), {_DPP_FROM_LEFT:#x}, 0xf, 0xf, true));",
+        "}",
+        f'extern "C" __global__ void __launch_bounds__({WORKGROUP})',
+        "gray_scott_regs(const float* __restrict__ u_in, const float* __restrict__ v_in,",
+        "                float* __restrict__ u_out, float* __restrict__ v_out)",
+        "{",
+        f"    const unsigned int xcd = blockIdx.x % {NUM_XCDS}u, slot = blockIdx.x / {NUM_XCDS}u;",
+        f"    const unsigned int blk = (xcd < {rem}u) ? xcd * {per + 1}u + slot",
+        f"                                           : {rem * (per + 1)}u + (xcd - {rem}u) * {per}u + slot;",
+        f"    const unsigned int strip = blk * {WORKGROUP // WAVE}u + threadIdx.x / {WAVE}u;",
+        f"    if (strip >= {waves}u) return;  /* whole waves only */",
+        f"    const int lane = (int)(threadIdx.x % {WAVE}u);",
+        f"    const int i0 = (int)(strip / {strips_j}u) * {rows};",
+        f"    const int last = {n} - i0 < {rows} ? {n} - i0 : {rows};  /* rows of this strip inside the grid */",
+        f"    const int j0 = (int)(strip % {strips_j}u) * {w};",
+        f"    int gj = j0 - {k} + lane;",
+        f"    gj = gj < 0 ? gj + {n} : (gj >= {n} ? gj - {n} : gj);",
+        f"    const bool owner = lane >= {k} && lane < {WAVE - k} && j0 + lane - {k} < {n};",
+        "    /* Stores go through buffer descriptors spanning each output field: a",
+        "       lane that must not store gets an offset past the end, which the",
+        "       hardware drops, so no branch separates the stores from the loads",
+        "       (a branch would make the wait for each group's loads drain the",
+        "       previous group's stores). */",
+        f"    const __amdgpu_buffer_rsrc_t u_rs = __builtin_amdgcn_make_buffer_rsrc(u_out, (short)0, {n * n * 4}, PH_RSRC_WORD3);",
+        f"    const __amdgpu_buffer_rsrc_t v_rs = __builtin_amdgcn_make_buffer_rsrc(v_out, (short)0, {n * n * 4}, PH_RSRC_WORD3);",
+        f"    const int top = i0 - {k} + {n};  /* row r of the strip is grid row (top + r) % n */",
+        "    float " + ", ".join(f"pu{t}_{i} = 0.0f, pv{t}_{i} = 0.0f" for t in range(k) for i in (1, 2)) + ";",
+    ]
+    for g in range(group):
+        lines.append(f"    float qu{g}, qv{g};")
+        lines.append(f"    {{ const int gi = (int)((unsigned int)(top + {g}) % {n}u); qu{g} = u_in[gi * {n} + gj]; qv{g} = v_in[gi * {n} + gj]; }}")
+    lines += [f"    for (int r0 = 0; r0 < {groups * group}; r0 += {group}) {{"]
+    # The next group's loads are unconditional (the last iteration reads
+    # wrapped rows it never uses): behind a branch, the wait for this
+    # group's rows would also wait for the first of them.
+    for g in range(group):
+        lines.append(f"        const int gi{g} = (int)((unsigned int)(top + r0 + {group + g}) % {n}u);")
+        lines.append(f"        const float nu{g} = u_in[gi{g} * {n} + gj], nv{g} = v_in[gi{g} * {n} + gj];")
+    for g in range(group):
+        lines.append(f"        {{ /* input row r0 + {g} */")
+        cur = (f"qu{g}", f"qv{g}")
+        for t in range(k):
+            out = (f"yu{g}_{t}", f"yv{g}_{t}")
+            lines += ["            " + x for x in _reg_update(lit, (f"pu{t}_2", f"pv{t}_2"), (f"pu{t}_1", f"pv{t}_1"),
+                                                              cur, out, f"{g}_{t}")]
+            lines.append(f"            pu{t}_2 = pu{t}_1; pv{t}_2 = pv{t}_1; pu{t}_1 = {cur[0]}; pv{t}_1 = {cur[1]};")
+            cur = out
+        lines.append(f"            const int a = r0 + {g} - {2 * k};  /* output row, strip-relative */")
+        lines.append("            const bool keep = owner && a >= 0 && a < last;")
+        lines.append(f"            const int off = keep ? ((i0 + a) * {n} + (j0 + lane - {k})) * 4 : PH_DROP;")
+        lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[0]}), u_rs, off, 0, 0);")
+        lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[1]}), v_rs, off, 0, 0);")
+        lines.append("        }")
+    for g in range(group):
+        lines.append(f"        qu{g} = nu{g}; qv{g} = nv{g};")
+    lines += ["    }", "}", ""]
+    return "\n".join(lines)
+
+
 @dataclasses.dataclass
 class FusedGrayScott:
     """A compiled K-step pass (and, for step counts K does not divide, a
@@ -173,15 +317,17 @@ class FusedGrayScott:
     single_buffer: bool = True
 
     def __post_init__(self) -> None:
-        from palladium_amd.workloads import GS_CFG
-
-        cfg = self.cfg or GS_CFG
-        consts = (float(np.float32(cfg.du)), float(np.float32(cfg.dv)), float(np.float32(cfg.f)),
-                  float(np.float32(cfg.f + cfg.k)), float(np.float32(cfg.dt)))
+        consts = _consts(self.cfg)
         self._src = {kk: fused_source(self.n, kk, self.th, self.tw, *consts, single_buffer=self.single_buffer)
                      for kk in {self.k, 1}}
         self._kernels = {kk: rt.Kernel(src, "gray_scott_fused", self.math_mode) for kk, src in self._src.items()}
         self.blocks = (self.n // self.th) * (self.n // self.tw)
+
+    def blocks_for(self, k: int) -> int:
+        return self.blocks
+
+    def describe(self) -> str:
+        return f"LDS pass: {self.th}x{self.tw} tiles, {'one buffer' if self.single_buffer else 'two buffers'}"
 
     def source(self, k: int | None = None) -> str:
         return self._src[k or self.k]
@@ -190,7 +336,46 @@ class FusedGrayScott:
         return [self.k] * (steps // self.k) + [1] * (steps % self.k)
 
 
-def gray_scott_fused_run(fused: FusedGrayScott, u0: np.ndarray, v0: np.ndarray, steps: int, graph: bool = True):
+def _consts(cfg: Any) -> tuple:
+    from palladium_amd.workloads import GS_CFG
+
+    cfg = cfg or GS_CFG
+    return (float(np.float32(cfg.du)), float(np.float32(cfg.dv)), float(np.float32(cfg.f)),
+            float(np.float32(cfg.f + cfg.k)), float(np.float32(cfg.dt)))
+
+
+@dataclasses.dataclass
+class RegisterGrayScott:
+    """A compiled K-step register pass (`register_source`) and a one-step
+    pass of the same code for step counts K does not divide."""
+
+    n: int
+    k: int = 6
+    rows: int = 64
+    group: int = 4
+    math_mode: Any = "fast"
+    cfg: Any = None
+
+    def __post_init__(self) -> None:
+        consts = _consts(self.cfg)
+        self._src = {kk: register_source(self.n, kk, self.rows, *consts, group=self.group) for kk in {self.k, 1}}
+        self._kernels = {kk: rt.Kernel(src, "gray_scott_regs", self.math_mode) for kk, src in self._src.items()}
+        self._blocks = {kk: register_geometry(self.n, kk, self.rows)[1] for kk in self._src}
+
+    def blocks_for(self, k: int) -> int:
+        return self._blocks[k]
+
+    def describe(self) -> str:
+        return f"register pass: {self.rows}x{WAVE - 2 * self.k} strips, one wave each, rows in groups of {self.group}"
+
+    def source(self, k: int | None = None) -> str:
+        return self._src[k or self.k]
+
+    def launches(self, steps: int) -> list[int]:
+        return [self.k] * (steps // self.k) + [1] * (steps % self.k)
+
+
+def gray_scott_fused_run(fused: FusedGrayScott | RegisterGrayScott, u0: np.ndarray, v0: np.ndarray, steps: int, graph: bool = True):
     """`steps` Gray-Scott steps in passes of `fused.k`, ping-ponging two
     buffer pairs, queued as one batch (one HIP graph when `graph`).
     Returns (u, v, device seconds)."""
@@ -206,7 +391,7 @@ def gray_scott_fused_run(fused: FusedGrayScott, u0: np.ndarray, v0: np.ndarray, 
     src = 0
     for kk in fused.launches(steps):
         dst = 1 - src
-        batch.add(fused._kernels[kk], fused.blocks, WORKGROUP, [b.ptr for b in bufs[src]] + [b.ptr for b in bufs[dst]])
+        batch.add(fused._kernels[kk], fused.blocks_for(kk), WORKGROUP, [b.ptr for b in bufs[src]] + [b.ptr for b in bufs[dst]])
         src = dst
     batch.commit(graph=graph)
     batch.wait()

@@ -88,3 +88,88 @@ def test_bad_tiles_are_refused():
         stencil.fused_source(100, 2, 32, 64, 0.16, 0.08, 0.037, 0.097, 1.0)
     with pytest.raises(ValueError, match="out of range"):
         stencil.fused_source(4096, 9, 16, 64, 0.16, 0.08, 0.037, 0.097, 1.0)
+
+
+def _register_pass(u, v, k, rows, group, cfg):
+    """The register kernel's schedule, lane for lane: a wave's 64 lanes walk
+    down their columns, each step keeping two rows of the step before, the
+    left/right neighbours rotated in across the whole wave (np.roll), the
+    windows starting at zero, row indices wrapping, and only owner lanes
+    and rows K .. K + rows - 1 of step K stored."""
+    du, dv, f, fk, dt = (F(x) for x in (cfg.du, cfg.dv, cfg.f, cfg.f + cfg.k, cfg.dt))
+    n = u.shape[0]
+    w = 64 - 2 * k
+    h = rows + 2 * k
+    total = -(-h // group) * group
+    uo, vo = np.full_like(u, np.nan), np.full_like(v, np.nan)
+    lane = np.arange(64)
+    for i0 in range(0, n, rows):
+        last = min(rows, n - i0)
+        for j0 in range(0, -(-n // w) * w, w):
+            gj = (j0 - k + lane) % n
+            owner = (lane >= k) & (lane < 64 - k) & (j0 + lane - k < n)
+            win = [[np.zeros(64, F) for _ in range(4)] for _ in range(k)]  # pu2, pu1, pv2, pv1
+            for r in range(total):
+                gi = (i0 - k + r) % n
+                cu, cv = u[gi, gj], v[gi, gj]
+                for t in range(k):
+                    pu2, pu1, pv2, pv1 = win[t]
+                    with np.errstate(all="ignore"):
+                        lu = cu + pu2
+                        lu = lu + np.roll(pu1, -1)
+                        lu = lu + np.roll(pu1, 1)
+                        lu = lu - F(4.0) * pu1
+                        lv = cv + pv2
+                        lv = lv + np.roll(pv1, -1)
+                        lv = lv + np.roll(pv1, 1)
+                        lv = lv - F(4.0) * pv1
+                        uvv = (pu1 * pv1) * pv1
+                        a = du * lu
+                        a = a - uvv
+                        a = a + f * (F(1.0) - pu1)
+                        b = dv * lv
+                        b = b + uvv
+                        b = b - fk * pv1
+                        yu, yv = pu1 + dt * a, pv1 + dt * b
+                    win[t] = [pu1, cu, pv1, cv]
+                    cu, cv = yu, yv
+                a_row = r - 2 * k
+                if 0 <= a_row < last:
+                    cols = j0 + lane[owner] - k
+                    assert np.all(np.isnan(uo[i0 + a_row, cols])), "a cell stored twice"
+                    uo[i0 + a_row, cols] = cu[owner]
+                    vo[i0 + a_row, cols] = cv[owner]
+    assert not np.isnan(uo).any() and not np.isnan(vo).any(), "a cell never stored"
+    return uo, vo
+
+
+@pytest.mark.parametrize("n,k,rows,group,steps", [(64, 4, 16, 8, 8), (64, 4, 16, 8, 9), (64, 3, 32, 5, 6),
+                                                   (64, 8, 16, 8, 16), (124, 1, 62, 4, 3), (96, 4, 20, 8, 8),
+                                                   (80, 6, 27, 8, 12)])
+def test_register_schedule_restated_matches_oracle(n, k, rows, group, steps):
+    u0, v0 = gray_scott_initial(n)
+    u, v = u0.copy(), v0.copy()
+    for kk in [k] * (steps // k) + [1] * (steps % k):
+        u, v = _register_pass(u, v, kk, rows, group, GS_CFG)
+    wu, wv = oracle.gray_scott(u0, v0, GS_CFG, steps)
+    np.testing.assert_array_equal(u, wu)
+    np.testing.assert_array_equal(v, wv)
+
+
+@pytest.mark.parametrize("k,rows", [(4, 64), (8, 64)])
+def test_register_source_compiles_without_lds_or_spills(k, rows):
+    src = stencil.register_source(4096, k, rows, 0.16, 0.08, 0.037, 0.097, 1.0)
+    from palladium_amd.diagnostics import code_object_resources
+
+    res = code_object_resources(rt.compile_code_object(src, "gray_scott_regs", "fast"), "gray_scott_regs")
+    assert res.lds_bytes == 0 and res.vgpr_spills == 0 and res.scratch_bytes == 0
+    assert res.vgprs <= 128
+
+
+def test_register_bad_shapes_are_refused():
+    with pytest.raises(ValueError, match="positive"):
+        stencil.register_source(4096, 4, 0, 0.16, 0.08, 0.037, 0.097, 1.0)
+    with pytest.raises(ValueError, match="out of range"):
+        stencil.register_source(4096, 32, 64, 0.16, 0.08, 0.037, 0.097, 1.0)
+    with pytest.raises(ValueError, match="too small"):
+        stencil.register_source(32, 2, 16, 0.16, 0.08, 0.037, 0.097, 1.0)
