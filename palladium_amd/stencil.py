@@ -206,8 +206,8 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
                     group: int = 8) -> str:
     """HIP source of a K-step Gray-Scott pass with no LDS: each wave owns a
     strip of `rows` grid rows by 64 - 2K columns. Lane l walks down column
-    j0 - K + l from row i0 - K to row i0 + rows + K - 1, one input row at a
-    time. For each step t it keeps the last two rows of step t - 1 in
+    j0 - K + l from row i0 - K to row i0 + rows + K - 1 (in odd bands of
+    strips, up from i0 + rows + K - 1 to i0 - K), one input row at a time. For each step t it keeps the last two rows of step t - 1 in
     registers (the up and down neighbours) and takes the left and right
     neighbours from the adjacent lanes through DPP wave rotations: input row
     r yields step-t row r - t, so step K's row r - K leaves the pipeline as
@@ -255,7 +255,6 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
         f"    if (strip >= {waves}u) return;  /* whole waves only */",
         f"    const int lane = (int)(threadIdx.x % {WAVE}u);",
         f"    const int i0 = (int)(strip / {strips_j}u) * {rows};",
-        f"    const int last = {n} - i0 < {rows} ? {n} - i0 : {rows};  /* rows of this strip inside the grid */",
         f"    const int j0 = (int)(strip % {strips_j}u) * {w};",
         f"    int gj = j0 - {k} + lane;",
         f"    gj = gj < 0 ? gj + {n} : (gj >= {n} ? gj - {n} : gj);",
@@ -267,18 +266,25 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
         "       previous group's stores). */",
         f"    const __amdgpu_buffer_rsrc_t u_rs = __builtin_amdgcn_make_buffer_rsrc(u_out, (short)0, {n * n * 4}, PH_RSRC_WORD3);",
         f"    const __amdgpu_buffer_rsrc_t v_rs = __builtin_amdgcn_make_buffer_rsrc(v_out, (short)0, {n * n * 4}, PH_RSRC_WORD3);",
-        f"    const int top = i0 - {k} + {n};  /* row r of the strip is grid row (top + r) % n */",
+        "    /* Odd bands of strips walk up, even ones down: a band's last halo rows",
+        "       are then read at about the time the next band reads them too, which",
+        "       keeps them in L2. Pipeline row p is grid row (base + dir * p) % n. */",
+        f"    const bool up = ((strip / {strips_j}u) & 1u) != 0u;",
+        f"    const int base = up ? i0 + {rows - 1 + k + n} : i0 + {n - k};",
+        "    const int dir = up ? -1 : 1;",
         "    float " + ", ".join(f"pu{t}_{i} = 0.0f, pv{t}_{i} = 0.0f" for t in range(k) for i in (1, 2)) + ";",
     ]
     for g in range(group):
         lines.append(f"    float qu{g}, qv{g};")
-        lines.append(f"    {{ const int gi = (int)((unsigned int)(top + {g}) % {n}u); qu{g} = u_in[gi * {n} + gj]; qv{g} = v_in[gi * {n} + gj]; }}")
+        lines.append(f"    {{ const int gi = (int)((unsigned int)(base + dir * {min(g, h - 1)}) % {n}u); "
+                     f"qu{g} = u_in[gi * {n} + gj]; qv{g} = v_in[gi * {n} + gj]; }}")
     lines += [f"    for (int r0 = 0; r0 < {groups * group}; r0 += {group}) {{"]
-    # The next group's loads are unconditional (the last iteration reads
-    # wrapped rows it never uses): behind a branch, the wait for this
-    # group's rows would also wait for the first of them.
+    # The next group's loads are unconditional (past the strip's end they
+    # read its last row again, a cache hit): behind a branch, the wait for
+    # this group's rows would also wait for the first of them.
     for g in range(group):
-        lines.append(f"        const int gi{g} = (int)((unsigned int)(top + r0 + {group + g}) % {n}u);")
+        lines.append(f"        const int p{g} = r0 + {group + g} < {h - 1} ? r0 + {group + g} : {h - 1};")
+        lines.append(f"        const int gi{g} = (int)((unsigned int)(base + dir * p{g}) % {n}u);")
         lines.append(f"        const float nu{g} = u_in[gi{g} * {n} + gj], nv{g} = v_in[gi{g} * {n} + gj];")
     for g in range(group):
         lines.append(f"        {{ /* input row r0 + {g} */")
@@ -290,8 +296,9 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
             lines.append(f"            pu{t}_2 = pu{t}_1; pv{t}_2 = pv{t}_1; pu{t}_1 = {cur[0]}; pv{t}_1 = {cur[1]};")
             cur = out
         lines.append(f"            const int a = r0 + {g} - {2 * k};  /* output row, strip-relative */")
-        lines.append("            const bool keep = owner && a >= 0 && a < last;")
-        lines.append(f"            const int off = keep ? ((i0 + a) * {n} + (j0 + lane - {k})) * 4 : PH_DROP;")
+        lines.append(f"            const int ga = up ? i0 + {rows - 1} - a : i0 + a;  /* its grid row */")
+        lines.append(f"            const bool keep = owner && a >= 0 && a < {rows} && ga < {n};")
+        lines.append(f"            const int off = keep ? (ga * {n} + (j0 + lane - {k})) * 4 : PH_DROP;")
         lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[0]}), u_rs, off, 0, 0);")
         lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[1]}), v_rs, off, 0, 0);")
         lines.append("        }")

@@ -32,7 +32,7 @@ def test_lds_safe_bit_exact_against_oracle(k, th, tw, single, steps):
     np.testing.assert_array_equal(v, wv)
 
 
-@pytest.mark.parametrize("n,k,rows,group", [(256, 6, 64, 4), (256, 4, 40, 8), (256, 8, 27, 3), (192, 1, 64, 8),
+@pytest.mark.parametrize("n,k,rows,group", [(256, 6, 64, 4), (256, 4, 40, 8), (256, 8, 27, 3), (192, 1, 64, 8), (80, 3, 22, 5),
                                             (64, 12, 16, 8)])
 @pytest.mark.parametrize("steps", [12, 13])
 def test_regs_safe_bit_exact_against_oracle(n, k, rows, group, steps):

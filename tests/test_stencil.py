@@ -92,7 +92,7 @@ def test_bad_tiles_are_refused():
 
 def _register_pass(u, v, k, rows, group, cfg):
     """The register kernel's schedule, lane for lane: a wave's 64 lanes walk
-    down their columns, each step keeping two rows of the step before, the
+    down their columns (up, in odd bands of strips), each step keeping two rows of the step before, the
     left/right neighbours rotated in across the whole wave (np.roll), the
     windows starting at zero, row indices wrapping, and only owner lanes
     and rows K .. K + rows - 1 of step K stored."""
@@ -103,14 +103,15 @@ def _register_pass(u, v, k, rows, group, cfg):
     total = -(-h // group) * group
     uo, vo = np.full_like(u, np.nan), np.full_like(v, np.nan)
     lane = np.arange(64)
-    for i0 in range(0, n, rows):
-        last = min(rows, n - i0)
+    for band, i0 in enumerate(range(0, n, rows)):
+        up = band % 2 == 1  # odd bands walk up the grid
         for j0 in range(0, -(-n // w) * w, w):
             gj = (j0 - k + lane) % n
             owner = (lane >= k) & (lane < 64 - k) & (j0 + lane - k < n)
             win = [[np.zeros(64, F) for _ in range(4)] for _ in range(k)]  # pu2, pu1, pv2, pv1
             for r in range(total):
-                gi = (i0 - k + r) % n
+                p = min(r, h - 1)  # past the strip's end: its last row again
+                gi = (i0 + rows - 1 + k - p) % n if up else (i0 - k + p) % n
                 cu, cv = u[gi, gj], v[gi, gj]
                 for t in range(k):
                     pu2, pu1, pv2, pv1 = win[t]
@@ -134,18 +135,19 @@ def _register_pass(u, v, k, rows, group, cfg):
                     win[t] = [pu1, cu, pv1, cv]
                     cu, cv = yu, yv
                 a_row = r - 2 * k
-                if 0 <= a_row < last:
+                ga = i0 + rows - 1 - a_row if up else i0 + a_row
+                if 0 <= a_row < rows and ga < n:
                     cols = j0 + lane[owner] - k
-                    assert np.all(np.isnan(uo[i0 + a_row, cols])), "a cell stored twice"
-                    uo[i0 + a_row, cols] = cu[owner]
-                    vo[i0 + a_row, cols] = cv[owner]
+                    assert np.all(np.isnan(uo[ga, cols])), "a cell stored twice"
+                    uo[ga, cols] = cu[owner]
+                    vo[ga, cols] = cv[owner]
     assert not np.isnan(uo).any() and not np.isnan(vo).any(), "a cell never stored"
     return uo, vo
 
 
 @pytest.mark.parametrize("n,k,rows,group,steps", [(64, 4, 16, 8, 8), (64, 4, 16, 8, 9), (64, 3, 32, 5, 6),
                                                    (64, 8, 16, 8, 16), (124, 1, 62, 4, 3), (96, 4, 20, 8, 8),
-                                                   (80, 6, 27, 8, 12)])
+                                                   (80, 6, 27, 8, 12), (80, 3, 22, 5, 7)])
 def test_register_schedule_restated_matches_oracle(n, k, rows, group, steps):
     u0, v0 = gray_scott_initial(n)
     u, v = u0.copy(), v0.copy()
