@@ -1195,7 +1195,7 @@ def main() -> int:
         # other hot kernels at their configurations, are reported beside the
         # first (GPU only, no CPU baselines: a few seconds in all).
         res["secondary"] = {}
-        for key, fn in (("gray_scott_4096", bench_gs), ("gray_scott_4096_4_steps_per_pass", bench_gs_fused),
+        for key, fn in (("gray_scott_4096", bench_gs), ("gray_scott_4096_temporal_blocking", bench_gs_fused),
                         ("gbm_paths", bench_gbm), ("gbm_block_sums", bench_gbm_block),
                         ("bs3_vdp", bench_bs3), ("lv_rk4_df32", bench_df32)):
             r = fn(a.steps, a.warmup, cpu=False)
