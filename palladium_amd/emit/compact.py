@@ -45,10 +45,11 @@ from palladium_amd.ir import KeyAval
 WORKGROUP = 1024
 EPOCH = 64
 # LDS per workgroup the compaction may use (2 workgroups per CU fit in 160 KB).
-LDS_BUDGET = 72 * 1024
+LDS_BUDGET = 78 * 1024
 
 _LANE_SPECIFIC = {"program_id", "num_programs", "get", "swap", "lane_index", "lane_reduce", "while"}
-_STORABLE = {"float32": "f", "int32": "i", "uint32": "u", "bool": "b"}
+# dtype -> 32-bit LDS words per value
+_STORABLE = {"float32": 1, "int32": 1, "uint32": 1, "bool": 1, "float64": 2}
 
 
 @dataclasses.dataclass(frozen=True)
@@ -106,27 +107,50 @@ def plan_for(spec: Any, jaxpr: Any, lanes: int, block: int | None) -> CompactPla
     if not all(_storable(v) for v in list(e.invars) + list(e.outvars)):
         return None
     used = {v for x in jaxpr.eqns for v in x.invars} | set(jaxpr.outvars)
-    n_state = len(e.invars) + 1  # operands and carries, plus the slot index
-    n_kept = sum(1 for v in e.outvars if v in used)  # final carries read after the loop
+    n_state = sum(_nwords(v) for v in e.invars) + 1  # operands and carries, plus the slot index
+    n_kept = sum(_nwords(v) for v in e.outvars if v in used)  # final carries read after the loop
     if (n_state + n_kept) * WORKGROUP * 4 > LDS_BUDGET:
         return None
     return CompactPlan(whiles[0])
 
 
-def _to_bits(expr: str, ctype: str) -> str:
-    if ctype == "float":
-        return f"__float_as_uint({expr})"
-    if ctype == "bool":
-        return f"({expr} ? 1u : 0u)"
-    return f"(unsigned int)({expr})"
+def _nwords(v: Any) -> int:
+    return _STORABLE[np.dtype(v.aval.dtype).name]
 
 
-def _from_bits(expr: str, ctype: str) -> str:
-    if ctype == "float":
-        return f"__uint_as_float({expr})"
-    if ctype == "bool":
-        return f"({expr} != 0u)"
-    return f"({ctype})({expr})"
+def _store(arr: str, j: int, pos: str, c: Any) -> tuple[list[str], int]:
+    """Lines writing value `c` to rows j, j+1, ... of LDS array `arr` at
+    column `pos`, and the next free row."""
+    e, t = c.expr, c.ctype
+    if t == "double":
+        bits = f"(unsigned long long)__double_as_longlong({e})"
+        return [f"{arr}[{j}][{pos}] = (unsigned int)({bits});",
+                f"{arr}[{j + 1}][{pos}] = (unsigned int)(({bits}) >> 32);"], j + 2
+    if t == "float":
+        word = f"__float_as_uint({e})"
+    elif t == "bool":
+        word = f"({e} ? 1u : 0u)"
+    else:
+        word = f"(unsigned int)({e})"
+    return [f"{arr}[{j}][{pos}] = {word};"], j + 1
+
+
+def _load(arr: str, j: int, pos: str, c: Any) -> tuple[str, int]:
+    """The line reading `c` back from rows j, ... of `arr`, and the next row."""
+    e, t = c.expr, c.ctype
+    if t == "double":
+        return (f"{e} = __longlong_as_double((long long)(((unsigned long long){arr}[{j + 1}][{pos}] << 32)"
+                f" | (unsigned long long){arr}[{j}][{pos}]));"), j + 2
+    w = f"{arr}[{j}][{pos}]"
+    if t == "float":
+        return f"{e} = __uint_as_float({w});", j + 1
+    if t == "bool":
+        return f"{e} = ({w} != 0u);", j + 1
+    return f"{e} = ({t})({w});", j + 1
+
+
+def _rows(vals: list) -> int:
+    return sum(2 if c.ctype == "double" else 1 for c in vals)
 
 
 def emit_compacting_while(env: Any, cursor: Any, eqn: Any, emit_jaxpr: Any, declare_carries: Any,
@@ -149,9 +173,10 @@ def emit_compacting_while(env: Any, cursor: Any, eqn: Any, emit_jaxpr: Any, decl
     kept = [(k, c) for k, (c, ov) in enumerate(zip(carries, eqn.outvars)) if env.used(ov)]
     nw = WORKGROUP // 64
     buf, res, cnt = cursor.fresh("_cbuf"), cursor.fresh("_cres"), cursor.fresh("_ccnt")
-    cursor.emit(f"__shared__ unsigned int {buf}[{len(state) + 1}][{WORKGROUP}];")
+    n_rows, kept_vals = _rows(state), [c for _, c in kept]
+    cursor.emit(f"__shared__ unsigned int {buf}[{n_rows + 1}][{WORKGROUP}];")
     if kept:
-        cursor.emit(f"__shared__ unsigned int {res}[{len(kept)}][{WORKGROUP}];")
+        cursor.emit(f"__shared__ unsigned int {res}[{_rows(kept_vals)}][{WORKGROUP}];")
     cursor.emit(f"__shared__ int {cnt}[{nw}];")
     slot, own = cursor.fresh("_slot"), cursor.fresh("_own")
     first = f"(_in ? (int)threadIdx.x : -1)" if getattr(env, "compact_in", None) else "(int)threadIdx.x"
@@ -172,8 +197,11 @@ def emit_compacting_while(env: Any, cursor: Any, eqn: Any, emit_jaxpr: Any, decl
         (pred,) = emit_jaxpr(env, cursor, cj, cond_consts + carries)
         cursor.emit(f"bool {own} = ({pred.at('0')}) && {slot} >= 0;")
         with cursor.block(f"if (!{own} && {slot} >= 0)"):
-            for j, (_, c) in enumerate(kept):
-                cursor.emit(f"{res}[{j}][{slot}] = {_to_bits(c.expr, c.ctype)};")
+            j = 0
+            for c in kept_vals:
+                lines, j = _store(res, j, slot, c)
+                for line in lines:
+                    cursor.emit(line)
             cursor.emit(f"{slot} = -1;")
         mask, total, before, active = (cursor.fresh(p) for p in ("_cm", "_ctot", "_cbef", "_cact"))
         cursor.emit(f"const unsigned long long {mask} = __ballot({own});")
@@ -193,18 +221,25 @@ def emit_compacting_while(env: Any, cursor: Any, eqn: Any, emit_jaxpr: Any, decl
                 pos = cursor.fresh("_cpos")
                 cursor.emit(f"const int {pos} = {before} + (int)__builtin_amdgcn_mbcnt_hi("
                             f"(unsigned int)({mask} >> 32), __builtin_amdgcn_mbcnt_lo((unsigned int){mask}, 0u));")
-                for j, c in enumerate(state):
-                    cursor.emit(f"{buf}[{j}][{pos}] = {_to_bits(c.expr, c.ctype)};")
-                cursor.emit(f"{buf}[{len(state)}][{pos}] = (unsigned int){slot};")
+                j = 0
+                for c in state:
+                    lines, j = _store(buf, j, pos, c)
+                    for line in lines:
+                        cursor.emit(line)
+                cursor.emit(f"{buf}[{n_rows}][{pos}] = (unsigned int){slot};")
             cursor.emit("__syncthreads();")
             with cursor.block(f"if ((int)threadIdx.x < {total})"):
-                for j, c in enumerate(state):
-                    cursor.emit(f"{c.expr} = {_from_bits(f'{buf}[{j}][threadIdx.x]', c.ctype)};")
-                cursor.emit(f"{slot} = (int){buf}[{len(state)}][threadIdx.x];")
+                j = 0
+                for c in state:
+                    line, j = _load(buf, j, "threadIdx.x", c)
+                    cursor.emit(line)
+                cursor.emit(f"{slot} = (int){buf}[{n_rows}][threadIdx.x];")
             with cursor.block("else"):
                 cursor.emit(f"{slot} = -1;")
         # Nothing is written to LDS again before every lane has read.
         cursor.emit("__syncthreads();")
     # Every instance has finished: each lane takes its own back.
-    for j, (_, c) in enumerate(kept):
-        cursor.emit(f"{c.expr} = {_from_bits(f'{res}[{j}][threadIdx.x]', c.ctype)};")
+    j = 0
+    for c in kept_vals:
+        line, j = _load(res, j, "threadIdx.x", c)
+        cursor.emit(line)

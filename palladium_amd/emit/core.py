@@ -26,6 +26,7 @@ import contextlib
 import dataclasses
 import itertools
 import math
+import os
 import string
 from collections.abc import Callable, Iterator
 from typing import Any
@@ -73,9 +74,14 @@ DEFAULT_BLOCK = 256
 NUM_XCDS = 8
 
 
+# Value types only rewrites introduce (never a kernel operand): the double
+# log2 that the SAFE power carries between loop iterations.
+INTERNAL_CTYPES = {"float64": "double"}
+
+
 def ctype_of(dtype: Any) -> str:
     name = dtype_name(dtype)
-    c = CTYPES.get(name)
+    c = CTYPES.get(name) or INTERNAL_CTYPES.get(name)
     if c is None:
         raise EmitError(f"dtype {name} has no HIP lowering (supported: {', '.join(CTYPES)})")
     return c
@@ -495,11 +501,20 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         params.append(f"{qual}{ct}* __restrict__ arg{k}_base")
 
     body = plan.jaxpr if plan else spec.jaxpr
+    from palladium_amd.emit.compact import plan_for
+
     if math_mode is not None and math_mode_ordinal(math_mode) == 2:
         from palladium_amd.emit.optimize import fast_rewrites
 
         body = fast_rewrites(body)
-    from palladium_amd.emit.compact import plan_for
+    elif (math_mode is not None and math_mode_ordinal(math_mode) == 0
+          and os.environ.get("PALLADIUM_SHARE_POW_LOGS", "1") != "0"):
+        from palladium_amd.emit.optimize import share_pow_logs
+
+        shared = share_pow_logs(body)
+        # The extra carries must not cost the loop its compaction.
+        if not (plan is None and geo.block == 1024) or plan_for(spec, shared, lanes, block) is not None:
+            body = shared
 
     cplan = plan_for(spec, body, lanes, block)
     if (cplan is not None) != (plan is None and geo.block == 1024 and plan_for(spec, spec.jaxpr, lanes, block) is not None):

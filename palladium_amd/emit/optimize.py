@@ -45,7 +45,7 @@ import numpy as np
 
 from palladium_amd.ir import ClosedJaxpr, Jaxpr, JaxprEqn, Literal, ShapedArray, Var, primitive
 
-__all__ = ["drop_redundant_clamps", "factor_common_products", "fast_rewrites", "power_laws_to_exp2"]
+__all__ = ["drop_redundant_clamps", "factor_common_products", "fast_rewrites", "power_laws_to_exp2", "share_pow_logs"]
 
 
 def _same(a: Any, b: Any) -> bool:
@@ -351,3 +351,102 @@ def factor_common_products(jaxpr: Jaxpr) -> Jaxpr:
                     continue
         new_eqns.append(e)
     return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)
+
+
+def _closed_like(orig: Any, jaxpr: Jaxpr) -> Any:
+    return ClosedJaxpr(jaxpr, orig.consts) if isinstance(orig, ClosedJaxpr) else jaxpr
+
+
+def share_pow_logs(jaxpr: Jaxpr) -> Jaxpr:
+    """SAFE rewrite, exact: `pow(x, y)` is `pow_with_log(x, y, pow_log(x))`
+    bit for bit (the deterministic power splits into the double log2 of its
+    base and the rest), so a while loop whose body takes the power of a
+    carry `c` and of a value `v`, and updates the carry as
+    `c' = select_n(p, c, v)` (either case order), can carry `pow_log(c)`
+    beside `c`: the body uses the carried log for `c`'s powers, computes
+    `pow_log(v)` once for all of `v`'s powers, and selects the next log as
+    it selects the next carry. A power-law step-size controller
+    (`tests/test_08_adaptive.py:76-122` of the reference:
+    `factor = safety * inv_err**c1 * prev**c2`, `prev = where(accept,
+    inv_err, prev)`) then computes one log per attempt instead of two."""
+    new_eqns: list[JaxprEqn] = []
+    for e in jaxpr.eqns:
+        params = {k: _rewrite_sub(v, share_pow_logs) for k, v in e.params.items()}
+        e = JaxprEqn(e.invars, e.outvars, e.primitive, params)
+        if e.primitive.name == "while":
+            pre, e = _share_while(e)
+            new_eqns += pre
+        new_eqns.append(e)
+    return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)
+
+
+def _f64(shape: tuple) -> ShapedArray:
+    return ShapedArray(shape, np.float64)
+
+
+def _share_while(e: JaxprEqn) -> tuple[list[JaxprEqn], JaxprEqn]:
+    cn, bn = int(e.params["cond_nconsts"]), int(e.params["body_nconsts"])
+    body = getattr(e.params["body_jaxpr"], "jaxpr", e.params["body_jaxpr"])
+    cond = getattr(e.params["cond_jaxpr"], "jaxpr", e.params["cond_jaxpr"])
+    carries = body.invars[bn:]
+    producer = {ov: x for x in body.eqns for ov in x.outvars}
+
+    def f32_scalarish(v: Any) -> bool:
+        return isinstance(v, Var) and np.dtype(v.aval.dtype) == np.float32
+
+    bases = {x.invars[0] for x in body.eqns if x.primitive.name == "pow" and f32_scalarish(x.invars[0])}
+    found = []  # (carry index, carry var, other case, select eqn)
+    for k, c in enumerate(carries):
+        if c not in bases:
+            continue
+        sel = producer.get(body.outvars[k])
+        if sel is None or sel.primitive.name != "select_n" or len(sel.invars) != 3:
+            continue
+        if np.dtype(sel.invars[0].aval.dtype) != np.bool_:
+            continue
+        cases = sel.invars[1:]
+        others = [v for v in cases if v is not c]
+        if len(others) != 1 or sum(v is c for v in cases) != 1:
+            continue
+        v = others[0]
+        if v not in bases or tuple(v.aval.shape) != tuple(c.aval.shape):
+            continue
+        found.append((k, c, v, sel))
+    if not found:
+        return [], e
+    log_of: dict[Any, Any] = {}
+    new_in = []
+    for k, c, _, _ in found:
+        log_of[c] = Var(_f64(tuple(c.aval.shape)))
+        new_in.append(log_of[c])
+    wanted = {v for _, _, v, _ in found}
+    eqns: list[JaxprEqn] = []
+    for x in body.eqns:
+        if x.primitive.name == "pow" and x.invars[0] in (set(log_of) | wanted):
+            b = x.invars[0]
+            if b not in log_of:  # first power of v: its log, once
+                log_of[b] = Var(_f64(tuple(b.aval.shape)))
+                eqns.append(JaxprEqn([b], [log_of[b]], primitive("pow_log"), {}))
+            eqns.append(JaxprEqn([b, x.invars[1], log_of[b]], x.outvars, primitive("pow_with_log"), {}))
+            continue
+        eqns.append(x)
+    new_out = []
+    for k, c, v, sel in found:
+        nxt = Var(_f64(tuple(c.aval.shape)))
+        cases = [log_of[c] if u is c else log_of[v] for u in sel.invars[1:]]
+        eqns.append(JaxprEqn([sel.invars[0], *cases], [nxt], primitive("select_n"), {}))
+        new_out.append(nxt)
+    new_body = Jaxpr(body.constvars, body.invars + new_in, body.outvars + new_out, eqns)
+    new_cond = Jaxpr(cond.constvars, cond.invars + [Var(_f64(tuple(c.aval.shape))) for _, c, _, _ in found],
+                     cond.outvars, cond.eqns)
+    pre, inits = [], []
+    for k, c, _, _ in found:
+        init = e.invars[cn + bn + k]
+        lv = Var(_f64(tuple(c.aval.shape)))
+        pre.append(JaxprEqn([init], [lv], primitive("pow_log"), {}))
+        inits.append(lv)
+    params = dict(e.params)
+    params["body_jaxpr"] = _closed_like(e.params["body_jaxpr"], new_body)
+    params["cond_jaxpr"] = _closed_like(e.params["cond_jaxpr"], new_cond)
+    outs = e.outvars + [Var(_f64(tuple(c.aval.shape))) for _, c, _, _ in found]
+    return pre, JaxprEqn(e.invars + inits, outs, e.primitive, params)

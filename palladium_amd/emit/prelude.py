@@ -157,11 +157,22 @@ __device__ __forceinline__ double ph_exp2_dbl(double z) {
     return ldexp(p, (int)kd);
 }
 
+/* The part of ph_pow that depends on the base alone: log2 |x| for a
+   finite nonzero base (log2 1 = 0 otherwise, which the special cases then
+   override). ph_pow(x, y) == ph_pow_with_log(x, y, ph_pow_log(x)) bit for
+   bit, so a loop can compute the log of a base once and use it in several
+   powers, or carry it with the base. */
+__device__ __forceinline__ double ph_pow_log(float x) {
+    float ax = fabsf(x);
+    bool finite_base = ax > 0.0f && ax < __builtin_inff();
+    return ph_log2_pos((double)(finite_base ? ax : 1.0f));
+}
+
 /* Branch-free: the main path runs on a harmless base for special operands
    and the C99 special cases are selected over it, highest priority last,
    so the loop around it carries no exec-mask branches. Same results as
    oracle/oracle.c:oracle_pow, which tests them in order. */
-__device__ __forceinline__ float ph_pow(float x, float y) {
+__device__ __forceinline__ float ph_pow_with_log(float x, float y, double lg) {
     const float inf = __builtin_inff();
     float ax = fabsf(x);
     float ay = fabsf(y);
@@ -170,8 +181,7 @@ __device__ __forceinline__ float ph_pow(float x, float y) {
     /* fmodf(ay, 2) == 1 for an integral ay below 2^24, exactly */
     bool y_odd = y_int && small && (ay - 2.0f * truncf(0.5f * ay) == 1.0f);
     float sign = (__builtin_signbit(x) && y_odd) ? -1.0f : 1.0f; /* -0 too: pow(-0, 3) = -0 */
-    bool finite_base = ax > 0.0f && ax < inf;
-    double z = (double)y * ph_log2_pos((double)(finite_base ? ax : 1.0f));
+    double z = (double)y * lg;
     double zc = fmin(fmax(z, -151.0), 129.0);
     float r = sign * (float)ph_exp2_dbl(zc);
     r = (z > 129.0) ? sign * inf : r;
@@ -184,6 +194,8 @@ __device__ __forceinline__ float ph_pow(float x, float y) {
     r = (y == 0.0f || x == 1.0f) ? 1.0f : r;
     return r;
 }
+
+__device__ __forceinline__ float ph_pow(float x, float y) { return ph_pow_with_log(x, y, ph_pow_log(x)); }
 #elif PH_MATH_MODE == 2
 /* FAST: x^y = 2^(y log2 x) on the hardware base-2 logarithm and
    exponential (v_log_f32, v_exp_f32) for a positive normal finite base and

@@ -87,6 +87,10 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
         return "ph_fmax({a}, {b})" if f else "(({a} > {b}) ? {a} : {b})"
     if opname == "pow":
         return "ph_pow({a}, {b})"
+    if opname == "pow_log":
+        return "ph_pow_log({a})"
+    if opname == "pow_with_log":
+        return "ph_pow_with_log({a}, {b}, {c})"
     if opname == "neg":
         return "(-{a})"
     if opname == "abs":
@@ -254,7 +258,8 @@ def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     _emit_elementwise_loops(cursor, dst, body)
 
 
-for _name in [*ELEMENTWISE, "integer_pow", "convert_element_type", "bitcast_convert_type", "select_n"]:
+for _name in [*ELEMENTWISE, "integer_pow", "convert_element_type", "bitcast_convert_type", "select_n",
+              "pow_log", "pow_with_log"]:
     RULES[_name] = _rule_elementwise
 
 
