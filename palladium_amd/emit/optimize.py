@@ -45,7 +45,8 @@ import numpy as np
 
 from palladium_amd.ir import ClosedJaxpr, Jaxpr, JaxprEqn, Literal, ShapedArray, Var, primitive
 
-__all__ = ["drop_redundant_clamps", "factor_common_products", "fast_rewrites", "power_laws_to_exp2", "share_pow_logs"]
+__all__ = ["carry_logs", "drop_redundant_clamps", "factor_common_products", "fast_rewrites", "power_laws_to_exp2",
+           "share_pow_logs"]
 
 
 def _same(a: Any, b: Any) -> bool:
@@ -67,7 +68,7 @@ def _rewrite_sub(v: Any, fn: Any = None) -> Any:
 
 def fast_rewrites(jaxpr: Jaxpr) -> Jaxpr:
     """Every FAST-only rewrite, in order."""
-    return factor_common_products(power_laws_to_exp2(drop_redundant_clamps(jaxpr)))
+    return factor_common_products(carry_logs(power_laws_to_exp2(drop_redundant_clamps(jaxpr))))
 
 
 def _lower_bound(v: Any, producer: dict) -> float | None:
@@ -450,3 +451,123 @@ def _share_while(e: JaxprEqn) -> tuple[list[JaxprEqn], JaxprEqn]:
     params["cond_jaxpr"] = _closed_like(e.params["cond_jaxpr"], new_cond)
     outs = e.outvars + [Var(_f64(tuple(c.aval.shape))) for _, c, _, _ in found]
     return pre, JaxprEqn(e.invars + inits, outs, e.primitive, params)
+
+
+def carry_logs(jaxpr: Jaxpr) -> Jaxpr:
+    """FAST: a while-loop carry `c` that the body reads only through
+    `log2(c)` and updates only as `c' = select_n(p, c, v)` (either case
+    order), and that neither the condition nor the code after the loop
+    reads, is replaced by its log2: the body uses the carried log, the
+    update selects `log2(v)` (for `v = 1 / y`, `-log2(y)`, reusing a log2 of
+    y the body already takes), and the initial value's log is taken once
+    before the loop. After `power_laws_to_exp2`, the PI controller's
+    `prev_inv_err` (`tests/test_08_adaptive.py:76-122` of the reference) is
+    such a carry: the attempt then computes neither the reciprocal of the
+    error nor the log of `prev`. Results differ from the unrewritten loop
+    by the rounding of log2(1 / y) against -log2(y), within FAST's contract."""
+    used_after: set = set()
+    for e in jaxpr.eqns:
+        used_after.update(v for v in e.invars if isinstance(v, Var))
+    used_after.update(v for v in jaxpr.outvars if isinstance(v, Var))
+    new_eqns: list[JaxprEqn] = []
+    for e in jaxpr.eqns:
+        params = {k: _rewrite_sub(v, carry_logs) for k, v in e.params.items()}
+        e = JaxprEqn(e.invars, e.outvars, e.primitive, params)
+        if e.primitive.name == "while":
+            pre, e = _carry_logs_while(e, used_after)
+            new_eqns += pre
+        new_eqns.append(e)
+    return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)
+
+
+def _carry_logs_while(e: JaxprEqn, used_after: set) -> tuple[list[JaxprEqn], JaxprEqn]:
+    cn, bn = int(e.params["cond_nconsts"]), int(e.params["body_nconsts"])
+    body = getattr(e.params["body_jaxpr"], "jaxpr", e.params["body_jaxpr"])
+    cond = getattr(e.params["cond_jaxpr"], "jaxpr", e.params["cond_jaxpr"])
+    carries = body.invars[bn:]
+    producer = {ov: x for x in body.eqns for ov in x.outvars}
+    readers: dict[Any, list] = {}
+    for x in body.eqns:
+        for v in x.invars:
+            if isinstance(v, Var):
+                readers.setdefault(v, []).append(x)
+    out_pos: dict[Any, list] = {}
+    for k, v in enumerate(body.outvars):
+        out_pos.setdefault(v, []).append(k)
+    cond_used = {v for x in cond.eqns for v in x.invars} | set(cond.outvars)
+
+    def f32(v: Any) -> bool:
+        return isinstance(v, Var) and np.dtype(v.aval.dtype) == np.float32
+
+    plans = []
+    for k, c in enumerate(carries):
+        if not f32(c) or cond.invars[cn + k] in cond_used or e.outvars[k] in used_after:
+            continue
+        sel = producer.get(body.outvars[k])
+        if sel is None or sel.primitive.name != "select_n" or len(sel.invars) != 3:
+            continue
+        cases = sel.invars[1:]
+        if sum(u is c for u in cases) != 1 or out_pos.get(body.outvars[k]) != [k]:
+            continue
+        (v,) = [u for u in cases if u is not c]
+        rs = readers.get(c, [])
+        logs = [x for x in rs if x.primitive.name == "log2"]
+        if not logs or len(logs) + 1 != len(rs) or sel not in rs or readers.get(body.outvars[k], []):
+            continue
+        # log2(v): an existing log2 of v, or -log2(y) for v = 1 / y with log2(y) taken
+        lv = next((x.outvars[0] for x in readers.get(v, []) if x.primitive.name == "log2"), None)
+        neg_of = None
+        if lv is None:
+            d = producer.get(v)
+            if (d is not None and d.primitive.name == "div" and _f32_literal(d.invars[0]) == 1.0
+                    and isinstance(d.invars[1], Var)):
+                neg_of = next((x.outvars[0] for x in readers.get(d.invars[1], []) if x.primitive.name == "log2"),
+                              None)
+            if neg_of is None:
+                continue
+        plans.append((k, c, v, sel, logs, lv, neg_of))
+    if not plans:
+        return [], e
+    subst: dict[Any, Any] = {}
+    new_in = list(body.invars)
+    extra: list[JaxprEqn] = []
+    new_out = list(body.outvars)
+    drop = set()
+    for k, c, v, sel, logs, lv, neg_of in plans:
+        lc = Var(ShapedArray(c.aval.shape, np.float32))
+        new_in[bn + k] = lc
+        for x in logs:
+            subst[x.outvars[0]] = lc
+            drop.add(id(x))
+        if lv is None:
+            lv = Var(ShapedArray(c.aval.shape, np.float32))
+            extra.append(JaxprEqn([neg_of], [lv], primitive("neg"), {}))
+        nxt = Var(ShapedArray(c.aval.shape, np.float32))
+        cases = [lc if u is c else lv for u in sel.invars[1:]]
+        extra.append(JaxprEqn([sel.invars[0], *cases], [nxt], primitive("select_n"), {}))
+        new_out[k] = nxt
+        drop.add(id(sel))
+
+    def sub(v: Any) -> Any:
+        return subst.get(v, v) if isinstance(v, Var) else v
+
+    eqns = [JaxprEqn([sub(v) for v in x.invars], x.outvars, x.primitive, x.params)
+            for x in body.eqns if id(x) not in drop] + extra
+    new_body = Jaxpr(body.constvars, new_in, [sub(v) for v in new_out], eqns)
+    new_cond_in = list(cond.invars)
+    for k, *_ in plans:
+        new_cond_in[cn + k] = Var(ShapedArray(cond.invars[cn + k].aval.shape, np.float32))
+    new_cond = Jaxpr(cond.constvars, new_cond_in, cond.outvars, cond.eqns)
+    pre, inits = [], list(e.invars)
+    for k, c, *_ in plans:
+        lv0 = Var(ShapedArray(c.aval.shape, np.float32))
+        pre.append(JaxprEqn([e.invars[cn + bn + k]], [lv0], primitive("log2"), {}))
+        inits[cn + bn + k] = lv0
+    params = dict(e.params)
+    params["body_jaxpr"] = _closed_like(e.params["body_jaxpr"], new_body)
+    params["cond_jaxpr"] = _closed_like(e.params["cond_jaxpr"], new_cond)
+    outs = list(e.outvars)
+    for k, *_ in plans:
+        outs[k] = Var(ShapedArray(outs[k].aval.shape, np.float32))  # no longer the carry's value
+    return pre, JaxprEqn(inits, outs, e.primitive, params)
+
