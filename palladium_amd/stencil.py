@@ -165,19 +165,19 @@ _DPP_FROM_RIGHT = 0x134
 _DPP_FROM_LEFT = 0x13C
 
 
-def _reg_update(lit: dict, up: tuple, mid: tuple, down: tuple, out: tuple, tag: str) -> list[str]:
-    """One row of the next step from three rows of this one held in this
-    lane's registers (each a (u, v) pair of names); the left and right
-    columns are rotated in from the neighbouring lanes. The op order of
-    `_update`."""
+def _reg_update(lit: dict, up: tuple, mid: tuple, down: tuple, left: tuple, right: tuple, out: tuple,
+                tag: str) -> list[str]:
+    """One cell of the next step from its column's three rows of this step
+    (each a (u, v) pair of register names) and its left and right
+    neighbours (expressions: a register of this lane, or one rotated in from
+    the neighbouring lane). The op order of `_update`."""
     lines = []
-    for i, (f, d) in enumerate((("u", "DU"), ("v", "DV"))):
-        c = mid[i]
+    for i, f in enumerate("uv"):
         lines += [
             f"float l{f}{tag} = {down[i]} + {up[i]};",
-            f"l{f}{tag} = l{f}{tag} + ph_from_right({c});",
-            f"l{f}{tag} = l{f}{tag} + ph_from_left({c});",
-            f"l{f}{tag} = l{f}{tag} - 4.0f * {c};",
+            f"l{f}{tag} = l{f}{tag} + {right[i]};",
+            f"l{f}{tag} = l{f}{tag} + {left[i]};",
+            f"l{f}{tag} = l{f}{tag} - 4.0f * {mid[i]};",
         ]
     uc, vc = mid
     lines += [
@@ -194,48 +194,59 @@ def _reg_update(lit: dict, up: tuple, mid: tuple, down: tuple, out: tuple, tag: 
     return lines
 
 
-def register_geometry(n: int, k: int, rows: int) -> tuple[int, int]:
+def register_geometry(n: int, k: int, rows: int, cols: int = 1) -> tuple[int, int]:
     """(waves, workgroups) of a register pass: one wave per strip of `rows`
-    rows by 64 - 2K columns (the last strip of each kind may reach past the
-    grid), four waves per workgroup."""
-    waves = -(-n // rows) * -(-n // (WAVE - 2 * k))
+    rows by 64 `cols` - 2K columns (the last strip of each kind may reach
+    past the grid), four waves per workgroup."""
+    waves = -(-n // rows) * -(-n // (WAVE * cols - 2 * k))
     return waves, -(-waves // (WORKGROUP // WAVE))
 
 
 def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, fk: float, dt: float,
-                    group: int = 8) -> str:
+                    group: int = 8, cols: int = 1) -> str:
     """HIP source of a K-step Gray-Scott pass with no LDS: each wave owns a
-    strip of `rows` grid rows by 64 - 2K columns. Lane l walks down column
-    j0 - K + l from row i0 - K to row i0 + rows + K - 1 (in odd bands of
-    strips, up from i0 + rows + K - 1 to i0 - K), one input row at a time. For each step t it keeps the last two rows of step t - 1 in
-    registers (the up and down neighbours) and takes the left and right
-    neighbours from the adjacent lanes through DPP wave rotations: input row
-    r yields step-t row r - t, so step K's row r - K leaves the pipeline as
-    row r comes in. Edge lanes and the first rows of each step read values
-    that are not yet (or no longer) valid; each step moves that region in by
-    one lane and one row per side, so after K steps lanes K .. 63 - K and
-    rows K .. K + rows - 1 are exact, and only those are stored. Rows come
-    in `group` at a time, the next group's loads issued before the current
-    group's arithmetic. Row indices wrap around the grid, so every load is
-    in bounds; the last strip of a row (and of a column) may reach past the
-    grid, and its lanes (rows) outside it store nothing."""
-    w = WAVE - 2 * k
+    strip of `rows` grid rows by 64 C - 2K columns, C = `cols`. Lane l holds
+    strip columns C l .. C l + C - 1 (grid columns j0 - K + those) and walks
+    down them from row i0 - K to row i0 + rows + K - 1 (in odd bands of
+    strips, up from i0 + rows + K - 1 to i0 - K), one input row at a time.
+    For each step t it keeps the last two rows of step t - 1 in registers
+    (the up and down neighbours); a column's left and right neighbours are
+    the lane's own registers, except at the lane's first and last column,
+    whose outer neighbours come from the adjacent lanes through DPP wave
+    rotations (so a lane of C columns rotates 2 values per field and step
+    where C lanes of one column would rotate 2 C; on gfx950 a DPP add costs
+    several plain ones). Input row r yields step-t row r - t, so step K's
+    row r - K leaves the pipeline as row r comes in. The outer columns and
+    the first rows of each step read values that are not yet (or no longer)
+    valid; each step moves that region in by one column and one row per
+    side, so after K steps strip columns K .. 64 C - 1 - K and rows
+    K .. K + rows - 1 are exact, and only those are stored. Rows come in
+    `group` at a time, the next group's loads issued before the current
+    group's arithmetic. Row and column indices wrap around the grid, so
+    every load is in bounds; the last strip of a row (and of a column) may
+    reach past the grid, and its columns (rows) outside it store nothing."""
+    w = WAVE * cols - 2 * k
+    if cols < 1:
+        raise ValueError(f"columns per lane {cols} must be positive")
     if k < 1 or w < 1:
-        raise ValueError(f"steps per pass {k} out of range for a {WAVE}-lane wave")
+        raise ValueError(f"steps per pass {k} out of range for a {WAVE}-lane wave of {cols} columns per lane")
     if rows < 1:
         raise ValueError(f"strip height {rows} must be positive")
     if n * n * 4 >= 1 << 31:
         raise ValueError(f"grid {n}x{n} exceeds the 2 GiB a buffer descriptor addresses")
-    if rows + 2 * k > n or n < WAVE:
-        raise ValueError(f"grid {n}x{n} too small for {rows}-row strips with a {k}-row halo (and one {WAVE}-lane wave)")
+    if rows + 2 * k > n or n < WAVE * cols:
+        raise ValueError(f"grid {n}x{n} too small for {rows}-row strips with a {k}-row halo "
+                         f"(and one {WAVE}-lane wave of {cols} columns per lane)")
     h = rows + 2 * k
     groups = -(-h // group)
     strips_j = -(-n // w)
-    waves, blocks = register_geometry(n, k, rows)
+    waves, blocks = register_geometry(n, k, rows, cols)
     per, rem = divmod(blocks, NUM_XCDS)
     lit = {name: format_float(v) for name, v in (("DU", du), ("DV", dv), ("F", f), ("FK", fk), ("DT", dt))}
+    C = cols
     lines = [
-        f"// Gray-Scott, {k} steps per pass in registers, {rows}x{w} strips, {n}x{n} periodic grid.",
+        f"// Gray-Scott, {k} steps per pass in registers, {rows}x{w} strips, {C} columns per lane, "
+        f"{n}x{n} periodic grid.",
         "#define PH_RSRC_WORD3 0x00020000  /* gfx9 buffer descriptor word 3: 32-bit elements, raw */",
         "#define PH_DROP ((int)0x80000000)  /* an offset past every field: the store is dropped */",
         "static __device__ __forceinline__ float ph_from_right(float x) {",
@@ -256,14 +267,20 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
         f"    const int lane = (int)(threadIdx.x % {WAVE}u);",
         f"    const int i0 = (int)(strip / {strips_j}u) * {rows};",
         f"    const int j0 = (int)(strip % {strips_j}u) * {w};",
-        f"    int gj = j0 - {k} + lane;",
-        f"    gj = gj < 0 ? gj + {n} : (gj >= {n} ? gj - {n} : gj);",
-        f"    const bool owner = lane >= {k} && lane < {WAVE - k} && j0 + lane - {k} < {n};",
+    ]
+    for c in range(C):
+        sc = f"(lane * {C} + {c})" if C > 1 else "lane"
+        lines += [
+            f"    int gj{c} = j0 - {k} + {sc};",
+            f"    gj{c} = gj{c} < 0 ? gj{c} + {n} : (gj{c} >= {n} ? gj{c} - {n} : gj{c});",
+            f"    const bool owner{c} = {sc} >= {k} && {sc} < {WAVE * C - k} && j0 + {sc} - {k} < {n};",
+        ]
+    lines += [
         "    /* Stores go through buffer descriptors spanning each output field: a",
-        "       lane that must not store gets an offset past the end, which the",
-        "       hardware drops, so no branch separates the stores from the loads",
-        "       (a branch would make the wait for each group's loads drain the",
-        "       previous group's stores). */",
+        "       column that must not be stored gets an offset past the end, which",
+        "       the hardware drops, so no branch separates the stores from the",
+        "       loads (a branch would make the wait for each group's loads drain",
+        "       the previous group's stores). */",
         f"    const __amdgpu_buffer_rsrc_t u_rs = __builtin_amdgcn_make_buffer_rsrc(u_out, (short)0, {n * n * 4}, PH_RSRC_WORD3);",
         f"    const __amdgpu_buffer_rsrc_t v_rs = __builtin_amdgcn_make_buffer_rsrc(v_out, (short)0, {n * n * 4}, PH_RSRC_WORD3);",
         "    /* Odd bands of strips walk up, even ones down: a band's last halo rows",
@@ -272,12 +289,14 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
         f"    const bool up = ((strip / {strips_j}u) & 1u) != 0u;",
         f"    const int base = up ? i0 + {rows - 1 + k + n} : i0 + {n - k};",
         "    const int dir = up ? -1 : 1;",
-        "    float " + ", ".join(f"pu{t}_{i} = 0.0f, pv{t}_{i} = 0.0f" for t in range(k) for i in (1, 2)) + ";",
+        "    float " + ", ".join(f"pu{t}_{i}_{c} = 0.0f, pv{t}_{i}_{c} = 0.0f"
+                                for t in range(k) for i in (1, 2) for c in range(C)) + ";",
     ]
     for g in range(group):
-        lines.append(f"    float qu{g}, qv{g};")
+        lines.append(f"    float " + ", ".join(f"qu{g}_{c}, qv{g}_{c}" for c in range(C)) + ";")
         lines.append(f"    {{ const int gi = (int)((unsigned int)(base + dir * {min(g, h - 1)}) % {n}u); "
-                     f"qu{g} = u_in[gi * {n} + gj]; qv{g} = v_in[gi * {n} + gj]; }}")
+                     + " ".join(f"qu{g}_{c} = u_in[gi * {n} + gj{c}]; qv{g}_{c} = v_in[gi * {n} + gj{c}];"
+                                for c in range(C)) + " }")
     lines += [f"    for (int r0 = 0; r0 < {groups * group}; r0 += {group}) {{"]
     # The next group's loads are unconditional (past the strip's end they
     # read its last row again, a cache hit): behind a branch, the wait for
@@ -285,25 +304,41 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
     for g in range(group):
         lines.append(f"        const int p{g} = r0 + {group + g} < {h - 1} ? r0 + {group + g} : {h - 1};")
         lines.append(f"        const int gi{g} = (int)((unsigned int)(base + dir * p{g}) % {n}u);")
-        lines.append(f"        const float nu{g} = u_in[gi{g} * {n} + gj], nv{g} = v_in[gi{g} * {n} + gj];")
+        for c in range(C):
+            lines.append(f"        const float nu{g}_{c} = u_in[gi{g} * {n} + gj{c}], nv{g}_{c} = v_in[gi{g} * {n} + gj{c}];")
     for g in range(group):
         lines.append(f"        {{ /* input row r0 + {g} */")
-        cur = (f"qu{g}", f"qv{g}")
+        cur = [(f"qu{g}_{c}", f"qv{g}_{c}") for c in range(C)]
         for t in range(k):
-            out = (f"yu{g}_{t}", f"yv{g}_{t}")
-            lines += ["            " + x for x in _reg_update(lit, (f"pu{t}_2", f"pv{t}_2"), (f"pu{t}_1", f"pv{t}_1"),
-                                                              cur, out, f"{g}_{t}")]
-            lines.append(f"            pu{t}_2 = pu{t}_1; pv{t}_2 = pv{t}_1; pu{t}_1 = {cur[0]}; pv{t}_1 = {cur[1]};")
-            cur = out
+            mid = [(f"pu{t}_1_{c}", f"pv{t}_1_{c}") for c in range(C)]
+            # the outer neighbours of the lane's edge columns, one rotation each
+            lines.append(f"            const float ru{g}_{t} = ph_from_right({mid[0][0]}), "
+                         f"rv{g}_{t} = ph_from_right({mid[0][1]});")
+            lines.append(f"            const float lu{g}_{t}_ = ph_from_left({mid[C - 1][0]}), "
+                         f"lv{g}_{t}_ = ph_from_left({mid[C - 1][1]});")
+            outs = []
+            for c in range(C):
+                left = mid[c - 1] if c > 0 else (f"lu{g}_{t}_", f"lv{g}_{t}_")
+                right = mid[c + 1] if c < C - 1 else (f"ru{g}_{t}", f"rv{g}_{t}")
+                out = (f"yu{g}_{t}_{c}", f"yv{g}_{t}_{c}")
+                lines += ["            " + x for x in _reg_update(lit, (f"pu{t}_2_{c}", f"pv{t}_2_{c}"), mid[c],
+                                                                  cur[c], left, right, out, f"{g}_{t}_{c}")]
+                outs.append(out)
+            for c in range(C):
+                lines.append(f"            pu{t}_2_{c} = pu{t}_1_{c}; pv{t}_2_{c} = pv{t}_1_{c}; "
+                             f"pu{t}_1_{c} = {cur[c][0]}; pv{t}_1_{c} = {cur[c][1]};")
+            cur = outs
         lines.append(f"            const int a = r0 + {g} - {2 * k};  /* output row, strip-relative */")
         lines.append(f"            const int ga = up ? i0 + {rows - 1} - a : i0 + a;  /* its grid row */")
-        lines.append(f"            const bool keep = owner && a >= 0 && a < {rows} && ga < {n};")
-        lines.append(f"            const int off = keep ? (ga * {n} + (j0 + lane - {k})) * 4 : PH_DROP;")
-        lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[0]}), u_rs, off, 0, 0);")
-        lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[1]}), v_rs, off, 0, 0);")
+        lines.append(f"            const bool row_kept = a >= 0 && a < {rows} && ga < {n};")
+        for c in range(C):
+            sc = f"(lane * {C} + {c})" if C > 1 else "lane"
+            lines.append(f"            const int off{c} = (row_kept && owner{c}) ? (ga * {n} + (j0 + {sc} - {k})) * 4 : PH_DROP;")
+            lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[c][0]}), u_rs, off{c}, 0, 0);")
+            lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[c][1]}), v_rs, off{c}, 0, 0);")
         lines.append("        }")
     for g in range(group):
-        lines.append(f"        qu{g} = nu{g}; qv{g} = nv{g};")
+        lines.append("        " + " ".join(f"qu{g}_{c} = nu{g}_{c}; qv{g}_{c} = nv{g}_{c};" for c in range(C)))
     lines += ["    }", "}", ""]
     return "\n".join(lines)
 
@@ -362,18 +397,21 @@ class RegisterGrayScott:
     group: int = 4
     math_mode: Any = "fast"
     cfg: Any = None
+    cols: int = 1
 
     def __post_init__(self) -> None:
         consts = _consts(self.cfg)
-        self._src = {kk: register_source(self.n, kk, self.rows, *consts, group=self.group) for kk in {self.k, 1}}
+        self._src = {kk: register_source(self.n, kk, self.rows, *consts, group=self.group, cols=self.cols)
+                     for kk in {self.k, 1}}
         self._kernels = {kk: rt.Kernel(src, "gray_scott_regs", self.math_mode) for kk, src in self._src.items()}
-        self._blocks = {kk: register_geometry(self.n, kk, self.rows)[1] for kk in self._src}
+        self._blocks = {kk: register_geometry(self.n, kk, self.rows, self.cols)[1] for kk in self._src}
 
     def blocks_for(self, k: int) -> int:
         return self._blocks[k]
 
     def describe(self) -> str:
-        return f"register pass: {self.rows}x{WAVE - 2 * self.k} strips, one wave each, rows in groups of {self.group}"
+        return (f"register pass: {self.rows}x{WAVE * self.cols - 2 * self.k} strips, one wave each, "
+                f"{self.cols} column(s) per lane, rows in groups of {self.group}")
 
     def source(self, k: int | None = None) -> str:
         return self._src[k or self.k]

@@ -16,6 +16,7 @@ pytestmark = pytest.mark.gpu
 KINDS = {
     "lds": lambda n, **kw: stencil.FusedGrayScott(n, **kw),
     "regs": lambda n, **kw: stencil.RegisterGrayScott(n, **kw),
+    "regs4": lambda n, **kw: stencil.RegisterGrayScott(n, k=4, rows=32, group=2, cols=4, **kw),
 }
 
 
@@ -35,12 +36,16 @@ def test_lds_safe_bit_exact_against_oracle(k, th, tw, single, steps):
 @pytest.mark.parametrize("n,k,rows,group", [(256, 6, 64, 4), (256, 4, 40, 8), (256, 8, 27, 3), (192, 1, 64, 8), (80, 3, 22, 5),
                                             (64, 12, 16, 8)])
 @pytest.mark.parametrize("steps", [12, 13])
-def test_regs_safe_bit_exact_against_oracle(n, k, rows, group, steps):
+@pytest.mark.parametrize("cols", [1, 2])
+def test_regs_safe_bit_exact_against_oracle(n, k, rows, group, steps, cols):
     """Strips that divide the grid and strips that do not (the last strip of
-    a column or row reaches past the grid), K from 1 to 12."""
-    print(f"[stencil] regs safe n={n} k={k} rows={rows} group={group} steps={steps}", flush=True)
+    a column or row reaches past the grid), K from 1 to 12, one and two
+    columns per lane."""
+    if n < 64 * cols:
+        pytest.skip("grid narrower than one wave of this many columns per lane")
+    print(f"[stencil] regs safe n={n} k={k} rows={rows} group={group} steps={steps} cols={cols}", flush=True)
     u0, v0 = gray_scott_initial(n)
-    f = stencil.RegisterGrayScott(n, k, rows, group, math_mode="safe")
+    f = stencil.RegisterGrayScott(n, k, rows, group, math_mode="safe", cols=cols)
     u, v, _ = stencil.gray_scott_fused_run(f, u0, v0, steps)
     wu, wv = oracle.gray_scott(u0, v0, GS_CFG, steps)
     np.testing.assert_array_equal(u, wu)

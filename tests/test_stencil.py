@@ -90,25 +90,37 @@ def test_bad_tiles_are_refused():
         stencil.fused_source(4096, 9, 16, 64, 0.16, 0.08, 0.037, 0.097, 1.0)
 
 
-def _register_pass(u, v, k, rows, group, cfg):
-    """The register kernel's schedule, lane for lane: a wave's 64 lanes walk
-    down their columns (up, in odd bands of strips), each step keeping two rows of the step before, the
-    left/right neighbours rotated in across the whole wave (np.roll), the
-    windows starting at zero, row indices wrapping, and only owner lanes
-    and rows K .. K + rows - 1 of step K stored."""
+def _register_pass(u, v, k, rows, group, cfg, cols=1):
+    """The register kernel's schedule, lane for lane: a wave's 64 lanes of
+    `cols` columns each walk down their columns (up, in odd bands of
+    strips), each step keeping two rows of the step before; a column's
+    inner neighbours are its lane's own columns and the lane's outer ones
+    come from the adjacent lanes rotated across the whole wave (np.roll),
+    the windows start at zero, row and column indices wrap, and only owner
+    columns and rows K .. K + rows - 1 of step K are stored."""
     du, dv, f, fk, dt = (F(x) for x in (cfg.du, cfg.dv, cfg.f, cfg.f + cfg.k, cfg.dt))
     n = u.shape[0]
-    w = 64 - 2 * k
+    C = cols
+    w = 64 * C - 2 * k
     h = rows + 2 * k
     total = -(-h // group) * group
     uo, vo = np.full_like(u, np.nan), np.full_like(v, np.nan)
-    lane = np.arange(64)
+    sc = np.arange(64 * C).reshape(64, C)          # strip column of lane l, column c
     for band, i0 in enumerate(range(0, n, rows)):
         up = band % 2 == 1  # odd bands walk up the grid
         for j0 in range(0, -(-n // w) * w, w):
-            gj = (j0 - k + lane) % n
-            owner = (lane >= k) & (lane < 64 - k) & (j0 + lane - k < n)
-            win = [[np.zeros(64, F) for _ in range(4)] for _ in range(k)]  # pu2, pu1, pv2, pv1
+            gj = (j0 - k + sc) % n
+            owner = (sc >= k) & (sc < 64 * C - k) & (j0 + sc - k < n)
+            win = [[np.zeros((64, C), F) for _ in range(4)] for _ in range(k)]  # pu2, pu1, pv2, pv1
+
+            def neighbours(x):
+                """(right, left) of every column of (64, C) values x."""
+                right, left = np.empty_like(x), np.empty_like(x)
+                right[:, :-1], left[:, 1:] = x[:, 1:], x[:, :-1]
+                right[:, -1] = np.roll(x[:, 0], -1)
+                left[:, 0] = np.roll(x[:, -1], 1)
+                return right, left
+
             for r in range(total):
                 p = min(r, h - 1)  # past the strip's end: its last row again
                 gi = (i0 + rows - 1 + k - p) % n if up else (i0 - k + p) % n
@@ -116,13 +128,15 @@ def _register_pass(u, v, k, rows, group, cfg):
                 for t in range(k):
                     pu2, pu1, pv2, pv1 = win[t]
                     with np.errstate(all="ignore"):
+                        ru, lu_ = neighbours(pu1)
+                        rv, lv_ = neighbours(pv1)
                         lu = cu + pu2
-                        lu = lu + np.roll(pu1, -1)
-                        lu = lu + np.roll(pu1, 1)
+                        lu = lu + ru
+                        lu = lu + lu_
                         lu = lu - F(4.0) * pu1
                         lv = cv + pv2
-                        lv = lv + np.roll(pv1, -1)
-                        lv = lv + np.roll(pv1, 1)
+                        lv = lv + rv
+                        lv = lv + lv_
                         lv = lv - F(4.0) * pv1
                         uvv = (pu1 * pv1) * pv1
                         a = du * lu
@@ -137,10 +151,10 @@ def _register_pass(u, v, k, rows, group, cfg):
                 a_row = r - 2 * k
                 ga = i0 + rows - 1 - a_row if up else i0 + a_row
                 if 0 <= a_row < rows and ga < n:
-                    cols = j0 + lane[owner] - k
-                    assert np.all(np.isnan(uo[ga, cols])), "a cell stored twice"
-                    uo[ga, cols] = cu[owner]
-                    vo[ga, cols] = cv[owner]
+                    cols_g = j0 + sc[owner] - k
+                    assert np.all(np.isnan(uo[ga, cols_g])), "a cell stored twice"
+                    uo[ga, cols_g] = cu[owner]
+                    vo[ga, cols_g] = cv[owner]
     assert not np.isnan(uo).any() and not np.isnan(vo).any(), "a cell never stored"
     return uo, vo
 
@@ -153,6 +167,18 @@ def test_register_schedule_restated_matches_oracle(n, k, rows, group, steps):
     u, v = u0.copy(), v0.copy()
     for kk in [k] * (steps // k) + [1] * (steps % k):
         u, v = _register_pass(u, v, kk, rows, group, GS_CFG)
+    wu, wv = oracle.gray_scott(u0, v0, GS_CFG, steps)
+    np.testing.assert_array_equal(u, wu)
+    np.testing.assert_array_equal(v, wv)
+
+
+@pytest.mark.parametrize("n,k,rows,group,steps,cols", [(128, 4, 24, 4, 9, 2), (160, 6, 32, 4, 13, 2),
+                                                        (256, 3, 40, 2, 7, 4), (128, 1, 64, 8, 2, 2)])
+def test_register_schedule_with_several_columns_per_lane(n, k, rows, group, steps, cols):
+    u0, v0 = gray_scott_initial(n)
+    u, v = u0.copy(), v0.copy()
+    for kk in [k] * (steps // k) + [1] * (steps % k):
+        u, v = _register_pass(u, v, kk, rows, group, GS_CFG, cols)
     wu, wv = oracle.gray_scott(u0, v0, GS_CFG, steps)
     np.testing.assert_array_equal(u, wu)
     np.testing.assert_array_equal(v, wv)
@@ -175,3 +201,5 @@ def test_register_bad_shapes_are_refused():
         stencil.register_source(4096, 32, 64, 0.16, 0.08, 0.037, 0.097, 1.0)
     with pytest.raises(ValueError, match="too small"):
         stencil.register_source(32, 2, 16, 0.16, 0.08, 0.037, 0.097, 1.0)
+    with pytest.raises(ValueError, match="too small"):
+        stencil.register_source(96, 2, 16, 0.16, 0.08, 0.037, 0.097, 1.0, cols=2)
