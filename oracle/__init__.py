@@ -103,6 +103,8 @@ def _declare_more(L):
     L.oracle_gbm.argtypes = [l, l, l, u, u, f, f, f, f, f, _F]
     L.oracle_pow.argtypes = [f, f]
     L.oracle_pow.restype = f
+    L.oracle_pow_log_many.argtypes = [l, _F, ctypes.POINTER(ctypes.c_double)]
+    L.oracle_pow_log_many.restype = None
     L.oracle_bs3_vdp.argtypes = [l, _F, _F, _F, f, f, f, f, l, _F, _F, _F, _I, _I]
     L.oracle_gray_scott_step.argtypes = [l, _F, _F, f, f, f, f, f, _F, _F]
     L.oracle_gray_scott.argtypes = [l, l, _F, _F, _F, _F, f, f, f, f, f]
@@ -132,6 +134,14 @@ def gbm(cfg, n_paths: int, first_path: int = 0) -> np.ndarray:
 
 def pow32(x: float, y: float) -> np.float32:
     return np.float32(_lib2().oracle_pow(float(x), float(y)))
+
+
+def pow_log(x: np.ndarray) -> np.ndarray:
+    """The double log2 the deterministic pow takes of each float base."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.size, np.float64)
+    _lib2().oracle_pow_log_many(x.size, _fp(x), out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    return out
 
 
 def bs3_vdp(x0, v0, mu, cfg):

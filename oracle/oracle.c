@@ -174,7 +174,9 @@ static double ph_log2_pos(double x) {
   int e;
   double m = frexp(x, &e);
   if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
-  double t = (m - 1.0) / (m + 1.0);
+  /* (m - 1) times the correctly rounded reciprocal of m + 1: the device
+     reaches the same reciprocal by Newton steps (emit/prelude.py). */
+  double t = (m - 1.0) * (1.0 / (m + 1.0));
   double t2 = t * t;
   /* sum_{k=0..7} 2 t2^k / ((2k+1) ln 2) by Horner's rule (one constant per
      FMA, so no constant needs a register move first). |t| <= 0.1716, so the
@@ -205,6 +207,17 @@ static double ph_exp2_dbl(double z) {
   p = fma(p, r, 0.6931471805599453);
   p = fma(p, r, 1.0);
   return ldexp(p, (int)kd);
+}
+
+/* ph_pow's base-only part (palladium_amd/emit/prelude.py:ph_pow_log):
+   log2 |x| for a finite nonzero x, 0 otherwise. */
+double oracle_pow_log(float x) {
+  float ax = fabsf(x);
+  return ph_log2_pos((double)((ax > 0.0f && ax < INFINITY) ? ax : 1.0f));
+}
+
+void oracle_pow_log_many(long n, const float *x, double *out) {
+  for (long i = 0; i < n; ++i) out[i] = oracle_pow_log(x[i]);
 }
 
 float oracle_pow(float x, float y) {

@@ -12,7 +12,7 @@
   it is the device `powf`; under FAST, 2^(y log2 x) on the hardware base-2
   transcendentals for positive normal bases (powf otherwise).
   Method, in base 2: x = m * 2^e with m in [sqrt(1/2), sqrt(2));
-  log2 m = (2/ln 2) atanh(t), t = (m-1)/(m+1), as an odd series in t;
+  log2 m = (2/ln 2) atanh(t), t = (m-1) RN(1/(m+1)), as an odd series in t;
   2^z by z = k + r, |r| <= 1/2, and a degree-10 polynomial in r; both
   carried in double, so the float result is the double value rounded once
   (correctly rounded on every sampled argument).
@@ -116,13 +116,27 @@ __device__ __forceinline__ double ph_fma_k(double a, double b, double c) {
 }
 
 /* log2 of a positive finite double: x = m 2^e with m in [sqrt(1/2), sqrt(2)),
-   log2 m = (2 / ln 2) atanh(t), t = (m - 1) / (m + 1), as an odd series in t
+   log2 m = (2 / ln 2) atanh(t), t = (m - 1) RN(1 / (m + 1)), as an odd series in t
    whose coefficients carry the 2 / ln 2; log2 x = e + t P(t^2), one FMA. */
 __device__ __forceinline__ double ph_log2_pos(double x) {
     int e;
     double m = frexp(x, &e);          /* x = m 2^e, m in [0.5, 1) */
     if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
-    double t = (m - 1.0) / (m + 1.0);
+    /* t = (m - 1) RN(1 / (m + 1)), the reciprocal without a division. x is a
+       float, so d = m + 1 in [1.707, 2.414) has at most 25 significant bits.
+       From the hardware float reciprocal (relative error below 2^-22) two
+       Newton steps r + r (1 - d r), each two correctly rounded FMAs, leave
+       r within 2^-88 of 1 / d; 1 / d is never within 2^-79 of a midpoint
+       between doubles (1 - d * midpoint is a nonzero integer over 2^79 at
+       most), so r is RN(1 / d) exactly, the value the host oracle gets from
+       1.0 / d. */
+    double d = m + 1.0;
+    double r = (double)__builtin_amdgcn_rcpf((float)d);
+    double q = fma(-d, r, 1.0);
+    r = fma(r, q, r);
+    q = fma(-d, r, 1.0);
+    r = fma(r, q, r);
+    double t = (m - 1.0) * r;
     double t2 = t * t;
     /* sum_{k=0..7} 2 t2^k / ((2k+1) ln 2) by Horner's rule (one constant per
        FMA, so no constant needs a register move first). |t| <= 0.1716, so the
