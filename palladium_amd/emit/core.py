@@ -502,6 +502,7 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
 
     body = plan.jaxpr if plan else spec.jaxpr
     from palladium_amd.emit.compact import plan_for
+    from palladium_amd.emit.optimize import funnel_shifts
 
     if math_mode is not None and math_mode_ordinal(math_mode) == 2:
         from palladium_amd.emit.optimize import fast_rewrites
@@ -515,6 +516,8 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         # The extra carries must not cost the loop its compaction.
         if not (plan is None and geo.block == 1024) or plan_for(spec, shared, lanes, block) is not None:
             body = shared
+    # Exact, every mode; after the rewrites that read the or-and-shift form.
+    body = funnel_shifts(body)
 
     cplan = plan_for(spec, body, lanes, block)
     if (cplan is not None) != (plan is None and geo.block == 1024 and plan_for(spec, spec.jaxpr, lanes, block) is not None):

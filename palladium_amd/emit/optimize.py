@@ -45,8 +45,8 @@ import numpy as np
 
 from palladium_amd.ir import ClosedJaxpr, Jaxpr, JaxprEqn, Literal, ShapedArray, Var, primitive
 
-__all__ = ["carry_logs", "drop_redundant_clamps", "factor_common_products", "fast_rewrites", "power_laws_to_exp2",
-           "share_pow_logs"]
+__all__ = ["carry_logs", "drop_redundant_clamps", "factor_common_products", "fast_rewrites", "funnel_shifts",
+           "power_laws_to_exp2", "share_pow_logs"]
 
 
 def _same(a: Any, b: Any) -> bool:
@@ -570,4 +570,61 @@ def _carry_logs_while(e: JaxprEqn, used_after: set) -> tuple[list[JaxprEqn], Jax
     for k, *_ in plans:
         outs[k] = Var(ShapedArray(outs[k].aval.shape, np.float32))  # no longer the carry's value
     return pre, JaxprEqn(inits, outs, e.primitive, params)
+
+
+def funnel_shifts(jaxpr: Jaxpr) -> Jaxpr:
+    """Exact, every math mode: `or(shift_right_logical(x, n), C)` for a
+    32-bit integer literal C whose low 32 - n bits are zero is
+    `alignbit(C >> (32 - n), x, n)`, the low word of the 64-bit pair
+    (C >> (32 - n), x) shifted right by n: one `v_alignbit_b32` where the
+    compiler emits a shift and an or. `jax.random.uniform`'s float
+    construction `bits >> 9 | 0x3F800000` (the reference's staged ops,
+    `tests/test_10_random_bits.py:42-54`) is this form."""
+    producer = {ov: e for e in jaxpr.eqns for ov in e.outvars}
+
+    def const(v: Any) -> int | None:
+        """The integer value of a scalar literal, or of a broadcast of one."""
+        for _ in range(4):
+            if isinstance(v, Literal):
+                return int(np.asarray(v.val).astype(np.int64)) if np.ndim(v.val) == 0 else None
+            e = producer.get(v) if isinstance(v, Var) else None
+            if e is None or e.primitive.name != "broadcast_in_dim":
+                return None
+            v = e.invars[0]
+        return None
+
+    new_eqns: list[JaxprEqn] = []
+    for e in jaxpr.eqns:
+        params = {k: _rewrite_sub(v, funnel_shifts) for k, v in e.params.items()}
+        e = JaxprEqn(e.invars, e.outvars, e.primitive, params)
+        if e.primitive.name == "or" and len(e.invars) == 2:
+            out = e.outvars[0]
+            dt = np.dtype(out.aval.dtype)
+            for sv, cv in (e.invars, e.invars[::-1]):
+                sh = producer.get(sv) if isinstance(sv, Var) else None
+                cval = const(cv)
+                if (dt not in (np.uint32, np.int32) or cval is None or sh is None
+                        or sh.primitive.name != "shift_right_logical" or const(sh.invars[1]) is None):
+                    continue
+                n = const(sh.invars[1])
+                c = cval & 0xFFFFFFFF
+                x = sh.invars[0]
+                if not (0 < n < 32) or c & ((1 << (32 - n)) - 1) or np.dtype(x.aval.dtype) != dt \
+                        or tuple(x.aval.shape) != tuple(out.aval.shape):
+                    continue
+                hi = Literal(np.uint32(c >> (32 - n)), ShapedArray((), np.uint32))
+                amt = Literal(np.uint32(n), ShapedArray((), np.uint32))
+                if dt == np.uint32:
+                    new_eqns.append(JaxprEqn([hi, x, amt], [out], primitive("alignbit"), {}))
+                else:
+                    xu, ru = Var(ShapedArray(x.aval.shape, np.uint32)), Var(ShapedArray(x.aval.shape, np.uint32))
+                    new_eqns.append(JaxprEqn([x], [xu], primitive("bitcast_convert_type"), {"new_dtype": np.dtype(np.uint32)}))
+                    new_eqns.append(JaxprEqn([hi, xu, amt], [ru], primitive("alignbit"), {}))
+                    new_eqns.append(JaxprEqn([ru], [out], primitive("bitcast_convert_type"), {"new_dtype": dt}))
+                break
+            else:
+                new_eqns.append(e)
+            continue
+        new_eqns.append(e)
+    return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)
 

@@ -87,6 +87,8 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
         return "ph_fmax({a}, {b})" if f else "(({a} > {b}) ? {a} : {b})"
     if opname == "pow":
         return "ph_pow({a}, {b})"
+    if opname == "alignbit":
+        return "__builtin_amdgcn_alignbit({a}, {b}, {c})"
     if opname == "pow_log":
         return "ph_pow_log({a})"
     if opname == "pow_with_log":
@@ -259,7 +261,7 @@ def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
 
 
 for _name in [*ELEMENTWISE, "integer_pow", "convert_element_type", "bitcast_convert_type", "select_n",
-              "pow_log", "pow_with_log"]:
+              "pow_log", "pow_with_log", "alignbit"]:
     RULES[_name] = _rule_elementwise
 
 

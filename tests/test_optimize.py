@@ -344,3 +344,42 @@ def test_carry_read_elsewhere_is_kept(read_after):
     j = power_laws_to_exp2(spec.jaxpr)
     assert _count(j, "log2") == 2 and _count(j, "eq") == 0   # c and v proven non-negative: no guards
     assert (carry_logs(j).eqns == j.eqns) == read_after
+
+
+def _funnel_kernel(n, c, signed):
+    def kernel(x_ref, o_ref):
+        x = x_ref[...]
+        o_ref[...] = lax.shift_right_logical(x, jnp.asarray(n, x.dtype)) | jnp.asarray(c, x.dtype)
+    return kernel
+
+
+def _funnel_spec(n, c, signed, size=256):
+    dt = np.int32 if signed else np.uint32
+    x = np.random.default_rng(n).integers(0, 2 ** 32, size, dtype=np.uint64).astype(np.uint32).view(dt)
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    call = pl.pallas_call(_funnel_kernel(n, np.uint32(c).view(dt), signed), grid=(size,), in_specs=[s], out_specs=s,
+                          out_shape=pl.ShapeDtypeStruct((size,), dt))
+    return trace(call, x), x
+
+
+@pytest.mark.parametrize("n,c,signed,rewritten", [
+    (9, 0x3F800000, False, True),          # jax.random.uniform's float32 construction
+    (9, 0x3F800000, True, True),
+    (20, 0xABC00000, False, True),
+    (9, 0x3F800001, False, False),         # a bit below the shifted field: not a funnel shift
+    (1, 0x80000000, True, True),
+])
+def test_or_of_a_logical_shift_becomes_alignbit(n, c, signed, rewritten):
+    from palladium_amd.emit.optimize import funnel_shifts
+
+    spec, x = _funnel_spec(n, c, signed)
+    opt = funnel_shifts(spec.jaxpr)
+    assert (_count(opt, "alignbit") == 1) == rewritten
+    if rewritten:
+        (e,) = [q for q in opt.eqns if q.primitive.name == "alignbit"]
+        hi, amt = int(e.invars[0].val), int(e.invars[2].val)
+        xu = x.view(np.uint32).astype(np.uint64)
+        # alignbit(hi, lo, s) = low word of ((hi << 32) | lo) >> s
+        got = (((np.uint64(hi) << np.uint64(32)) | xu) >> np.uint64(amt)) & np.uint64(0xFFFFFFFF)
+        want = (xu >> np.uint64(n)) | np.uint64(c)
+        np.testing.assert_array_equal(got, want)
