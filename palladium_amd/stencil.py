@@ -244,9 +244,14 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
     per, rem = divmod(blocks, NUM_XCDS)
     lit = {name: format_float(v) for name, v in (("DU", du), ("DV", dv), ("F", f), ("FK", fk), ("DT", dt))}
     C = cols
+    # With K and n multiples of C, a lane's C columns start at a multiple of
+    # C: contiguous, aligned, never split by the periodic wrap or an edge of
+    # the grid or the strip, so each row moves as one C-wide access.
+    vec = C in (2, 4) and k % C == 0 and n % C == 0
     lines = [
         f"// Gray-Scott, {k} steps per pass in registers, {rows}x{w} strips, {C} columns per lane, "
         f"{n}x{n} periodic grid.",
+        f"typedef unsigned int ph_u32x{C} __attribute__((ext_vector_type({C})));" if vec else "",
         "#define PH_RSRC_WORD3 0x00020000  /* gfx9 buffer descriptor word 3: 32-bit elements, raw */",
         "#define PH_DROP ((int)0x80000000)  /* an offset past every field: the store is dropped */",
         "static __device__ __forceinline__ float ph_from_right(float x) {",
@@ -292,11 +297,24 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
         "    float " + ", ".join(f"pu{t}_{i}_{c} = 0.0f, pv{t}_{i}_{c} = 0.0f"
                                 for t in range(k) for i in (1, 2) for c in range(C)) + ";",
     ]
+    vt = f"float{C}" if vec else None
+    comps = "xyzw"
+
+    def load_row(dst_u: str, dst_v: str, gi: str, decl: str) -> list[str]:
+        """Lines loading grid row `gi` of this lane's columns into dst_u{c}, dst_v{c}."""
+        if vec:
+            out = [f"{{ const {vt} _u = *(const {vt}*)(u_in + {gi} * {n} + gj0), "
+                   f"_v = *(const {vt}*)(v_in + {gi} * {n} + gj0);"]
+            out += [f"  {dst_u}{c} = _u.{comps[c]}; {dst_v}{c} = _v.{comps[c]};" for c in range(C)]
+            return out + ["}"]
+        return [" ".join(f"{dst_u}{c} = u_in[{gi} * {n} + gj{c}]; {dst_v}{c} = v_in[{gi} * {n} + gj{c}];"
+                         for c in range(C))]
+
     for g in range(group):
         lines.append(f"    float " + ", ".join(f"qu{g}_{c}, qv{g}_{c}" for c in range(C)) + ";")
-        lines.append(f"    {{ const int gi = (int)((unsigned int)(base + dir * {min(g, h - 1)}) % {n}u); "
-                     + " ".join(f"qu{g}_{c} = u_in[gi * {n} + gj{c}]; qv{g}_{c} = v_in[gi * {n} + gj{c}];"
-                                for c in range(C)) + " }")
+        lines.append(f"    {{ const int gi = (int)((unsigned int)(base + dir * {min(g, h - 1)}) % {n}u);")
+        lines += ["        " + x for x in load_row(f"qu{g}_", f"qv{g}_", "gi", "")]
+        lines.append("    }")
     lines += [f"    for (int r0 = 0; r0 < {groups * group}; r0 += {group}) {{"]
     # The next group's loads are unconditional (past the strip's end they
     # read its last row again, a cache hit): behind a branch, the wait for
@@ -304,8 +322,8 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
     for g in range(group):
         lines.append(f"        const int p{g} = r0 + {group + g} < {h - 1} ? r0 + {group + g} : {h - 1};")
         lines.append(f"        const int gi{g} = (int)((unsigned int)(base + dir * p{g}) % {n}u);")
-        for c in range(C):
-            lines.append(f"        const float nu{g}_{c} = u_in[gi{g} * {n} + gj{c}], nv{g}_{c} = v_in[gi{g} * {n} + gj{c}];")
+        lines.append("        float " + ", ".join(f"nu{g}_{c}, nv{g}_{c}" for c in range(C)) + ";")
+        lines += ["        " + x for x in load_row(f"nu{g}_", f"nv{g}_", f"gi{g}", "")]
     for g in range(group):
         lines.append(f"        {{ /* input row r0 + {g} */")
         cur = [(f"qu{g}_{c}", f"qv{g}_{c}") for c in range(C)]
@@ -331,11 +349,19 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
         lines.append(f"            const int a = r0 + {g} - {2 * k};  /* output row, strip-relative */")
         lines.append(f"            const int ga = up ? i0 + {rows - 1} - a : i0 + a;  /* its grid row */")
         lines.append(f"            const bool row_kept = a >= 0 && a < {rows} && ga < {n};")
-        for c in range(C):
-            sc = f"(lane * {C} + {c})" if C > 1 else "lane"
-            lines.append(f"            const int off{c} = (row_kept && owner{c}) ? (ga * {n} + (j0 + {sc} - {k})) * 4 : PH_DROP;")
-            lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[c][0]}), u_rs, off{c}, 0, 0);")
-            lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[c][1]}), v_rs, off{c}, 0, 0);")
+        if vec:
+            # one owner flag for the lane: its columns are all in or all out
+            sc = f"(lane * {C})"
+            lines.append(f"            const int off = (row_kept && owner0) ? (ga * {n} + (j0 + {sc} - {k})) * 4 : PH_DROP;")
+            for i, rs in ((0, "u_rs"), (1, "v_rs")):
+                vals = ", ".join(f"__float_as_uint({cur[c][i]})" for c in range(C))
+                lines.append(f"            __builtin_amdgcn_raw_buffer_store_b{32 * C}((ph_u32x{C}){{{vals}}}, {rs}, off, 0, 0);")
+        else:
+            for c in range(C):
+                sc = f"(lane * {C} + {c})" if C > 1 else "lane"
+                lines.append(f"            const int off{c} = (row_kept && owner{c}) ? (ga * {n} + (j0 + {sc} - {k})) * 4 : PH_DROP;")
+                lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[c][0]}), u_rs, off{c}, 0, 0);")
+                lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[c][1]}), v_rs, off{c}, 0, 0);")
         lines.append("        }")
     for g in range(group):
         lines.append("        " + " ".join(f"qu{g}_{c} = nu{g}_{c}; qv{g}_{c} = nv{g}_{c};" for c in range(C)))
