@@ -641,6 +641,28 @@ def bench_gs_fused(steps: int, warmup: int, cpu: bool) -> dict:
                                 "overlaps its arithmetic, not by HBM bandwidth: alone, its arithmetic takes 50 us "
                                 "and its loads and stores 43 us of a 76 us pass. effective_per_step_GBps prices "
                                 "each step at the per-step kernel's 16 B/cell, traffic this kernel does not make")}
+    if kind == "regs":
+        # VALU issue over the whole graph: each launch's loop-iteration slots
+        # (this build's ISA, measured per-instruction costs) times its
+        # lane-iterations (waves x 64 x row groups), against the sustained
+        # FMA issue rate.
+        from palladium_amd import isa
+        from palladium_amd import runtime as rt
+
+        rates = valu_costs()
+        total, per = 0.0, {}
+        for kk in set(fused.launches(n_steps)):
+            code = rt.compile_code_object(fused.source(kk), "gray_scott_regs", "fast")
+            slots, _ = isa.issue_slots(code, rates["relative_cost_vs_fma"])
+            waves = stencil.register_geometry(cfg.size, kk, fused.rows, fused.cols)[0]
+            iters = waves * 64 * -(-(fused.rows + 2 * kk) // fused.group)
+            count = fused.launches(n_steps).count(kk)
+            per[kk] = {"slots_per_iteration": slots, "lane_iterations_per_launch": iters, "launches": count}
+            total += slots * iters * count
+        sustained = rates["sustained_fma_tflops"] * 1e12 / 2
+        res["roofline"]["issue"] = {"per_kernel": per, "achieved_slots_per_s": total / gpu_s,
+                                    "sustained_fma_slots_per_s": sustained,
+                                    "frac_of_sustained_issue": total / gpu_s / sustained}
     res["pattern_energy"] = float(np.sum(v, dtype=np.float64))
     if cpu:
         import oracle
