@@ -33,16 +33,19 @@ def test_lds_safe_bit_exact_against_oracle(k, th, tw, single, steps):
     np.testing.assert_array_equal(v, wv)
 
 
-@pytest.mark.parametrize("n,k,rows,group", [(256, 6, 64, 4), (256, 4, 40, 8), (256, 8, 27, 3), (192, 1, 64, 8), (80, 3, 22, 5),
-                                            (64, 12, 16, 8)])
+_REGS_CASES = [(256, 6, 64, 4, 1), (256, 4, 40, 8, 1), (256, 8, 27, 3, 1), (192, 1, 64, 8, 1), (80, 3, 22, 5, 1),
+               (64, 12, 16, 8, 1),
+               # two and four columns per lane: 64-/128-bit rows (K, n multiples of the columns)
+               # and 32-bit ones (odd K), strips that divide the grid and ragged ones
+               (256, 6, 64, 4, 2), (192, 4, 40, 8, 2), (160, 3, 27, 3, 2), (128, 1, 64, 8, 2), (256, 8, 30, 2, 4)]
+
+
+@pytest.mark.parametrize("n,k,rows,group,cols", _REGS_CASES)
 @pytest.mark.parametrize("steps", [12, 13])
-@pytest.mark.parametrize("cols", [1, 2])
-def test_regs_safe_bit_exact_against_oracle(n, k, rows, group, steps, cols):
+def test_regs_safe_bit_exact_against_oracle(n, k, rows, group, cols, steps):
     """Strips that divide the grid and strips that do not (the last strip of
-    a column or row reaches past the grid), K from 1 to 12, one and two
-    columns per lane."""
-    if n < 64 * cols:
-        pytest.skip("grid narrower than one wave of this many columns per lane")
+    a column or row reaches past the grid), K from 1 to 12, one, two and
+    four columns per lane."""
     print(f"[stencil] regs safe n={n} k={k} rows={rows} group={group} steps={steps} cols={cols}", flush=True)
     u0, v0 = gray_scott_initial(n)
     f = stencil.RegisterGrayScott(n, k, rows, group, math_mode="safe", cols=cols)
