@@ -267,7 +267,10 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
         f"    const unsigned int xcd = blockIdx.x % {NUM_XCDS}u, slot = blockIdx.x / {NUM_XCDS}u;",
         f"    const unsigned int blk = (xcd < {rem}u) ? xcd * {per + 1}u + slot",
         f"                                           : {rem * (per + 1)}u + (xcd - {rem}u) * {per}u + slot;",
-        f"    const unsigned int strip = blk * {WORKGROUP // WAVE}u + threadIdx.x / {WAVE}u;",
+        "    /* The strip, and with it every row index, is the same for all lanes",
+        "       of a wave; readfirstlane lets the compiler keep them in scalar",
+        "       registers. */",
+        f"    const unsigned int strip = __builtin_amdgcn_readfirstlane(blk * {WORKGROUP // WAVE}u + threadIdx.x / {WAVE}u);",
         f"    if (strip >= {waves}u) return;  /* whole waves only */",
         f"    const int lane = (int)(threadIdx.x % {WAVE}u);",
         f"    const int i0 = (int)(strip / {strips_j}u) * {rows};",
