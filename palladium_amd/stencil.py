@@ -284,13 +284,25 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
             f"    const bool owner{c} = {sc} >= {k} && {sc} < {WAVE * C - k} && j0 + {sc} - {k} < {n};",
         ]
     lines += [
-        "    /* Stores go through buffer descriptors spanning each output field: a",
-        "       column that must not be stored gets an offset past the end, which",
-        "       the hardware drops, so no branch separates the stores from the",
-        "       loads (a branch would make the wait for each group's loads drain",
-        "       the previous group's stores). */",
-        f"    const __amdgpu_buffer_rsrc_t u_rs = __builtin_amdgcn_make_buffer_rsrc(u_out, (short)0, {n * n * 4}, PH_RSRC_WORD3);",
-        f"    const __amdgpu_buffer_rsrc_t v_rs = __builtin_amdgcn_make_buffer_rsrc(v_out, (short)0, {n * n * 4}, PH_RSRC_WORD3);",
+        "    /* Memory goes through buffer descriptors. A lane's column offset is",
+        "       fixed for the whole walk (vector register); the row is a scalar",
+        "       offset (loads) or the base of a per-row descriptor (stores), so",
+        "       no per-row address arithmetic runs on the VALU. A column that must",
+        "       not be stored has an offset past the end and a row that must not",
+        "       be stored a descriptor of no bytes: the hardware drops those",
+        "       stores, so no branch separates the stores from the loads (a",
+        "       branch would make the wait for each group's loads drain the",
+        "       previous group's stores). */",
+        f"    const __amdgpu_buffer_rsrc_t u_src = __builtin_amdgcn_make_buffer_rsrc((void*)u_in, (short)0, {n * n * 4}, PH_RSRC_WORD3);",
+        f"    const __amdgpu_buffer_rsrc_t v_src = __builtin_amdgcn_make_buffer_rsrc((void*)v_in, (short)0, {n * n * 4}, PH_RSRC_WORD3);",
+    ]
+    for c in (range(1) if vec else range(C)):
+        sc = f"(lane * {C} + {c})" if C > 1 else "lane"
+        lines += [
+            f"    const int lo{c} = gj{c} * 4;  /* load column offset */",
+            f"    const int so{c} = owner{c} ? (j0 + {sc} - {k}) * 4 : PH_DROP;  /* store column offset */",
+        ]
+    lines += [
         "    /* Odd bands of strips walk up, even ones down: a band's last halo rows",
         "       are then read at about the time the next band reads them too, which",
         "       keeps them in L2. Pipeline row p is grid row (base + dir * p) % n. */",
@@ -305,12 +317,15 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
 
     def load_row(dst_u: str, dst_v: str, gi: str, decl: str) -> list[str]:
         """Lines loading grid row `gi` of this lane's columns into dst_u{c}, dst_v{c}."""
+        row = f"({gi}) * {4 * n}"
         if vec:
-            out = [f"{{ const {vt} _u = *(const {vt}*)(u_in + {gi} * {n} + gj0), "
-                   f"_v = *(const {vt}*)(v_in + {gi} * {n} + gj0);"]
-            out += [f"  {dst_u}{c} = _u.{comps[c]}; {dst_v}{c} = _v.{comps[c]};" for c in range(C)]
+            out = [f"{{ const ph_u32x{C} _u = __builtin_amdgcn_raw_buffer_load_b{32 * C}(u_src, lo0, {row}, 0), "
+                   f"_v = __builtin_amdgcn_raw_buffer_load_b{32 * C}(v_src, lo0, {row}, 0);"]
+            out += [f"  {dst_u}{c} = __uint_as_float(_u.{comps[c]}); {dst_v}{c} = __uint_as_float(_v.{comps[c]});"
+                    for c in range(C)]
             return out + ["}"]
-        return [" ".join(f"{dst_u}{c} = u_in[{gi} * {n} + gj{c}]; {dst_v}{c} = v_in[{gi} * {n} + gj{c}];"
+        return [" ".join(f"{dst_u}{c} = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(u_src, lo{c}, {row}, 0)); "
+                         f"{dst_v}{c} = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(v_src, lo{c}, {row}, 0));"
                          for c in range(C))]
 
     for g in range(group):
@@ -352,19 +367,21 @@ def register_source(n: int, k: int, rows: int, du: float, dv: float, f: float, f
         lines.append(f"            const int a = r0 + {g} - {2 * k};  /* output row, strip-relative */")
         lines.append(f"            const int ga = up ? i0 + {rows - 1} - a : i0 + a;  /* its grid row */")
         lines.append(f"            const bool row_kept = a >= 0 && a < {rows} && ga < {n};")
+        lines.append(f"            const int row_at = row_kept ? ga * {n} : 0;")
+        lines.append(f"            const int row_bytes = row_kept ? {4 * n} : 0;")
+        lines.append("            const __amdgpu_buffer_rsrc_t u_row = __builtin_amdgcn_make_buffer_rsrc("
+                     "u_out + row_at, (short)0, row_bytes, PH_RSRC_WORD3);")
+        lines.append("            const __amdgpu_buffer_rsrc_t v_row = __builtin_amdgcn_make_buffer_rsrc("
+                     "v_out + row_at, (short)0, row_bytes, PH_RSRC_WORD3);")
         if vec:
             # one owner flag for the lane: its columns are all in or all out
-            sc = f"(lane * {C})"
-            lines.append(f"            const int off = (row_kept && owner0) ? (ga * {n} + (j0 + {sc} - {k})) * 4 : PH_DROP;")
-            for i, rs in ((0, "u_rs"), (1, "v_rs")):
+            for i, rs in ((0, "u_row"), (1, "v_row")):
                 vals = ", ".join(f"__float_as_uint({cur[c][i]})" for c in range(C))
-                lines.append(f"            __builtin_amdgcn_raw_buffer_store_b{32 * C}((ph_u32x{C}){{{vals}}}, {rs}, off, 0, 0);")
+                lines.append(f"            __builtin_amdgcn_raw_buffer_store_b{32 * C}((ph_u32x{C}){{{vals}}}, {rs}, so0, 0, 0);")
         else:
             for c in range(C):
-                sc = f"(lane * {C} + {c})" if C > 1 else "lane"
-                lines.append(f"            const int off{c} = (row_kept && owner{c}) ? (ga * {n} + (j0 + {sc} - {k})) * 4 : PH_DROP;")
-                lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[c][0]}), u_rs, off{c}, 0, 0);")
-                lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[c][1]}), v_rs, off{c}, 0, 0);")
+                lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[c][0]}), u_row, so{c}, 0, 0);")
+                lines.append(f"            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint({cur[c][1]}), v_row, so{c}, 0, 0);")
         lines.append("        }")
     for g in range(group):
         lines.append("        " + " ".join(f"qu{g}_{c} = nu{g}_{c}; qv{g}_{c} = nv{g}_{c};" for c in range(C)))
