@@ -4,8 +4,10 @@
  * with gcc against include/palladium_hip.h only.
  *
  *   ph_client compile   compile a saxpy kernel for gfx950 (no GPU needed)
- *   ph_client dispatch  run it through ph_dispatch on host buffers and
- *                       through ph_dispatch_device on device buffers
+ *   ph_client dispatch  run it through ph_dispatch on host buffers,
+ *                       through ph_dispatch_device on device buffers and
+ *                       through ph_dispatch_noalloc (twice, the second
+ *                       call smaller, then once too large to fit)
  */
 #include <stdio.h>
 #include <stdlib.h>
@@ -98,6 +100,32 @@ int main(int argc, char **argv) {
     }
   }
   printf("ph_dispatch_device ok\n");
+
+  /* The allocation-free entry point: the kernel from the cache, operands
+   * staged in the library's fixed per-GPU array. The kernel guards i < 1000,
+   * so a shorter call gets a shorter grid and shorter buffers. */
+  ph_kernel *k = NULL;
+  if ((rc = ph_get_kernel(kSource, strlen(kSource), "saxpy", PH_MATH_SAFE, &k, &err))) return fail("ph_get_kernel", rc, err);
+  for (int pass = 0; pass < 2; ++pass) {
+    const int n = pass == 0 ? N : 300;
+    size_t nb[2] = {n * sizeof(float), n * sizeof(float)}, ob[1] = {n * sizeof(float)};
+    memset(o, 0, N * sizeof(float));
+    rc = ph_dispatch_noalloc(k, n, 1, 1, 256, 1, NULL, ins, nb, 2, outs, ob, 1, &err);
+    if (rc != PH_OK) return fail("ph_dispatch_noalloc", rc, err);
+    if (check(x, y, o, n)) return 1;
+    for (int i = n; i < N; ++i)
+      if (o[i] != 0.0f) {
+        fprintf(stderr, "o[%d] written past the output\n", i);
+        return 1;
+      }
+  }
+  size_t huge[2] = {ph_noalloc_scratch_bytes(), N * sizeof(float)};
+  rc = ph_dispatch_noalloc(k, N, 1, 1, 256, 1, NULL, ins, huge, 2, outs, out_bytes, 1, &err);
+  printf("oversized -> %d (%s)\n", rc, err ? err : "");
+  ph_free_error(err);
+  err = NULL;
+  if (rc == PH_OK) return 1;
+  printf("ph_dispatch_noalloc ok\n");
   ph_free(dx);
   ph_free(dy);
   ph_free(dout);

@@ -31,3 +31,4 @@ def test_c_client_dispatches_on_the_gpu(tmp_path):
     r = subprocess.run([str(_build(tmp_path)), "dispatch"], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "ph_dispatch ok" in r.stdout and "ph_dispatch_device ok" in r.stdout
+    assert "ph_dispatch_noalloc ok" in r.stdout and "oversized -> 1" in r.stdout
