@@ -637,9 +637,8 @@ def bench_gs_fused(steps: int, warmup: int, cpu: bool) -> dict:
                        "bytes_per_pass_algorithmic": pass_bytes, "avg_pass_ms": gpu_s * 1e3 / passes,
                        "effective_per_step_GBps": GS_BYTES_PER_CELL_STEP * cells / (ms / 1e3) / 1e9,
                        "note": ("achieved/frac: both fields read and written once per pass (16 B/cell) over the "
-                                "pass time. The pass is bound by VALU issue and by how little of its HBM time "
-                                "overlaps its arithmetic, not by HBM bandwidth: alone, its arithmetic takes 50 us "
-                                "and its loads and stores 43 us of a 76 us pass. effective_per_step_GBps prices "
+                                "pass time. The register pass is bound by VALU issue and by how little of its HBM "
+                                "time overlaps its arithmetic, not by HBM bandwidth. effective_per_step_GBps prices "
                                 "each step at the per-step kernel's 16 B/cell, traffic this kernel does not make")}
     if kind == "regs":
         # VALU issue over the whole graph: each launch's loop-iteration slots
@@ -653,16 +652,28 @@ def bench_gs_fused(steps: int, warmup: int, cpu: bool) -> dict:
         total, per = 0.0, {}
         for kk in set(fused.launches(n_steps)):
             code = rt.compile_code_object(fused.source(kk), "gray_scott_regs", "fast")
-            slots, _ = isa.issue_slots(code, rates["relative_cost_vs_fma"])
+            # one pass of the machine loop is one group of rows of one lane
+            slots, _ = isa.issue_slots(code, rates["relative_cost_vs_fma"], per_machine_iteration=True)
             waves = stencil.register_geometry(cfg.size, kk, fused.rows, fused.cols)[0]
             iters = waves * 64 * -(-(fused.rows + 2 * kk) // fused.group)
             count = fused.launches(n_steps).count(kk)
             per[kk] = {"slots_per_iteration": slots, "lane_iterations_per_launch": iters, "launches": count}
             total += slots * iters * count
         sustained = rates["sustained_fma_tflops"] * 1e12 / 2
-        res["roofline"]["issue"] = {"per_kernel": per, "achieved_slots_per_s": total / gpu_s,
-                                    "sustained_fma_slots_per_s": sustained,
-                                    "frac_of_sustained_issue": total / gpu_s / sustained}
+        issue = {"per_kernel": per, "achieved_slots_per_s": total / gpu_s, "sustained_fma_slots_per_s": sustained,
+                 "frac_of_sustained_issue": total / gpu_s / sustained}
+        # The register pass is bound by VALU issue (its HBM figures go under
+        # "hbm"): FMA-equivalent slots, 2 FLOP each, against the FP32 peak.
+        hbm_part = {k: res["roofline"][k] for k in ("achieved", "peak", "unit", "frac", "traffic",
+                                                    "bytes_per_pass_algorithmic", "avg_pass_ms",
+                                                    "effective_per_step_GBps", "note")}
+        flops = 2 * total / gpu_s
+        res["roofline"] = {"bound": "valu", "achieved": flops / 1e12, "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
+                           "frac": flops / FP32_PEAK, "traffic": hbm_part["traffic"], "issue": issue,
+                           "hbm": hbm_part,
+                           "note": ("achieved: the graph's FMA-equivalent VALU issue slots (this build's ISA, measured "
+                                    "per-instruction costs) at 2 FLOP each per second; issue.frac_of_sustained_issue "
+                                    "against the measured sustained rate; hbm: the passes' own traffic")}
     res["pattern_energy"] = float(np.sum(v, dtype=np.float64))
     if cpu:
         import oracle

@@ -201,7 +201,8 @@ def loop_model(code_or_asm: bytes | str, lat_valu: float, lat_trans: float, issu
 _VOP3_INT = ("v_add3_", "v_xad_", "v_lshl_add_", "v_add_lshl_", "v_lshl_or_", "v_and_or_", "v_or3_", "v_xor3_")
 
 
-def issue_slots(code_or_asm: bytes | str, costs: dict[str, float]) -> tuple[float, dict[str, int]]:
+def issue_slots(code_or_asm: bytes | str, costs: dict[str, float],
+                per_machine_iteration: bool = False) -> tuple[float, dict[str, int]]:
     """FMA-equivalent issue slots of one iteration of the hot loop: each
     vector instruction weighted by its measured cost relative to
     v_fma_f32 (`costs`, keyed by mnemonic without encoding suffix, e.g.
@@ -210,7 +211,9 @@ def issue_slots(code_or_asm: bytes | str, costs: dict[str, float]) -> tuple[floa
     every other vector instruction 1. Scalar instructions are not counted
     (they issue beside vector ones from other wavefronts). Returns the
     slots and the instruction histogram, both per source iteration (a
-    machine loop unrolled k times is divided by k)."""
+    machine loop unrolled k times is divided by k), or per pass of the
+    machine loop with `per_machine_iteration` (for a loop whose induction
+    step is not a count of source iterations)."""
     asm = code_or_asm if isinstance(code_or_asm, str) else disassemble(code_or_asm)
     body = loop_body(parse(asm))
     hist: dict[str, int] = {}
@@ -228,7 +231,7 @@ def issue_slots(code_or_asm: bytes | str, costs: dict[str, float]) -> tuple[floa
             slots += costs.get("v_add3_u32", 1.0)
         else:
             slots += 1.0
-    unroll = unroll_factor(body)
+    unroll = 1 if per_machine_iteration else unroll_factor(body)
     return slots / unroll, {k: v / unroll for k, v in hist.items()}
 
 

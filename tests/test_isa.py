@@ -89,3 +89,17 @@ def test_issue_slots_divide_by_the_unroll_factor():
     assert sum(b.op.startswith("v_") for b in body) == pytest.approx(slots * k)
     costs = {"v_fma_f32": 1.0, "v_mul_f32": 2.0}
     assert isa.issue_slots(code, costs)[0] == pytest.approx(slots + hist.get("v_mul_f32_e32", 0))
+
+
+@pytest.mark.skipif(not os.path.exists(isa.OBJDUMP), reason="ROCm llvm-objdump absent")
+def test_register_stencil_slots_per_machine_iteration():
+    """The register Gray-Scott loop's induction step counts rows, not source
+    iterations: per machine iteration its slots are the whole group's."""
+    from palladium_amd import runtime as rt
+    from palladium_amd import stencil
+
+    code = rt.compile_code_object(stencil.register_source(4096, 6, 64, .16, .08, .037, .097, 1.0, group=4),
+                                  "gray_scott_regs", "fast")
+    whole, hist = isa.issue_slots(code, {}, per_machine_iteration=True)
+    # 4 rows x 6 steps of ~15 float ops per cell, plus addressing
+    assert 360 <= whole <= 480 and hist.get("v_add_f32_dpp", 0) == 96
