@@ -472,6 +472,10 @@ def gray_scott_fused_run(fused: FusedGrayScott | RegisterGrayScott, u0: np.ndarr
     Returns (u, v, device seconds)."""
     if u0.shape != (fused.n, fused.n) or v0.shape != u0.shape:
         raise ValueError(f"fields must be {fused.n}x{fused.n}")
+    if steps < 0:
+        raise ValueError(f"steps must be non-negative, got {steps}")
+    if steps == 0:
+        return np.array(u0, np.float32), np.array(v0, np.float32), 0.0
     bufs = [
         [rt.Buffer.from_numpy(np.ascontiguousarray(u0, np.float32)),
          rt.Buffer.from_numpy(np.ascontiguousarray(v0, np.float32))],

@@ -203,3 +203,15 @@ def test_register_bad_shapes_are_refused():
         stencil.register_source(32, 2, 16, 0.16, 0.08, 0.037, 0.097, 1.0)
     with pytest.raises(ValueError, match="too small"):
         stencil.register_source(96, 2, 16, 0.16, 0.08, 0.037, 0.097, 1.0, cols=2)
+
+
+def test_runner_checks_its_arguments_before_touching_a_device():
+    f = stencil.FusedGrayScott.__new__(stencil.FusedGrayScott)
+    f.n = 64
+    u0 = np.ones((64, 64), np.float32)
+    with pytest.raises(ValueError, match="64x64"):
+        stencil.gray_scott_fused_run(f, u0[:32], u0, 4)
+    with pytest.raises(ValueError, match="non-negative"):
+        stencil.gray_scott_fused_run(f, u0, u0, -1)
+    u, v, t = stencil.gray_scott_fused_run(f, u0, 2 * u0, 0)
+    assert t == 0.0 and np.array_equal(u, u0) and np.array_equal(v, 2 * u0) and u is not u0
