@@ -33,7 +33,7 @@ GS_MEASURED_TRAFFIC_BYTES = int((131612.4 + 131072.0) * 1024)
 # The same for one 4-step pass of the LDS temporal-blocking Gray-Scott kernel.
 GSF_MEASURED_TRAFFIC_BYTES = int((2 * 66687.3 + 131072.0) * 1024)
 # And for one 6-step pass of the register Gray-Scott kernel (64-row strips).
-GSR_MEASURED_TRAFFIC_BYTES = int((2 * 73659.0 + 131521.5) * 1024)
+GSR_MEASURED_TRAFFIC_BYTES = int((2 * 71623.8 + 132082.9) * 1024)
 
 
 def _cpu_cores() -> int:
