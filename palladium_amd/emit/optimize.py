@@ -510,6 +510,8 @@ def _carry_logs_while(e: JaxprEqn, used_after: set) -> tuple[list[JaxprEqn], Jax
         if sum(u is c for u in cases) != 1 or out_pos.get(body.outvars[k]) != [k]:
             continue
         (v,) = [u for u in cases if u is not c]
+        if c in out_pos:  # returned as some carry's next value: read as a value
+            continue
         rs = readers.get(c, [])
         logs = [x for x in rs if x.primitive.name == "log2"]
         if not logs or len(logs) + 1 != len(rs) or sel not in rs or readers.get(body.outvars[k], []):

@@ -383,3 +383,30 @@ def test_or_of_a_logical_shift_becomes_alignbit(n, c, signed, rewritten):
         got = (((np.uint64(hi) << np.uint64(32)) | xu) >> np.uint64(amt)) & np.uint64(0xFFFFFFFF)
         want = (xu >> np.uint64(n)) | np.uint64(c)
         np.testing.assert_array_equal(got, want)
+
+
+def test_carry_returned_as_another_carry_is_kept():
+    """`prev` also becomes the next value of a second carry: it is read as a
+    value there, so it must not turn into its log."""
+    from palladium_amd.emit.optimize import carry_logs, power_laws_to_exp2
+
+    def kernel(x_ref, o_ref):
+        x = x_ref[...]
+
+        def body(s):
+            k, c, d = s
+            v = 1.0 / (jnp.abs(x + k.astype(jnp.float32)) + 1.0)
+            f = v ** 0.3 * c ** 0.2
+            return k + 1, jnp.where(f < 0.5, v, c), c        # d' = c
+        _, c, d = lax.while_loop(lambda s: s[0] < 4, body, (jnp.int32(0), jnp.abs(x) + 1.0, jnp.abs(x)))
+        o_ref[...] = d
+
+    x = np.linspace(-2, 2, 64, dtype=np.float32)
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    call = pl.pallas_call(kernel, grid=(64,), in_specs=[s], out_specs=s,
+                          out_shape=pl.ShapeDtypeStruct((64,), np.float32))
+    spec = trace(call, x)
+    j = power_laws_to_exp2(spec.jaxpr)
+    assert carry_logs(j).eqns == j.eqns
+    got = interpret_spec(dataclasses.replace(spec, jaxpr=carry_logs(j)), x)[0]
+    np.testing.assert_array_equal(got, interpret_spec(dataclasses.replace(spec, jaxpr=j), x)[0])
