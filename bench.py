@@ -67,9 +67,7 @@ def bench_lv(steps: int, warmup: int, cpu: bool, cfg=None, block: int = 1, track
     stream = bound.stream
     ops = [*ins, *outs]
     print(f"[bench] lv_rk4 n={n} steps/traj={cfg.steps} blocks={bound.geometry.blocks}x{bound.geometry.block}", file=sys.stderr, flush=True)
-    for _ in range(warmup):
-        bound.launch_device(*ops, stream=stream)
-    stream.synchronize()
+    warm_launches = _warm_up(bound, ops, warmup)
 
     evs = [rt.Event() for _ in range(steps + 1)]
     rt.synchronize()
@@ -101,6 +99,8 @@ def bench_lv(steps: int, warmup: int, cpu: bool, cfg=None, block: int = 1, track
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
+        # the requested warm-up plus the top-up to MIN_WARMUP_S of device time
+        "warmup_launches": warm_launches,
         "ms_per_step": ms_per_step,
         "higher_is_better": True,
         "scaling": "weak",
@@ -232,13 +232,43 @@ def _lv_cpu_more(host, cfg) -> dict:
     return out
 
 
-def _timed_launches(bound, ops, steps: int, warmup: int):
+# Warm-up tops up to at least this much device time: the first tens of
+# milliseconds under load run at lower clocks (a 70 us kernel ran 0.071 ms
+# after 3 warm-up launches and 0.060 ms after 1,000 on the same box).
+MIN_WARMUP_S = 0.1
+# Warm-up launches the last _timed_launches call made, the requested ones
+# and the top-up together.
+LAST_WARMUP_LAUNCHES = 0
+
+
+def _warm_up(bound, ops, warmup: int) -> int:
+    """`warmup` untimed launches, topped up to MIN_WARMUP_S of device time
+    (at most 5,000 launches); returns how many ran."""
+    global LAST_WARMUP_LAUNCHES
     from palladium_amd import runtime as rt
 
     stream = bound.stream
     for _ in range(warmup):
         bound.launch_device(*ops, stream=stream)
+    e0, e1 = rt.Event(), rt.Event()
+    e0.record(stream)
+    bound.launch_device(*ops, stream=stream)
+    e1.record(stream)
     stream.synchronize()
+    one_s = max(e0.elapsed_ms(e1) / 1e3, 1e-6)
+    extra = max(0, min(int(MIN_WARMUP_S / one_s), 5000) - warmup - 1)
+    for _ in range(extra):
+        bound.launch_device(*ops, stream=stream)
+    stream.synchronize()
+    LAST_WARMUP_LAUNCHES = warmup + 1 + extra
+    return LAST_WARMUP_LAUNCHES
+
+
+def _timed_launches(bound, ops, steps: int, warmup: int):
+    from palladium_amd import runtime as rt
+
+    stream = bound.stream
+    _warm_up(bound, ops, warmup)
     evs = [rt.Event() for _ in range(steps + 1)]
     evs[0].record(stream)
     for k in range(steps):
@@ -513,9 +543,10 @@ def bench_gs(steps: int, warmup: int, cpu: bool) -> dict:
     cfg = GS_CFG
     u0, v0 = gray_scott_initial(cfg.size)
     call = gray_scott_call(cfg)
-    gray_scott_run(call, u0, v0, 10)  # compile + warm
+    gray_scott_run(call, u0, v0, 10)  # compile
     n_steps = int(os.environ.get("PALLADIUM_GS_STEPS", cfg.steps))
     graph = os.environ.get("PALLADIUM_GS_GRAPH", "1") != "0"
+    gray_scott_run(call, u0, v0, n_steps, graph=graph)  # warm: clocks settle under load
     _, v, gpu_s = gray_scott_run(call, u0, v0, n_steps, graph=graph)
     cells = cfg.size * cfg.size
     ms = gpu_s * 1e3 / n_steps
@@ -616,9 +647,10 @@ def bench_gs_fused(steps: int, warmup: int, cpu: bool) -> dict:
     kind = os.environ.get("PALLADIUM_GS_KERNEL", "regs")
     make = {"regs": stencil.RegisterGrayScott, "lds": stencil.FusedGrayScott}[kind]
     fused = make(cfg.size)
-    stencil.gray_scott_fused_run(fused, u0, v0, 2 * fused.k)  # compile + warm
+    stencil.gray_scott_fused_run(fused, u0, v0, 2 * fused.k)  # compile
     n_steps = int(os.environ.get("PALLADIUM_GS_STEPS", cfg.steps))
     graph = os.environ.get("PALLADIUM_GS_GRAPH", "1") != "0"
+    stencil.gray_scott_fused_run(fused, u0, v0, n_steps, graph=graph)  # warm: clocks settle under load
     u, v, gpu_s = stencil.gray_scott_fused_run(fused, u0, v0, n_steps, graph=graph)
     cells = cfg.size * cfg.size
     ms = gpu_s * 1e3 / n_steps
