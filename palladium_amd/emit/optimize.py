@@ -39,6 +39,7 @@ within FAST's approximate-transcendental contract.
 
 from __future__ import annotations
 
+import os
 from typing import Any
 
 import numpy as np
@@ -46,7 +47,7 @@ import numpy as np
 from palladium_amd.ir import ClosedJaxpr, Jaxpr, JaxprEqn, Literal, ShapedArray, Var, primitive
 
 __all__ = ["carry_logs", "drop_redundant_clamps", "factor_common_products", "fast_rewrites", "funnel_shifts",
-           "power_laws_to_exp2", "share_pow_logs"]
+           "power_laws_to_exp2", "reuse_affine_shifts", "share_pow_logs"]
 
 
 def _same(a: Any, b: Any) -> bool:
@@ -68,7 +69,8 @@ def _rewrite_sub(v: Any, fn: Any = None) -> Any:
 
 def fast_rewrites(jaxpr: Jaxpr) -> Jaxpr:
     """Every FAST-only rewrite, in order."""
-    return factor_common_products(carry_logs(power_laws_to_exp2(drop_redundant_clamps(jaxpr))))
+    j = factor_common_products(carry_logs(power_laws_to_exp2(drop_redundant_clamps(jaxpr))))
+    return j if os.environ.get("PALLADIUM_AFFINE_SHIFTS") == "0" else reuse_affine_shifts(j)
 
 
 def _lower_bound(v: Any, producer: dict) -> float | None:
@@ -628,5 +630,115 @@ def funnel_shifts(jaxpr: Jaxpr) -> Jaxpr:
                 new_eqns.append(e)
             continue
         new_eqns.append(e)
+    return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)
+
+
+def reuse_affine_shifts(jaxpr: Jaxpr) -> Jaxpr:
+    """FAST: a Runge-Kutta stage evaluates the right-hand side at a shifted
+    state, `y + h k`; where the same expression was already evaluated at
+    the unshifted state, the shift can be added to that value instead:
+
+        a - b (y + h k)   ->   (a - b y) - (b h) k      (a - b y computed before)
+        c (x + h k) - d   ->   (c x - d) + (c h) k      (c x - d computed before)
+
+    for a literal h. The instruction count stays (the shifted state is still
+    needed elsewhere, and `b h` is loop-invariant when b is), but the new
+    value no longer waits for the shifted state: one dependent operation
+    fewer per stage on a latency-bound integrator (the LV right-hand side
+    `x (a - b y)`, `y (c x - d)` of the reference's
+    `examples/01_ode_ensembles.py:72-91`). Rounding differs from the traced
+    order, within FAST's reassociation contract."""
+    producer = {ov: e for e in jaxpr.eqns for ov in e.outvars}
+    f32 = np.dtype(np.float32)
+
+    def is_f32(v: Any) -> bool:
+        return np.dtype(getattr(v.aval, "dtype", np.float64)) == f32
+
+    def same(a: Any, b: Any) -> bool:
+        return _same(a, b)
+
+    def prod_of(v: Any) -> tuple | None:
+        e = producer.get(v) if isinstance(v, Var) else None
+        return tuple(e.invars) if e is not None and e.primitive.name == "mul" else None
+
+    def shift_of(v: Any) -> tuple | None:
+        """(y, h, k) for v = y + h k (either order, h a literal)."""
+        e = producer.get(v) if isinstance(v, Var) else None
+        if e is None or e.primitive.name != "add":
+            return None
+        for y, m in (e.invars, e.invars[::-1]):
+            hk = prod_of(m)
+            if hk is None:
+                continue
+            for h, k in (hk, hk[::-1]):
+                if _f32_literal(h) is not None and isinstance(k, Var):
+                    return y, h, k
+        return None
+
+    def _aval_of(v: Any, out: Any) -> Any:
+        return v.aval if isinstance(v, Var) else ShapedArray((), np.float32)
+
+    def fits(v: Any, k: Any, out: Any) -> bool:
+        """v * h * k has out's shape with no broadcast of a variable."""
+        return (k.aval.shape == out.aval.shape
+                and (_f32_literal(v) is not None or (isinstance(v, Var) and v.aval.shape == out.aval.shape)))
+
+    seen_sub: list[JaxprEqn] = []   # earlier subs, in order
+    bypassed: set = set()           # products the rewritten subs no longer read
+    new_eqns: list[JaxprEqn] = []
+    for e in jaxpr.eqns:
+        params = {k: _rewrite_sub(v, reuse_affine_shifts) for k, v in e.params.items()}
+        e = JaxprEqn(e.invars, e.outvars, e.primitive, params)
+        out = e.outvars[0] if len(e.outvars) == 1 else None
+        done = False
+        if e.primitive.name == "sub" and out is not None and is_f32(out):
+            lhs, rhs = e.invars
+            # a - b (y + h k), with a - b y earlier
+            bv = prod_of(rhs)
+            for b, v in ((bv, bv[::-1]) if bv else ()):
+                sh = shift_of(v)
+                if done or sh is None:
+                    continue
+                y, h, k = sh
+                if not fits(b, k, out):
+                    continue
+                for s0 in seen_sub:
+                    p0 = prod_of(s0.invars[1])
+                    if (same(s0.invars[0], lhs) and p0 is not None
+                            and ((same(p0[0], b) and same(p0[1], y)) or (same(p0[0], y) and same(p0[1], b)))):
+                        bh, t = Var(_aval_of(b, out)), Var(out.aval)
+                        new_eqns.append(JaxprEqn([b, h], [bh], primitive("mul"), {}))
+                        new_eqns.append(JaxprEqn([bh, k], [t], primitive("mul"), {}))
+                        new_eqns.append(JaxprEqn([s0.outvars[0], t], [out], primitive("sub"), {}))
+                        bypassed.add(rhs)
+                        done = True
+                        break
+            # c (x + h k) - d, with c x - d earlier
+            cv = prod_of(lhs)
+            for c, v in ((cv, cv[::-1]) if (cv and not done) else ()):
+                sh = shift_of(v)
+                if done or sh is None:
+                    continue
+                x, h, k = sh
+                if not fits(c, k, out):
+                    continue
+                for s0 in seen_sub:
+                    q0 = prod_of(s0.invars[0])
+                    if (same(s0.invars[1], rhs) and q0 is not None
+                            and ((same(q0[0], c) and same(q0[1], x)) or (same(q0[0], x) and same(q0[1], c)))):
+                        ch, t = Var(_aval_of(c, out)), Var(out.aval)
+                        new_eqns.append(JaxprEqn([c, h], [ch], primitive("mul"), {}))
+                        new_eqns.append(JaxprEqn([ch, k], [t], primitive("mul"), {}))
+                        new_eqns.append(JaxprEqn([s0.outvars[0], t], [out], primitive("add"), {}))
+                        bypassed.add(lhs)
+                        done = True
+                        break
+        if done:
+            continue
+        if e.primitive.name == "sub" and out is not None:
+            seen_sub.append(e)
+        new_eqns.append(e)
+    used = {v for e in new_eqns for v in e.invars if isinstance(v, Var)} | set(jaxpr.outvars)
+    new_eqns = [e for e in new_eqns if not (e.outvars[0] in bypassed and e.outvars[0] not in used)]
     return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)
 

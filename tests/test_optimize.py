@@ -108,7 +108,10 @@ def test_gray_scott_and_bs3_agree_after_rewrite():
     np.testing.assert_allclose(got[0], want[0], rtol=1e-3, atol=1e-4)
 
 
-def test_emitter_applies_rewrite_only_under_fast():
+def test_emitter_applies_rewrite_only_under_fast(monkeypatch):
+    # the common-factor rewrite alone: the affine-shift reuse trades a
+    # product of the shifted state for a product of the shift
+    monkeypatch.setenv("PALLADIUM_AFFINE_SHIFTS", "0")
     args = lv_inputs(256, 0)
     spec = trace(lv_rk4_call(256, 0.01, 10)._staged, *args)
     safe = emit_hip(spec, math_mode="safe")
@@ -410,3 +413,74 @@ def test_carry_returned_as_another_carry_is_kept():
     assert carry_logs(j).eqns == j.eqns
     got = interpret_spec(dataclasses.replace(spec, jaxpr=carry_logs(j)), x)[0]
     np.testing.assert_array_equal(got, interpret_spec(dataclasses.replace(spec, jaxpr=j), x)[0])
+
+
+from palladium_amd.emit.optimize import reuse_affine_shifts  # noqa: E402
+
+
+def _shift_kernel(h, reorder=False):
+    """One explicit stage of the LV right-hand side at y and at y + h k."""
+    def kernel(x_ref, y_ref, a_ref, b_ref, o_ref, p_ref):
+        x, y, a, b = x_ref[...], y_ref[...], a_ref[...], b_ref[...]
+        f0 = a - b * y              # the unshifted value
+        g0 = b * x - a
+        k, j = x * f0, y * g0
+        y2 = (y + h * k) if not reorder else (k * h + y)
+        x2 = x + h * j
+        o_ref[...] = x2 * (a - b * y2)
+        p_ref[...] = y2 * ((x2 * b if reorder else b * x2) - a)
+    return kernel
+
+
+def _shift_spec(h, x, y, a, b, reorder=False):
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    call = pl.pallas_call(_shift_kernel(h, reorder), grid=(x.size,), in_specs=[s] * 4, out_specs=(s, s),
+                          out_shape=(pl.ShapeDtypeStruct(x.shape, np.float32),) * 2)
+    return trace(call, x, y, a, b)
+
+
+@pytest.mark.parametrize("reorder", [False, True])
+def test_affine_shift_reuse_is_exact_where_arithmetic_is(reorder):
+    # small integers and h = 1/2: every product and sum is exact in float32,
+    # so the reassociated form must agree bit for bit; a dropped term, a
+    # wrong sign or the wrong base value would not
+    r = np.random.default_rng(3)
+    x, y, a, b = (r.integers(-8, 9, 256).astype(np.float32) for _ in range(4))
+    spec = _shift_spec(0.5, x, y, a, b, reorder)
+    opt = dataclasses.replace(spec, jaxpr=reuse_affine_shifts(spec.jaxpr))
+    # both shifted right-hand sides now start from the unshifted ones
+    subs = [e for e in opt.jaxpr.eqns if e.primitive.name in ("sub", "add")]
+    assert _count(opt.jaxpr, "sub") == _count(spec.jaxpr, "sub") - 1
+    assert _count(opt.jaxpr, "mul") == _count(spec.jaxpr, "mul") + 2     # b h, c h and their uses; 2 dead gone
+    assert len(subs) == len([e for e in spec.jaxpr.eqns if e.primitive.name in ("sub", "add")])
+    for g, w in zip(interpret_spec(opt, x, y, a, b), interpret_spec(spec, x, y, a, b)):
+        np.testing.assert_array_equal(g, w)
+    # and against the closed form evaluated in float64
+    xf, yf, af, bf = (v.astype(np.float64) for v in (x, y, a, b))
+    y2 = yf + 0.5 * xf * (af - bf * yf)
+    x2 = xf + 0.5 * yf * (bf * xf - af)
+    got = interpret_spec(opt, x, y, a, b)
+    np.testing.assert_array_equal(got[0], (x2 * (af - bf * y2)).astype(np.float32))
+    np.testing.assert_array_equal(got[1], (y2 * (bf * x2 - af)).astype(np.float32))
+
+
+def test_affine_shift_needs_the_unshifted_value():
+    def kernel(y_ref, a_ref, b_ref, k_ref, o_ref):
+        y, a, b, k = y_ref[...], a_ref[...], b_ref[...], k_ref[...]
+        o_ref[...] = a - b * (y + 0.5 * k)      # a - b y never computed: nothing to reuse
+
+    v = np.linspace(1, 2, 64, dtype=np.float32)
+    call = pl.pallas_call(kernel, out_shape=pl.ShapeDtypeStruct((64,), np.float32))
+    spec = trace(call, v, v, v, v)
+    assert reuse_affine_shifts(spec.jaxpr).eqns == spec.jaxpr.eqns
+
+
+def test_affine_shift_reuse_on_lv_rk4_within_fast_tolerance():
+    args = lv_inputs(512, 1)
+    spec = trace(lv_rk4_call(512, 0.005, 400)._staged, *args)
+    # the traced x a - b x y becomes x (a - b y) under the common-factor rewrite first
+    fac = factor_common_products(spec.jaxpr)
+    opt = dataclasses.replace(spec, jaxpr=reuse_affine_shifts(fac))
+    assert opt.jaxpr.eqns != fac.eqns
+    for g, w in zip(interpret_spec(opt, *args), interpret_spec(spec, *args)):
+        np.testing.assert_allclose(g, w, rtol=2e-5, atol=1e-6)
