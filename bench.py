@@ -1041,6 +1041,10 @@ _VALU_PROBES = {
     "v_add3_u32": ("unsigned int", "v_add3_u32 %0, %0, %1, %2", True),
     "v_exp_f32": ("float", "v_exp_f32 %0, %0", None),
     "v_perm_b32": ("unsigned int", "v_perm_b32 %0, %0, %0, %1", False),
+    # the register stencil's neighbour sum: an add whose first operand is
+    # read from the next lane over (DPP wave rotation)
+    "v_add_f32_dpp": ("float", "v_add_f32_dpp %0, %1, %0 wave_rol:1 row_mask:0xf bank_mask:0xf bound_ctrl:1", False),
+    "v_mov_b32": ("unsigned int", "v_mov_b32 %0, %1", False),
 }
 _VALU_ITERS = 2048
 
