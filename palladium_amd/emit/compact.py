@@ -192,7 +192,9 @@ def emit_compacting_while(env: Any, cursor: Any, eqn: Any, emit_jaxpr: Any, decl
             with cursor.block(f"if (!__any({live}))"):
                 cursor.emit("break;")
             outs = emit_jaxpr(env, cursor, bj, body_consts + carries)
-            copy_back(cursor, outs, carries, predicate=live)
+            from palladium_amd.emit.rules import select_guards
+
+            copy_back(cursor, outs, carries, predicate=live, guards=select_guards(env, bj, bn))
         # Epoch boundary: the same condition, on the state as it stands.
         (pred,) = emit_jaxpr(env, cursor, cj, cond_consts + carries)
         cursor.emit(f"bool {own} = ({pred.at('0')}) && {slot} >= 0;")

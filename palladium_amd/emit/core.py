@@ -502,7 +502,7 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
 
     body = plan.jaxpr if plan else spec.jaxpr
     from palladium_amd.emit.compact import plan_for
-    from palladium_amd.emit.optimize import funnel_shifts
+    from palladium_amd.emit.optimize import fold_counters, funnel_shifts
 
     if math_mode is not None and math_mode_ordinal(math_mode) == 2:
         from palladium_amd.emit.optimize import fast_rewrites
@@ -518,6 +518,12 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
             body = shared
     # Exact, every mode; after the rewrites that read the or-and-shift form.
     body = funnel_shifts(body)
+    if os.environ.get("PALLADIUM_FOLD_COUNTERS", "1") != "0":
+        folded = fold_counters(body)
+        # A folded count is read after the loop: one more result row in LDS,
+        # which must not cost the loop its compaction either.
+        if not (plan is None and geo.block == 1024) or plan_for(spec, folded, lanes, block) is not None:
+            body = folded
 
     cplan = plan_for(spec, body, lanes, block)
     if (cplan is not None) != (plan is None and geo.block == 1024 and plan_for(spec, spec.jaxpr, lanes, block) is not None):

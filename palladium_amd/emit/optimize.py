@@ -742,3 +742,122 @@ def reuse_affine_shifts(jaxpr: Jaxpr) -> Jaxpr:
     new_eqns = [e for e in new_eqns if not (e.outvars[0] in bypassed and e.outvars[0] not in used)]
     return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)
 
+
+
+def fold_counters(jaxpr: Jaxpr) -> Jaxpr:
+    """Exact, every math mode: in a while loop with integer carries
+
+        a' = a + select_n(p, a0, a1)     b' = b + select_n(p, b0, b1)     n' = n + s
+
+    for literals with a0 + b0 == a1 + b1 == s (an adaptive solver's
+    accepted and rejected counts beside its attempt count,
+    `examples/02_adaptive_lockstep.py:85-140` and
+    `tests/test_08_adaptive.py:33-142` of the reference), a + b - n never
+    changes, so b need not be carried: its carry becomes the identity, which
+    the compiler hoists out of the loop, and after the loop
+
+        b_final = b_init + (n_final - n_init) - (a_final - a_init)
+
+    in the same wrapping integer arithmetic. The loop loses b's add and
+    select; the condition and the rest of the body must not read b."""
+    new_eqns: list[JaxprEqn] = []
+    for e in jaxpr.eqns:
+        params = {k: _rewrite_sub(v, fold_counters) for k, v in e.params.items()}
+        e = JaxprEqn(e.invars, e.outvars, e.primitive, params)
+        if e.primitive.name == "while":
+            e, post = _fold_counters_while(e)
+            new_eqns.append(e)
+            new_eqns.extend(post)
+            continue
+        new_eqns.append(e)
+    return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)
+
+
+def _fold_counters_while(e: JaxprEqn) -> tuple[JaxprEqn, list[JaxprEqn]]:
+    cn, bn = int(e.params["cond_nconsts"]), int(e.params["body_nconsts"])
+    body = getattr(e.params["body_jaxpr"], "jaxpr", e.params["body_jaxpr"])
+    cond = getattr(e.params["cond_jaxpr"], "jaxpr", e.params["cond_jaxpr"])
+    carries = body.invars[bn:]
+    producer = {ov: x for x in body.eqns for ov in x.outvars}
+    readers: dict[Any, list] = {}
+    for x in body.eqns:
+        for v in x.invars:
+            if isinstance(v, Var):
+                readers.setdefault(v, []).append(x)
+    cond_used = {v for x in cond.eqns for v in x.invars} | set(cond.outvars)
+
+    def lit(v: Any) -> int | None:
+        for _ in range(4):
+            if isinstance(v, Literal):
+                return int(np.asarray(v.val).astype(np.int64)) if np.ndim(v.val) == 0 else None
+            x = producer.get(v) if isinstance(v, Var) else None
+            if x is None or x.primitive.name != "broadcast_in_dim":
+                return None
+            v = x.invars[0]
+        return None
+
+    def increment(k: int) -> Any:
+        """The added operand of carry k's update `c + X`, or None."""
+        c, out = carries[k], body.outvars[k]
+        x = producer.get(out) if isinstance(out, Var) else None
+        if x is None or x.primitive.name != "add" or len(x.invars) != 2:
+            return None
+        if x.invars[0] is c:
+            return x.invars[1]
+        return x.invars[0] if x.invars[1] is c else None
+
+    def is_int(v: Any) -> bool:
+        return np.issubdtype(np.dtype(v.aval.dtype), np.integer)
+
+    steps, selects = {}, {}
+    for k, c in enumerate(carries):
+        if not is_int(c) or body.outvars.count(body.outvars[k]) != 1:
+            continue
+        inc = increment(k)
+        if inc is None:
+            continue
+        s = lit(inc)
+        if s is not None:
+            steps[k] = s
+            continue
+        x = producer.get(inc) if isinstance(inc, Var) else None
+        if x is not None and x.primitive.name == "select_n" and len(x.invars) == 3:
+            cases = [lit(v) for v in x.invars[1:]]
+            if None not in cases:
+                selects[k] = (x.invars[0], cases[0], cases[1])
+    plan = None
+    for j, (pj, b0, b1) in selects.items():
+        cj = carries[j]
+        if (cond.invars[cn + j] in cond_used or readers.get(cj, []) != [producer[body.outvars[j]]]
+                or cj in body.outvars):
+            continue
+        for i, (pi, a0, a1) in selects.items():
+            if i == j or pi is not pj or a0 + b0 != a1 + b1:
+                continue
+            n = next((n for n, s in steps.items() if s == a0 + b0 and n not in (i, j)
+                      and carries[n].aval.dtype == cj.aval.dtype == carries[i].aval.dtype
+                      and carries[n].aval.shape == cj.aval.shape == carries[i].aval.shape), None)
+            if n is not None:
+                plan = (i, j, n)
+                break
+        if plan:
+            break
+    if plan is None:
+        return e, []
+    i, j, n = plan
+    new_out = list(body.outvars)
+    new_out[j] = carries[j]  # the identity: b keeps its initial value in the loop
+    new_body = Jaxpr(body.constvars, body.invars, new_out, body.eqns)
+    params = dict(e.params)
+    params["body_jaxpr"] = _closed_like(e.params["body_jaxpr"], new_body)
+    outs = list(e.outvars)
+    b_final = outs[j]
+    outs[j] = Var(b_final.aval)
+    init = e.invars[cn + bn:]
+    aval = b_final.aval
+    dn, da, d = Var(aval), Var(aval), Var(aval)
+    post = [JaxprEqn([outs[n], init[n]], [dn], primitive("sub"), {}),
+            JaxprEqn([outs[i], init[i]], [da], primitive("sub"), {}),
+            JaxprEqn([dn, da], [d], primitive("sub"), {}),
+            JaxprEqn([outs[j], d], [b_final], primitive("add"), {})]
+    return JaxprEqn(e.invars, outs, e.primitive, params), post

@@ -725,35 +725,69 @@ def _declare_carries(env: Environment, cursor: Cursor, invars: list[Any], outvar
     return carries
 
 
-def copy_back_carries(cursor: Cursor, outs: list[CVal], carries: list[CVal], predicate: str | None = None) -> None:
+def copy_back_carries(cursor: Cursor, outs: list[CVal], carries: list[CVal], predicate: str | None = None,
+                      guards: list | None = None) -> None:
     """Simultaneous carry update: read every new value into a temporary,
     then write all carries (reference: `src/palladium/emit/rules.py:741-809`;
     the Metal `volatile` workaround is not needed here). With `predicate`,
-    a carry takes its new value only where the predicate holds."""
-    updates = [(o, c) for o, c in zip(outs, carries) if o.expr != c.expr]
+    a carry takes its new value only where the predicate holds. `guards`
+    (one entry per carry, from `select_guards`) narrows that further: a
+    carry whose new value is `p ? x : carry` takes x where the predicate
+    and p hold, one select where two would otherwise be emitted."""
+    guards = guards or [None] * len(carries)
+    updates = [(o, c, g) for o, c, g in zip(outs, carries, guards) if o.expr != c.expr]
     staged = []
-    for out, carry in updates:
+    for out, carry, g in updates:
         if carry.size == 1:
             t = cursor.fresh("_cb")
+            when = predicate
+            if g is not None and predicate is not None:
+                out, cond = g
+                when = cursor.fresh("_cg")
+                cursor.emit(f"const bool {when} = ({predicate}) && ({cond});")
             cursor.emit(f"const {carry.ctype} {t} = {out.at('0')};")
-            staged.append((carry, t, None))
+            staged.append((carry, t, None, when))
         else:
             t = cursor.fresh("_cb")
             cursor.emit(f"{carry.ctype} {t}[{carry.size}];")
             tv = CVal(t, carry.shape, carry.ctype)
             cursor.copy(tv, out, carry.size)
-            staged.append((carry, t, tv))
-    for carry, t, tv in staged:
-        if predicate is not None:
+            staged.append((carry, t, tv, predicate))
+    for carry, t, tv, when in staged:
+        if when is not None:
             if tv is None:
-                cursor.emit(f"{carry.at('0')} = {predicate} ? {t} : {carry.at('0')};")
+                cursor.emit(f"{carry.at('0')} = {when} ? {t} : {carry.at('0')};")
             else:
                 with cursor.loop(carry.size) as i:
-                    cursor.emit(f"{carry.at(i)} = {predicate} ? {tv.at(i)} : {carry.at(i)};")
+                    cursor.emit(f"{carry.at(i)} = {when} ? {tv.at(i)} : {carry.at(i)};")
         elif tv is None:
             cursor.emit(f"{carry.at('0')} = {t};")
         else:
             cursor.copy(carry, tv, carry.size)
+
+
+def select_guards(env: Environment, body: Any, nconsts: int) -> list:
+    """Per carry of a while body: (x, "p") when the carry's next value is
+    `select_n(p, carry, x)`, (x, "!p") for `select_n(p, x, carry)`, else
+    None; p a scalar boolean, the C expressions as bound after the body was
+    emitted."""
+    body = getattr(body, "jaxpr", body)
+    producer = {ov: e for e in body.eqns for ov in e.outvars}
+    out = []
+    for k, ov in enumerate(body.outvars):
+        c = body.invars[nconsts + k]
+        e = producer.get(ov) if isinstance(ov, Var) else None
+        g = None
+        if (e is not None and e.primitive.name == "select_n" and len(e.invars) == 3 and isinstance(e.invars[0], Var)
+                and np.dtype(e.invars[0].aval.dtype) == np.bool_ and math.prod(e.invars[0].aval.shape) == 1
+                and math.prod(c.aval.shape) == 1):
+            p = env.val(e.invars[0]).at("0")
+            if e.invars[1] is c and e.invars[2] is not c:
+                g = (env.val(e.invars[2]), p)
+            elif e.invars[2] is c and e.invars[1] is not c:
+                g = (env.val(e.invars[1]), f"!({p})")
+        out.append(g)
+    return out
 
 
 @rule("scan")
@@ -850,7 +884,10 @@ def _rule_while(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
             with cursor.block(f"if (!({p}))"):
                 cursor.emit("break;")
         outs = emit_jaxpr(env, cursor, getattr(bj, "jaxpr", bj), body_consts + carries)
-        copy_back_carries(cursor, outs, carries, predicate=live if predicated else None)
+        if predicated:
+            copy_back_carries(cursor, outs, carries, predicate=live, guards=select_guards(env, bj, bn))
+        else:
+            copy_back_carries(cursor, outs, carries)
 
 
 @rule("cond")

@@ -1,0 +1,119 @@
+"""The exact counter fold (palladium_amd.emit.optimize.fold_counters): an
+adaptive loop's accepted and rejected counts beside its attempt count."""
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+from palladium_amd.emit.optimize import fold_counters
+from palladium_amd.frontend import jnp, lax, pl
+from palladium_amd.interpret import interpret_spec
+from palladium_amd.trace import trace
+from palladium_amd.workloads import bs3_inputs, bs3_vdp_call
+
+
+def _counter_kernel(step=1, a_cases=(0, 1), b_cases=(1, 0), cond_reads_counts=False):
+    def kernel(x_ref, a_ref, b_ref, n_ref):
+        x = x_ref[...]
+
+        def cond(c):
+            k, v, a, b, n = c
+            go = (v > 0.05) & (n < 40)
+            return go & (a < 1000) & (b < 1000) if cond_reads_counts else go
+
+        def body(c):
+            k, v, a, b, n = c
+            p = v * 7.0 - jnp.floor(v * 7.0) < 0.5          # a data-dependent accept
+            v = jnp.where(p, v * 0.5, v * 0.9)
+            a = a + jnp.where(p, a_cases[1], a_cases[0])
+            b = b + jnp.where(p, b_cases[1], b_cases[0])
+            return k, v, a, b, n + step
+
+        init = [jnp.full_like(x, c, jnp.int32) for c in (3, -5, 11)]
+        _, _, a, b, n = lax.while_loop(cond, body, (jnp.int32(0), x, *init))
+        a_ref[...] = a
+        b_ref[...] = b
+        n_ref[...] = n
+
+    return kernel
+
+
+def _spec(kernel, n=256):
+    x = np.random.default_rng(17).uniform(0.0, 1.0, n).astype(np.float32)
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    call = pl.pallas_call(kernel, grid=(n,), in_specs=[s], out_specs=(s, s, s),
+                          out_shape=(pl.ShapeDtypeStruct((n,), np.int32),) * 3)
+    return trace(call, x), x
+
+
+def _while(jaxpr):
+    (w,) = [e for e in jaxpr.eqns if e.primitive.name == "while"]
+    return w
+
+
+def _identity_carries(w):
+    body = getattr(w.params["body_jaxpr"], "jaxpr", w.params["body_jaxpr"])
+    bn = int(w.params["body_nconsts"])
+    return [k for k, o in enumerate(body.outvars) if o is body.invars[bn + k]]
+
+
+@pytest.mark.parametrize("step,a_cases,b_cases", [(1, (0, 1), (1, 0)), (2, (0, 2), (2, 0)), (2, (1, 2), (1, 0))])
+def test_fold_is_exact_and_drops_one_counter(step, a_cases, b_cases):
+    spec, x = _spec(_counter_kernel(step, a_cases, b_cases))
+    opt = dataclasses.replace(spec, jaxpr=fold_counters(spec.jaxpr))
+    assert len(_identity_carries(_while(opt.jaxpr))) == len(_identity_carries(_while(spec.jaxpr))) + 1
+    got, want = interpret_spec(opt, x), interpret_spec(spec, x)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
+    # the counts themselves, from a plain restatement of the loop
+    a_np, b_np, n_np = [], [], []
+    for v in x:
+        v, a, b, n = np.float32(v), 3, -5, 11
+        while v > np.float32(0.05) and n < 40:
+            p = v * np.float32(7) - np.floor(v * np.float32(7)) < 0.5
+            v = v * np.float32(0.5) if p else v * np.float32(0.9)
+            a, b, n = a + a_cases[int(p)], b + b_cases[int(p)], n + step
+        a_np.append(a), b_np.append(b), n_np.append(n)
+    np.testing.assert_array_equal(got[0], a_np)
+    np.testing.assert_array_equal(got[1], b_np)
+    np.testing.assert_array_equal(got[2], n_np)
+    assert len(set(b_np)) > 3  # the counts vary from lane to lane
+
+
+@pytest.mark.parametrize("kw", [dict(a_cases=(0, 1), b_cases=(1, 1)),        # a + b - n not invariant
+                                dict(step=2),                                 # increments sum to 1, not 2
+                                dict(cond_reads_counts=True)])                # both are read by the condition
+def test_fold_leaves_loops_it_cannot_prove(kw):
+    spec, _ = _spec(_counter_kernel(**kw))
+    assert fold_counters(spec.jaxpr).eqns == spec.jaxpr.eqns
+
+
+def test_fold_takes_the_counter_the_condition_does_not_read():
+    def kernel(x_ref, a_ref, b_ref, n_ref):
+        x = x_ref[...]
+
+        def body(c):
+            v, a, b, n = c
+            p = v * 3.0 - jnp.floor(v * 3.0) < 0.5
+            return v * 0.8, a + jnp.where(p, 1, 0), b + jnp.where(p, 0, 1), n + 1
+
+        init = [jnp.full_like(x, 0, jnp.int32) for _ in range(3)]
+        _, a, b, n = lax.while_loop(lambda c: (c[0] > 0.1) & (c[2] < 7), body, (x, *init))
+        a_ref[...], b_ref[...], n_ref[...] = a, b, n
+
+    spec, x = _spec(kernel)
+    w = _while(fold_counters(spec.jaxpr))
+    assert _identity_carries(w) == [1]          # a, not the b the condition reads
+    opt = dataclasses.replace(spec, jaxpr=fold_counters(spec.jaxpr))
+    for g, want in zip(interpret_spec(opt, x), interpret_spec(spec, x)):
+        np.testing.assert_array_equal(g, want)
+
+
+def test_bs3_counts_fold_bit_identically():
+    args = bs3_inputs(512)
+    spec = trace(bs3_vdp_call(512)._staged, *args)
+    opt = dataclasses.replace(spec, jaxpr=fold_counters(spec.jaxpr))
+    assert len(_identity_carries(_while(opt.jaxpr))) == len(_identity_carries(_while(spec.jaxpr))) + 1
+    for g, w in zip(interpret_spec(opt, *args), interpret_spec(spec, *args)):
+        np.testing.assert_array_equal(g, w)
