@@ -47,7 +47,7 @@ import numpy as np
 from palladium_amd.ir import ClosedJaxpr, Jaxpr, JaxprEqn, Literal, ShapedArray, Var, primitive
 
 __all__ = ["carry_logs", "drop_redundant_clamps", "factor_common_products", "fast_rewrites", "funnel_shifts",
-           "power_laws_to_exp2", "reuse_affine_shifts", "share_pow_logs"]
+           "power_laws_to_exp2", "reuse_affine_shifts", "share_pow_logs", "fold_counters"]
 
 
 def _same(a: Any, b: Any) -> bool:
