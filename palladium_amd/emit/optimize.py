@@ -753,8 +753,7 @@ def fold_counters(jaxpr: Jaxpr) -> Jaxpr:
     accepted and rejected counts beside its attempt count,
     `examples/02_adaptive_lockstep.py:85-140` and
     `tests/test_08_adaptive.py:33-142` of the reference), a + b - n never
-    changes, so b need not be carried: its carry becomes the identity, which
-    the compiler hoists out of the loop, and after the loop
+    changes, so b need not be carried: it leaves the loop, and after it
 
         b_final = b_init + (n_final - n_init) - (a_final - a_init)
 
@@ -845,19 +844,30 @@ def _fold_counters_while(e: JaxprEqn) -> tuple[JaxprEqn, list[JaxprEqn]]:
     if plan is None:
         return e, []
     i, j, n = plan
-    new_out = list(body.outvars)
-    new_out[j] = carries[j]  # the identity: b keeps its initial value in the loop
-    new_body = Jaxpr(body.constvars, body.invars, new_out, body.eqns)
+    # b leaves the loop: its update (and the select feeding only it) goes,
+    # and so does its slot in the body's, the condition's and the loop's
+    # operands and results; after the loop its initial value is still the
+    # loop operand's, so
+    #     b_final = b_init + (n_final - n_init) - (a_final - a_init).
+    upd = producer[body.outvars[j]]
+    dead = {id(upd)}
+    sel = producer.get(upd.invars[0] if upd.invars[1] is carries[j] else upd.invars[1])
+    if sel is not None and len(readers.get(sel.outvars[0], [])) == 1 and sel.outvars[0] not in body.outvars:
+        dead.add(id(sel))
+    new_body = Jaxpr(body.constvars, body.invars[:bn + j] + body.invars[bn + j + 1:],
+                     body.outvars[:j] + body.outvars[j + 1:], [x for x in body.eqns if id(x) not in dead])
+    new_cond = Jaxpr(cond.constvars, cond.invars[:cn + j] + cond.invars[cn + j + 1:], cond.outvars, cond.eqns)
     params = dict(e.params)
     params["body_jaxpr"] = _closed_like(e.params["body_jaxpr"], new_body)
-    outs = list(e.outvars)
-    b_final = outs[j]
-    outs[j] = Var(b_final.aval)
+    params["cond_jaxpr"] = _closed_like(e.params["cond_jaxpr"], new_cond)
     init = e.invars[cn + bn:]
+    b_final = e.outvars[j]
     aval = b_final.aval
     dn, da, d = Var(aval), Var(aval), Var(aval)
-    post = [JaxprEqn([outs[n], init[n]], [dn], primitive("sub"), {}),
-            JaxprEqn([outs[i], init[i]], [da], primitive("sub"), {}),
+    post = [JaxprEqn([e.outvars[n], init[n]], [dn], primitive("sub"), {}),
+            JaxprEqn([e.outvars[i], init[i]], [da], primitive("sub"), {}),
             JaxprEqn([dn, da], [d], primitive("sub"), {}),
-            JaxprEqn([outs[j], d], [b_final], primitive("add"), {})]
-    return JaxprEqn(e.invars, outs, e.primitive, params), post
+            JaxprEqn([init[j], d], [b_final], primitive("add"), {})]
+    k = cn + bn + j
+    outs = e.outvars[:j] + e.outvars[j + 1:]
+    return JaxprEqn(e.invars[:k] + e.invars[k + 1:], outs, e.primitive, params), post
