@@ -116,3 +116,82 @@ def test_bs3_counts_fold_bit_identically():
     assert len(_dropped(spec.jaxpr, opt.jaxpr)) == 1
     for g, w in zip(interpret_spec(opt, *args), interpret_spec(spec, *args)):
         np.testing.assert_array_equal(g, w)
+
+
+def _random_counter_kernel(seed):
+    """A while loop with 3-5 integer counters, each stepping by a select of
+    two small literals on one of two predicates, or by a fixed literal; the
+    condition reads the float state and, sometimes, one counter."""
+    r = np.random.default_rng(seed)
+    m = int(r.integers(3, 6))
+    kinds = []
+    for _ in range(m):
+        if r.random() < 0.3:
+            kinds.append(("step", int(r.integers(-2, 4))))
+        else:
+            kinds.append(("sel", int(r.integers(0, 2)), int(r.integers(-2, 4)), int(r.integers(-2, 4))))
+    if r.random() < 0.7:  # plant a complementary pair
+        i, j = r.choice(m, 2, replace=False)
+        s = int(r.integers(1, 4))
+        a0 = int(r.integers(-2, 4))
+        a1 = int(r.integers(-2, 4))
+        p = int(r.integers(0, 2))
+        kinds[i] = ("sel", p, a0, a1)
+        kinds[j] = ("sel", p, s - a0, s - a1)
+        kinds.append(("step", s))
+    init = [int(v) for v in r.integers(-50, 50, len(kinds))]
+    cond_reads = int(r.integers(-1, len(kinds)))
+    cap = int(r.integers(5, 40))
+
+    def kernel(x_ref, *outs):
+        x = x_ref[...]
+
+        def cond(c):
+            v, cs = c[0], c[1:]
+            go = (v > 0.02) & (cs[-1] < cap + 1000)
+            return go & (cs[cond_reads] < 10_000) if cond_reads >= 0 else go
+
+        def body(c):
+            v, cs = c[0], list(c[1:])
+            p0 = v * 7.0 - jnp.floor(v * 7.0) < 0.5
+            p1 = v * 3.0 - jnp.floor(v * 3.0) < 0.3
+            for k, kind in enumerate(kinds):
+                if kind[0] == "step":
+                    cs[k] = cs[k] + kind[1]
+                else:
+                    cs[k] = cs[k] + jnp.where((p0, p1)[kind[1]], kind[3], kind[2])
+            return (jnp.where(p0, v * 0.5, v * 0.85), *cs)
+
+        res = lax.while_loop(cond, body, (x, *[jnp.full_like(x, c, jnp.int32) for c in init]))
+        for o, c in zip(outs, res[1:]):
+            o[...] = c
+
+    return kernel, len(kinds)
+
+
+@pytest.mark.parametrize("seed", range(60))
+def test_fold_fuzz_bit_identical(seed):
+    kernel, m = _random_counter_kernel(seed)
+    n = 64
+    x = np.random.default_rng(seed).uniform(0.0, 1.0, n).astype(np.float32)
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    call = pl.pallas_call(kernel, grid=(n,), in_specs=[s], out_specs=(s,) * m,
+                          out_shape=(pl.ShapeDtypeStruct((n,), np.int32),) * m)
+    spec = trace(call, x)
+    folded = fold_counters(spec.jaxpr)
+    opt = dataclasses.replace(spec, jaxpr=folded)
+    for g, w in zip(interpret_spec(opt, x), interpret_spec(spec, x)):
+        np.testing.assert_array_equal(g, w)
+
+
+def test_fold_fuzz_fires_on_most_planted_pairs():
+    fired = 0
+    for seed in range(60):
+        kernel, m = _random_counter_kernel(seed)
+        x = np.zeros(64, np.float32)
+        s = pl.BlockSpec((1,), lambda i: (i,))
+        call = pl.pallas_call(kernel, grid=(64,), in_specs=[s], out_specs=(s,) * m,
+                              out_shape=(pl.ShapeDtypeStruct((64,), np.int32),) * m)
+        spec = trace(call, x)
+        fired += bool(_dropped(spec.jaxpr, fold_counters(spec.jaxpr)))
+    assert fired >= 35   # 41 of these 60 seeds plant a pair the fold can prove

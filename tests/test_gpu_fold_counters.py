@@ -11,7 +11,7 @@ import palladium_amd as pa
 from palladium_amd.frontend import pl
 from palladium_amd.trace import trace
 from palladium_amd.workloads import bs3_inputs, bs3_vdp_call
-from test_fold_counters import _counter_kernel
+from test_fold_counters import _counter_kernel, _random_counter_kernel
 
 pytestmark = pytest.mark.gpu
 
@@ -56,3 +56,18 @@ def test_bs3_fast_folded_equals_unfolded(monkeypatch):
     want = off(*args)
     for g, w in zip(got, want):
         np.testing.assert_array_equal(np.asarray(g).view(np.uint32), np.asarray(w).view(np.uint32))
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_counter_loops_equal_the_interpreter(seed, monkeypatch):
+    """The fuzz programs of tests/test_fold_counters.py, compiled (SAFE,
+    folded where the fold applies): bit-identical to the interpreter."""
+    n = 2048
+    print(f"[fold_counters] fuzz seed={seed}", flush=True)
+    kernel, m = _random_counter_kernel(seed)
+    x = np.random.default_rng(seed).uniform(0.0, 1.0, n).astype(np.float32)
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    f = pa.hip_call(kernel, grid=(n,), in_specs=[s], out_specs=(s,) * m,
+                    out_shape=(pl.ShapeDtypeStruct((n,), np.int32),) * m, math_mode="safe")
+    for g, w in zip(f(x), f.interpret(x)):
+        np.testing.assert_array_equal(g, w)
