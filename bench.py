@@ -1207,13 +1207,18 @@ def bs3_latency_bound(call, host, lat: dict, max_attempts: int, kernel_ms: float
     (palladium_amd.isa) with the measured latencies."""
     from palladium_amd import isa
     from palladium_amd import runtime as rt
+    from palladium_amd.emit.compact import epoch_unroll
 
     bound = call.bound(*host)
     code = rt.compile_code_object(bound.hip_source, bound.spec.name, mode)
     m = isa.loop_model(code, lat["fma_dependent_ns"], lat["transcendental_dependent_ns"], lat["issue_ns"])
-    floor_ms = max_attempts * m.cycles_per_iteration / 1e6
-    return {"ns_per_attempt_chain_model": m.cycles_per_iteration, "loop_instructions": m.instructions,
-            "loop_valu": m.valu, "loop_transcendental": m.transcendental, "max_attempts_one_lane": max_attempts,
+    # a compacted loop runs epoch_unroll() attempts per pass of its machine loop
+    per = epoch_unroll(mode) if "_cbuf" in bound.hip_source else 1
+    ns = m.cycles_per_iteration / per
+    floor_ms = max_attempts * ns / 1e6
+    return {"ns_per_attempt_chain_model": ns, "loop_instructions": m.instructions / per,
+            "loop_valu": m.valu / per, "loop_transcendental": m.transcendental / per,
+            "attempts_per_machine_iteration": per, "max_attempts_one_lane": max_attempts,
             "measured_ns_per_attempt_slowest_wave": kernel_ms * 1e6 / max_attempts,
             "latency_floor_ms": floor_ms, "latency_frac": floor_ms / kernel_ms, "latencies_ns": lat}
 

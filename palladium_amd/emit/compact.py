@@ -44,6 +44,27 @@ from palladium_amd.ir import KeyAval
 
 WORKGROUP = 1024
 EPOCH = 64
+# Loop iterations per pass of the epoch loop (see emit_compacting_while), by
+# math mode. More iterations per pass spread the pass's counter and branch
+# over more attempts; SAFE's deterministic pow makes its iteration about 2.5
+# times FAST's code, and past 16 of them its loop no longer fits the
+# instruction cache two CUs share (64 KiB). Measured on BS3: FAST 0.698 /
+# 0.690 / 0.673 / 0.667 / 0.659 / 0.652 ms at 1 / 2 / 4 / 8 / 16 / 32, SAFE
+# 2.14 / 2.13 / 2.10 / 2.08 / 2.07 / 2.08, SAFE 2.12 at 64.
+EPOCH_UNROLL = {"safe": 16, "other": 32}
+
+
+def epoch_unroll(math_mode: Any = None) -> int:
+    """Iterations of a compacted while loop per pass of its machine loop
+    (`PALLADIUM_EPOCH_UNROLL` overrides the default)."""
+    from palladium_amd.runtime import math_mode_ordinal
+
+    raw = os.environ.get("PALLADIUM_EPOCH_UNROLL")
+    safe = math_mode is None or math_mode_ordinal(math_mode) == 0
+    u = EPOCH_UNROLL["safe" if safe else "other"] if raw is None else int(raw)
+    if u < 1 or EPOCH % u:
+        raise ValueError(f"PALLADIUM_EPOCH_UNROLL={u} must divide the epoch of {EPOCH} iterations")
+    return u
 # LDS per workgroup the compaction may use (2 workgroups per CU fit in 160 KB).
 LDS_BUDGET = 78 * 1024
 
@@ -185,16 +206,21 @@ def emit_compacting_while(env: Any, cursor: Any, eqn: Any, emit_jaxpr: Any, decl
     cursor.emit(f"const int {wave} = (int)(threadIdx.x >> 6);")
     with cursor.block("while (true)"):
         ep = cursor.fresh("_ep")
-        with cursor.block(f"for (int {ep} = 0; {ep} < {EPOCH}; ++{ep})"):
-            (pred,) = emit_jaxpr(env, cursor, cj, cond_consts + carries)
-            live = cursor.fresh("_live")
-            cursor.emit(f"const bool {live} = ({pred.at('0')}) && {slot} >= 0;")
-            with cursor.block(f"if (!__any({live}))"):
-                cursor.emit("break;")
-            outs = emit_jaxpr(env, cursor, bj, body_consts + carries)
-            from palladium_amd.emit.rules import select_guards
+        unroll = getattr(env, "epoch_unroll", None) or epoch_unroll()
+        from palladium_amd.emit.rules import select_guards
 
-            copy_back(cursor, outs, carries, predicate=live, guards=select_guards(env, bj, bn))
+        # `unroll` iterations per pass, each with its own exit test (a break
+        # in any of them leaves the epoch): the pass's counter and branch are
+        # shared among them.
+        with cursor.block(f"for (int {ep} = 0; {ep} < {EPOCH}; {ep} += {unroll})"):
+            for _ in range(unroll):
+                (pred,) = emit_jaxpr(env, cursor, cj, cond_consts + carries)
+                live = cursor.fresh("_live")
+                cursor.emit(f"const bool {live} = ({pred.at('0')}) && {slot} >= 0;")
+                with cursor.block(f"if (!__any({live}))"):
+                    cursor.emit("break;")
+                outs = emit_jaxpr(env, cursor, bj, body_consts + carries)
+                copy_back(cursor, outs, carries, predicate=live, guards=select_guards(env, bj, bn))
         # Epoch boundary: the same condition, on the state as it stands.
         (pred,) = emit_jaxpr(env, cursor, cj, cond_consts + carries)
         cursor.emit(f"bool {own} = ({pred.at('0')}) && {slot} >= 0;")

@@ -825,7 +825,12 @@ def _fold_counters_while(e: JaxprEqn) -> tuple[JaxprEqn, list[JaxprEqn]]:
             if None not in cases:
                 selects[k] = (x.invars[0], cases[0], cases[1])
     plan = None
-    for j, (pj, b0, b1) in selects.items():
+    # Drop, of a pair, the count that moves when p is false (a rejection
+    # count): the one kept then steps under `p`, the mask the loop's other
+    # selects already use, not under `!p`.
+    order = sorted(selects, key=lambda j: not (selects[j][1] != 0 and selects[j][2] == 0))
+    for j in order:
+        pj, b0, b1 = selects[j]
         cj = carries[j]
         if (cond.invars[cn + j] in cond_used or readers.get(cj, []) != [producer[body.outvars[j]]]
                 or cj in body.outvars):

@@ -60,14 +60,18 @@ def test_bs3_fast_loop_has_one_exp_and_no_branches_inside():
     code = rt.compile_code_object(emit_hip(spec, math_mode="fast"), spec.name, "fast")
     body = isa.loop_body(isa.parse(isa.disassemble(code)))
     ops = [b.op for b in body]
-    assert sum(o.startswith("v_exp_") for o in ops) == 1
+    # the compacted loop's machine loop runs epoch_unroll() attempts per pass
+    from palladium_amd.emit.compact import epoch_unroll
+
+    u = epoch_unroll("fast")
+    assert sum(o.startswith("v_exp_") for o in ops) == u
     # log2(err) only: log2(prev) is carried (emit/optimize.py:carry_logs)
-    assert sum(o.startswith("v_log_") for o in ops) == 1
+    assert sum(o.startswith("v_log_") for o in ops) == u
     # the two divisions of the error norm; 1 / err no longer feeds a carry
-    assert sum(o.startswith("v_rcp_") for o in ops) == 2
+    assert sum(o.startswith("v_rcp_") for o in ops) == 2 * u
     assert not any("saveexec" in o for o in ops), "a pow slow path still branches inside the loop"
     m = isa.loop_model(code, 4.0, 12.0, 1.0)
-    assert 50 < m.valu < 120
+    assert 50 * u < m.valu < 120 * u
     assert m.cycles_per_iteration > m.instructions  # latency, not issue, sets it
 
 
