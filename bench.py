@@ -1207,13 +1207,13 @@ def bs3_latency_bound(call, host, lat: dict, max_attempts: int, kernel_ms: float
     (palladium_amd.isa) with the measured latencies."""
     from palladium_amd import isa
     from palladium_amd import runtime as rt
-    from palladium_amd.emit.compact import epoch_unroll
+    from palladium_amd.emit.compact import iterations_per_pass
 
     bound = call.bound(*host)
     code = rt.compile_code_object(bound.hip_source, bound.spec.name, mode)
     m = isa.loop_model(code, lat["fma_dependent_ns"], lat["transcendental_dependent_ns"], lat["issue_ns"])
-    # a compacted loop runs epoch_unroll() attempts per pass of its machine loop
-    per = epoch_unroll(mode) if "_cbuf" in bound.hip_source else 1
+    # a compacted loop runs several attempts per pass of its machine loop
+    per = iterations_per_pass(bound.hip_source)
     ns = m.cycles_per_iteration / per
     floor_ms = max_attempts * ns / 1e6
     return {"ns_per_attempt_chain_model": ns, "loop_instructions": m.instructions / per,

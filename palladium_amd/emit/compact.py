@@ -54,16 +54,49 @@ EPOCH = 64
 EPOCH_UNROLL = {"safe": 16, "other": 32}
 
 
-def epoch_unroll(math_mode: Any = None) -> int:
-    """Iterations of a compacted while loop per pass of its machine loop
-    (`PALLADIUM_EPOCH_UNROLL` overrides the default)."""
+# A pass holds at most this many traced operations of the loop body, so that
+# a large body is not copied 32 times (code size, compile time).
+EPOCH_UNROLL_OPS = 4096
+
+
+def _count_eqns(j: Any) -> int:
+    n = 0
+    for e in j.eqns:
+        n += 1
+        for v in e.params.values():
+            for sub in (v if isinstance(v, tuple) else (v,)):
+                if hasattr(getattr(sub, "jaxpr", sub), "eqns"):
+                    n += _count_eqns(getattr(sub, "jaxpr", sub))
+    return n
+
+
+def iterations_per_pass(hip_source: str) -> int:
+    """The iterations per machine-loop pass the emitter chose for a
+    compacted while loop in `hip_source` (1 if it has none)."""
+    import re
+
+    m = re.search(r"// (\d+) iterations per pass", hip_source)
+    return int(m.group(1)) if m else 1
+
+
+def epoch_unroll(math_mode: Any = None, body: Any = None) -> int:
+    """Iterations of a compacted while loop per pass of its machine loop:
+    the math mode's default, halved until the pass holds at most
+    EPOCH_UNROLL_OPS of `body`'s operations (`PALLADIUM_EPOCH_UNROLL`
+    overrides both)."""
     from palladium_amd.runtime import math_mode_ordinal
 
     raw = os.environ.get("PALLADIUM_EPOCH_UNROLL")
+    if raw is not None:
+        u = int(raw)
+        if u < 1 or EPOCH % u:
+            raise ValueError(f"PALLADIUM_EPOCH_UNROLL={u} must divide the epoch of {EPOCH} iterations")
+        return u
     safe = math_mode is None or math_mode_ordinal(math_mode) == 0
-    u = EPOCH_UNROLL["safe" if safe else "other"] if raw is None else int(raw)
-    if u < 1 or EPOCH % u:
-        raise ValueError(f"PALLADIUM_EPOCH_UNROLL={u} must divide the epoch of {EPOCH} iterations")
+    u = EPOCH_UNROLL["safe" if safe else "other"]
+    n = _count_eqns(getattr(body, "jaxpr", body)) if body is not None else 0
+    while u > 1 and u * n > EPOCH_UNROLL_OPS:
+        u //= 2
     return u
 # LDS per workgroup the compaction may use (2 workgroups per CU fit in 160 KB).
 LDS_BUDGET = 78 * 1024
@@ -206,7 +239,8 @@ def emit_compacting_while(env: Any, cursor: Any, eqn: Any, emit_jaxpr: Any, decl
     cursor.emit(f"const int {wave} = (int)(threadIdx.x >> 6);")
     with cursor.block("while (true)"):
         ep = cursor.fresh("_ep")
-        unroll = getattr(env, "epoch_unroll", None) or epoch_unroll()
+        unroll = epoch_unroll(getattr(env, "math_mode", None), bj)
+        cursor.emit(f"// {unroll} iterations per pass")
         from palladium_amd.emit.rules import select_guards
 
         # `unroll` iterations per pass, each with its own exit test (a break

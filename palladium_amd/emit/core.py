@@ -501,7 +501,7 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         params.append(f"{qual}{ct}* __restrict__ arg{k}_base")
 
     body = plan.jaxpr if plan else spec.jaxpr
-    from palladium_amd.emit.compact import epoch_unroll, plan_for
+    from palladium_amd.emit.compact import plan_for
     from palladium_amd.emit.optimize import fold_counters, funnel_shifts
 
     if math_mode is not None and math_mode_ordinal(math_mode) == 2:
@@ -548,7 +548,7 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         cursor.emit(f"const unsigned int _inst = _flat / {lanes}u;")
         cursor.emit(f"const int _lane = (int)(_flat % {lanes}u);")
     env.lanes = lanes  # type: ignore[attr-defined]
-    env.epoch_unroll = epoch_unroll(math_mode)  # type: ignore[attr-defined]
+    env.math_mode = math_mode  # type: ignore[attr-defined]
     env.grid = tuple(spec.grid)  # type: ignore[attr-defined]
     pid_vals = []
     rem = "_inst" if lanes > 1 else ("_flatc" if getattr(env, "compact_in", None) else "_flat")

@@ -90,3 +90,22 @@ def test_loops_reading_the_program_id_are_not_compacted():
                                     out_specs=pl.BlockSpec((1,), lambda i: (i,)),
                                     out_shape=pl.ShapeDtypeStruct((n,), np.int32)), np.ones(n, np.int32))
     assert "__syncthreads" not in emit_hip(spec_pid)
+
+
+def test_iterations_per_pass_follow_mode_and_body_size(monkeypatch):
+    from palladium_amd.emit import compact
+
+    spec = _bs3_spec(4096)
+    assert compact.iterations_per_pass(emit_hip(spec, math_mode="fast")) == 32
+    assert compact.iterations_per_pass(emit_hip(spec, math_mode="safe")) == 16
+    assert compact.iterations_per_pass(emit_hip(spec)) == 16
+    # a body that would not fit: fewer iterations per pass
+    monkeypatch.setattr(compact, "EPOCH_UNROLL_OPS", 400)
+    assert compact.iterations_per_pass(emit_hip(spec, math_mode="fast")) in (2, 4)
+    monkeypatch.setattr(compact, "EPOCH_UNROLL_OPS", 10)
+    assert compact.iterations_per_pass(emit_hip(spec, math_mode="fast")) == 1
+    monkeypatch.setenv("PALLADIUM_EPOCH_UNROLL", "8")
+    assert compact.iterations_per_pass(emit_hip(spec, math_mode="fast")) == 8
+    monkeypatch.setenv("PALLADIUM_EPOCH_UNROLL", "3")
+    with pytest.raises(ValueError, match="divide"):
+        emit_hip(spec, math_mode="fast")

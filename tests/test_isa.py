@@ -60,10 +60,11 @@ def test_bs3_fast_loop_has_one_exp_and_no_branches_inside():
     code = rt.compile_code_object(emit_hip(spec, math_mode="fast"), spec.name, "fast")
     body = isa.loop_body(isa.parse(isa.disassemble(code)))
     ops = [b.op for b in body]
-    # the compacted loop's machine loop runs epoch_unroll() attempts per pass
-    from palladium_amd.emit.compact import epoch_unroll
+    # the compacted loop's machine loop runs several attempts per pass
+    from palladium_amd.emit.compact import iterations_per_pass
 
-    u = epoch_unroll("fast")
+    u = iterations_per_pass(emit_hip(spec, math_mode="fast"))
+    assert u == 32
     assert sum(o.startswith("v_exp_") for o in ops) == u
     # log2(err) only: log2(prev) is carried (emit/optimize.py:carry_logs)
     assert sum(o.startswith("v_log_") for o in ops) == u
