@@ -871,23 +871,34 @@ def _rule_while(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     body_consts = [env.val(v) for v in eqn.invars[cn : cn + bn]]
     carries = _declare_carries(env, cursor, eqn.invars[cn + bn :], eqn.outvars)
     predicated = getattr(env, "lanes", 1) == 1 and _predicable(bj)
+    # A predicated loop runs several iterations per pass of its machine loop,
+    # each with its own exit test (a break in any of them leaves the loop),
+    # as the compacting form does.
+    unroll = 1
+    if predicated:
+        from palladium_amd.emit.compact import epoch_unroll
+
+        unroll = epoch_unroll(getattr(env, "math_mode", None), bj)
     with cursor.block("while (true)"):
-        (pred,) = emit_jaxpr(env, cursor, getattr(cj, "jaxpr", cj), cond_consts + carries)
-        p = pred.at("0")
-        if predicated:
-            # Evaluate once: the body may overwrite what the condition read.
-            live = cursor.fresh("_live")
-            cursor.emit(f"const bool {live} = {p};")
-            with cursor.block(f"if (!__any({live}))"):
-                cursor.emit("break;")
-        else:
-            with cursor.block(f"if (!({p}))"):
-                cursor.emit("break;")
-        outs = emit_jaxpr(env, cursor, getattr(bj, "jaxpr", bj), body_consts + carries)
-        if predicated:
-            copy_back_carries(cursor, outs, carries, predicate=live, guards=select_guards(env, bj, bn))
-        else:
-            copy_back_carries(cursor, outs, carries)
+        if unroll > 1:
+            cursor.emit(f"// {unroll} iterations per pass")
+        for _ in range(unroll):
+            (pred,) = emit_jaxpr(env, cursor, getattr(cj, "jaxpr", cj), cond_consts + carries)
+            p = pred.at("0")
+            if predicated:
+                # Evaluate once: the body may overwrite what the condition read.
+                live = cursor.fresh("_live")
+                cursor.emit(f"const bool {live} = {p};")
+                with cursor.block(f"if (!__any({live}))"):
+                    cursor.emit("break;")
+            else:
+                with cursor.block(f"if (!({p}))"):
+                    cursor.emit("break;")
+            outs = emit_jaxpr(env, cursor, getattr(bj, "jaxpr", bj), body_consts + carries)
+            if predicated:
+                copy_back_carries(cursor, outs, carries, predicate=live, guards=select_guards(env, bj, bn))
+            else:
+                copy_back_carries(cursor, outs, carries)
 
 
 @rule("cond")
