@@ -70,26 +70,6 @@ def _count_eqns(j: Any) -> int:
     return n
 
 
-# A predicated loop tests for the wavefront's exit on every EXIT_EVERY-th
-# iteration of a pass only: a lane whose condition has failed keeps its
-# carries, so the iterations between two tests change nothing once every
-# lane is done, and the test (a lane mask turned into a value and back, a
-# scalar compare and branch) is paid a quarter as often. BS3: FAST 0.657 ->
-# 0.641 ms, SAFE 2.087 -> 2.072 ms from every to every fourth iteration,
-# counts unchanged.
-EXIT_EVERY = 4
-
-
-def exit_every() -> int:
-    """Iterations per exit test of a predicated loop (`PALLADIUM_EXIT_EVERY`
-    overrides the default)."""
-    raw = os.environ.get("PALLADIUM_EXIT_EVERY")
-    e = EXIT_EVERY if raw is None else int(raw)
-    if e < 1:
-        raise ValueError(f"PALLADIUM_EXIT_EVERY={e} must be positive")
-    return e
-
-
 def iterations_per_pass(hip_source: str) -> int:
     """The iterations per machine-loop pass the emitter chose for a
     compacted while loop in `hip_source` (1 if it has none)."""
@@ -267,14 +247,12 @@ def emit_compacting_while(env: Any, cursor: Any, eqn: Any, emit_jaxpr: Any, decl
         # in any of them leaves the epoch): the pass's counter and branch are
         # shared among them.
         with cursor.block(f"for (int {ep} = 0; {ep} < {EPOCH}; {ep} += {unroll})"):
-            every = exit_every()
-            for u in range(unroll):
+            for _ in range(unroll):
                 (pred,) = emit_jaxpr(env, cursor, cj, cond_consts + carries)
                 live = cursor.fresh("_live")
                 cursor.emit(f"const bool {live} = ({pred.at('0')}) && {slot} >= 0;")
-                if u % every == 0:
-                    with cursor.block(f"if (!__any({live}))"):
-                        cursor.emit("break;")
+                with cursor.block(f"if (!__any({live}))"):
+                    cursor.emit("break;")
                 outs = emit_jaxpr(env, cursor, bj, body_consts + carries)
                 copy_back(cursor, outs, carries, predicate=live, guards=select_guards(env, bj, bn))
         # Epoch boundary: the same condition, on the state as it stands.

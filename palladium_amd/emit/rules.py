@@ -874,24 +874,23 @@ def _rule_while(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     # A predicated loop runs several iterations per pass of its machine loop,
     # each with its own exit test (a break in any of them leaves the loop),
     # as the compacting form does.
-    unroll, every = 1, 1
+    unroll = 1
     if predicated:
-        from palladium_amd.emit.compact import epoch_unroll, exit_every
+        from palladium_amd.emit.compact import epoch_unroll
 
-        unroll, every = epoch_unroll(getattr(env, "math_mode", None), bj), exit_every()
+        unroll = epoch_unroll(getattr(env, "math_mode", None), bj)
     with cursor.block("while (true)"):
         if unroll > 1:
             cursor.emit(f"// {unroll} iterations per pass")
-        for u in range(unroll):
+        for _ in range(unroll):
             (pred,) = emit_jaxpr(env, cursor, getattr(cj, "jaxpr", cj), cond_consts + carries)
             p = pred.at("0")
             if predicated:
                 # Evaluate once: the body may overwrite what the condition read.
                 live = cursor.fresh("_live")
                 cursor.emit(f"const bool {live} = {p};")
-                if u % every == 0:
-                    with cursor.block(f"if (!__any({live}))"):
-                        cursor.emit("break;")
+                with cursor.block(f"if (!__any({live}))"):
+                    cursor.emit("break;")
             else:
                 with cursor.block(f"if (!({p}))"):
                     cursor.emit("break;")

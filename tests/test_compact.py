@@ -96,10 +96,7 @@ def test_iterations_per_pass_follow_mode_and_body_size(monkeypatch):
     from palladium_amd.emit import compact
 
     spec = _bs3_spec(4096)
-    src = emit_hip(spec, math_mode="fast")
-    assert compact.iterations_per_pass(src) == 32
-    # one wavefront exit test every EXIT_EVERY iterations
-    assert src.count("if (!__any(") == 32 // compact.EXIT_EVERY
+    assert compact.iterations_per_pass(emit_hip(spec, math_mode="fast")) == 32
     assert compact.iterations_per_pass(emit_hip(spec, math_mode="safe")) == 16
     assert compact.iterations_per_pass(emit_hip(spec)) == 16
     # a body that would not fit: fewer iterations per pass
