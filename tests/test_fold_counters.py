@@ -195,3 +195,33 @@ def test_fold_fuzz_fires_on_most_planted_pairs():
         spec = trace(call, x)
         fired += bool(_dropped(spec.jaxpr, fold_counters(spec.jaxpr)))
     assert fired >= 35   # 41 of these 60 seeds plant a pair the fold can prove
+
+
+def test_fold_on_unsigned_counters_wraps_like_the_loop():
+    """uint32 counts starting near 2**32: the rebuilt count wraps exactly as
+    the carried one would have."""
+    def kernel(x_ref, a_ref, b_ref, n_ref):
+        x = x_ref[...]
+
+        def body(c):
+            v, a, b, n = c
+            p = v * 5.0 - jnp.floor(v * 5.0) < 0.5
+            one, zero = jnp.uint32(1), jnp.uint32(0)
+            return v * 0.8, a + jnp.where(p, one, zero), b + jnp.where(p, zero, one), n + jnp.uint32(1)
+
+        init = [jnp.full_like(x, c, jnp.uint32) for c in (0xFFFFFFF0, 0xFFFFFFFA, 7)]
+        _, a, b, n = lax.while_loop(lambda c: c[0] > 0.05, body, (x, *init))
+        a_ref[...], b_ref[...], n_ref[...] = a, b, n
+
+    n = 64
+    x = np.random.default_rng(2).uniform(0.1, 1.0, n).astype(np.float32)
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    call = pl.pallas_call(kernel, grid=(n,), in_specs=[s], out_specs=(s, s, s),
+                          out_shape=(pl.ShapeDtypeStruct((n,), np.uint32),) * 3)
+    spec = trace(call, x)
+    opt = dataclasses.replace(spec, jaxpr=fold_counters(spec.jaxpr))
+    assert len(_dropped(spec.jaxpr, opt.jaxpr)) == 1
+    got, want = interpret_spec(opt, x), interpret_spec(spec, x)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
+    assert (got[1] < 100).any() and (got[1] > 0xFFFFFF00).any()   # some wrapped, some not

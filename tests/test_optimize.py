@@ -484,3 +484,19 @@ def test_affine_shift_reuse_on_lv_rk4_within_fast_tolerance():
     assert opt.jaxpr.eqns != fac.eqns
     for g, w in zip(interpret_spec(opt, *args), interpret_spec(spec, *args)):
         np.testing.assert_allclose(g, w, rtol=2e-5, atol=1e-6)
+
+
+def test_affine_shift_needs_the_same_coefficient_and_offset():
+    def kernel(x_ref, y_ref, a_ref, b_ref, o_ref, p_ref):
+        x, y, a, b = x_ref[...], y_ref[...], a_ref[...], b_ref[...]
+        f0 = a - b * y                          # a - b y exists ...
+        k = x * f0
+        o_ref[...] = (a + 1.0) - b * (y + 0.5 * k)   # ... but this offset differs
+        p_ref[...] = a - x * (y + 0.5 * k)           # ... and this coefficient
+
+    v = np.linspace(1, 2, 64, dtype=np.float32)
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    call = pl.pallas_call(kernel, grid=(64,), in_specs=[s] * 4, out_specs=(s, s),
+                          out_shape=(pl.ShapeDtypeStruct((64,), np.float32),) * 2)
+    spec = trace(call, v, v, v, v)
+    assert reuse_affine_shifts(spec.jaxpr).eqns == spec.jaxpr.eqns
