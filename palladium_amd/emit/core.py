@@ -504,29 +504,37 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
     from palladium_amd.emit.compact import plan_for
     from palladium_amd.emit.optimize import fold_counters, funnel_shifts
 
+    # The launch geometry was chosen on the traced jaxpr: a rewrite that
+    # adds or removes loop carries can move a loop across the LDS budget of
+    # lane compaction, so each such rewrite is taken only if it leaves the
+    # loop's compaction as the geometry has it.
+    compacting = plan is None and geo.block == 1024 and plan_for(spec, spec.jaxpr, lanes, block) is not None
+
+    def keeps_compaction(candidate: Jaxpr) -> bool:
+        return (plan_for(spec, candidate, lanes, block) is not None) == compacting
+
     if math_mode is not None and math_mode_ordinal(math_mode) == 2:
         from palladium_amd.emit.optimize import fast_rewrites
 
-        body = fast_rewrites(body)
+        rewritten = fast_rewrites(body)
+        if keeps_compaction(rewritten):
+            body = rewritten
     elif (math_mode is not None and math_mode_ordinal(math_mode) == 0
           and os.environ.get("PALLADIUM_SHARE_POW_LOGS", "1") != "0"):
         from palladium_amd.emit.optimize import share_pow_logs
 
         shared = share_pow_logs(body)
-        # The extra carries must not cost the loop its compaction.
-        if not (plan is None and geo.block == 1024) or plan_for(spec, shared, lanes, block) is not None:
+        if keeps_compaction(shared):
             body = shared
     # Exact, every mode; after the rewrites that read the or-and-shift form.
     body = funnel_shifts(body)
     if os.environ.get("PALLADIUM_FOLD_COUNTERS", "1") != "0":
         folded = fold_counters(body)
-        # A folded count is read after the loop: one more result row in LDS,
-        # which must not cost the loop its compaction either.
-        if not (plan is None and geo.block == 1024) or plan_for(spec, folded, lanes, block) is not None:
+        if keeps_compaction(folded):
             body = folded
 
     cplan = plan_for(spec, body, lanes, block)
-    if (cplan is not None) != (plan is None and geo.block == 1024 and plan_for(spec, spec.jaxpr, lanes, block) is not None):
+    if (cplan is not None) != compacting:
         raise EmitError("internal: while-loop compaction disagrees with the launch geometry")
 
     for line in _xcd_remap(geo.blocks):

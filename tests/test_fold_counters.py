@@ -225,3 +225,56 @@ def test_fold_on_unsigned_counters_wraps_like_the_loop():
     for g, w in zip(got, want):
         np.testing.assert_array_equal(g, w)
     assert (got[1] < 100).any() and (got[1] > 0xFFFFFF00).any()   # some wrapped, some not
+
+
+def _boundary_kernel(nx):
+    """A loop carrying v, accepted, rejected and attempt counts plus `nx`
+    float carries, all read after the loop: 9 + 2 nx LDS words per lane
+    before the fold, one carry (two words) fewer after it."""
+
+    def kernel(x_ref, *outs):
+        x = x_ref[...]
+
+        def cond(c):
+            return (c[0] > 0.05) & (c[3] < 40)
+
+        def body(c):
+            v, a, b, n = c[:4]
+            fs = c[4:]
+            p = v * 7.0 - jnp.floor(v * 7.0) < 0.5
+            v = jnp.where(p, v * 0.5, v * 0.9)
+            fs = tuple(f * 0.5 + v for f in fs)
+            return (v, a + jnp.where(p, 1, 0), b + jnp.where(p, 0, 1), n + 1, *fs)
+
+        zi = jnp.zeros(x.shape, jnp.int32)
+        init = (x, zi, zi, zi, *[x * float(k + 1) for k in range(nx)])
+        res = lax.while_loop(cond, body, init)
+        for ref, val in zip(outs, res):
+            ref[...] = val
+
+    return kernel
+
+
+def test_fold_does_not_move_a_loop_across_the_compaction_budget():
+    """With six float carries the traced loop is over compaction's LDS
+    budget and the fold would bring it under; the emitter must keep the
+    launch geometry's choice (no compaction) and still emit and run."""
+    from palladium_amd.emit.compact import plan_for
+    from palladium_amd.emit.core import emit_hip, launch_geometry
+
+    nx, n = 6, 256
+    x = np.random.default_rng(5).uniform(0.0, 1.0, n).astype(np.float32)
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    shapes = (pl.ShapeDtypeStruct((n,), np.float32),) + (pl.ShapeDtypeStruct((n,), np.int32),) * 3 \
+        + (pl.ShapeDtypeStruct((n,), np.float32),) * nx
+    call = pl.pallas_call(_boundary_kernel(nx), grid=(n,), in_specs=[s], out_specs=(s,) * (4 + nx),
+                          out_shape=shapes)
+    spec = trace(call, x)
+    assert plan_for(spec, spec.jaxpr, 1, None) is None
+    assert plan_for(spec, fold_counters(spec.jaxpr), 1, None) is not None
+    assert launch_geometry(spec).block != 1024
+    for mode in ("safe", "relaxed", "fast"):
+        src = emit_hip(spec, math_mode=mode)
+        assert "__shared__" not in src
+    ref = interpret_spec(spec, [x])
+    assert int(np.sum(ref[1]) + np.sum(ref[2])) == int(np.sum(ref[3]))
