@@ -283,8 +283,8 @@ def emit_jaxpr(env: Environment, cursor: Cursor, jaxpr: Jaxpr, in_vals: list[CVa
     """
     if jaxpr.constvars:
         raise EmitError(
-            "kernel jaxpr has constvars (captured arrays); close over Python "
-            "scalars only, or pass arrays as kernel operands"
+            f"the kernel captures {len(jaxpr.constvars)} array(s) from its enclosing scope; "
+            "a kernel may close over Python scalars, and arrays must be passed in as operands"
         )
     if len(jaxpr.invars) != len(in_vals):
         raise EmitError(f"jaxpr takes {len(jaxpr.invars)} inputs, got {len(in_vals)}")
@@ -363,8 +363,8 @@ def ref_view(env: Environment, ref: CVal, indexer: NDIndexer) -> CVal:
     for d, size in kept[1:]:
         if size != indexer.shape[d]:
             raise EmitError(
-                f"ref access dim {d}: a partial Slice must be the first "
-                "kept dim; non-contiguous access is unimplemented"
+                f"ref access dim {d}: only the leading sliced dimension may take part of "
+                "its extent (strided, non-contiguous views cannot be emitted)"
             )
     offset = " + ".join(terms) or "0"
     shape = tuple(size for _, size in kept)

@@ -92,8 +92,8 @@ class _Converter:
     def jaxpr(self, j: Any) -> ir.Jaxpr:
         if j.constvars:
             raise TraceError(
-                "kernel jaxpr has constvars (captured arrays); close over Python scalars only, "
-                "or pass arrays as kernel operands"
+                f"the kernel captures {len(j.constvars)} array(s) from its enclosing scope; "
+                "a kernel may close over Python scalars, and arrays must be passed in as operands"
             )
         invars = [self.atom(v) for v in j.invars]
         eqns = []

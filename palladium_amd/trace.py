@@ -29,21 +29,15 @@ __all__ = ["BlockInfo", "KernelSpec", "trace"]
 
 @dataclasses.dataclass(frozen=True)
 class BlockInfo:
-    """One kernel operand: the block a single program instance sees.
+    """How one operand of the kernel is cut into per-instance pieces.
 
-    Attributes
-    ----------
-    block_shape : tuple of int
-        Kernel-visible block shape, squeezed dims removed.
-    array_shape : tuple of int
-        Full array shape.
-    dtype : numpy.dtype
-        Element type, shared by block and array.
-    index_map_jaxpr : ClosedJaxpr
-        Staged BlockSpec index map: grid indices to block index, in
-        units of blocks.
-    full_block_shape : tuple of int
-        Block shape with squeezed dims restored as 1 (rank of the array).
+    block_shape: the shape a kernel body indexes, with the dimensions the
+    BlockSpec marks as squeezed left out. array_shape: the whole operand in
+    HBM. dtype: the element type (block and array agree). index_map_jaxpr:
+    the BlockSpec's index map as a closed jaxpr, taking the grid indices to
+    a block index (multiply by the block shape for an element offset).
+    full_block_shape: block_shape at the array's rank, squeezed dimensions
+    restored as size 1 (None means: derive it by left-padding with 1s).
     """
 
     block_shape: tuple[int, ...]
@@ -61,20 +55,14 @@ class BlockInfo:
 
 @dataclasses.dataclass(frozen=True)
 class KernelSpec:
-    """Everything the emitter needs.
+    """A traced pallas_call, ready for the emitter.
 
-    Attributes
-    ----------
-    name : str
-        Kernel name, used as the HIP entry point name.
-    jaxpr : Jaxpr
-        The kernel body: a stateful jaxpr over Refs (inputs then outputs).
-    grid : tuple of int
-        Pallas grid; `(1,)` for gridless calls.
-    inputs, outputs : tuple of BlockInfo
-        Operand descriptions in jaxpr order.
-    raw_params : dict
-        Extra pallas_call parameters.
+    name: the entry-point symbol of the emitted HIP kernel. jaxpr: the
+    kernel body, a stateful jaxpr whose parameters are Refs, the inputs
+    first and then the outputs. grid: the program-instance grid (a gridless
+    call has grid (1,)). inputs / outputs: one BlockInfo per operand, in the
+    jaxpr's parameter order. raw_params: whatever else the pallas_call was
+    given, kept as passed.
     """
 
     name: str

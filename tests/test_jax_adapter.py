@@ -194,5 +194,5 @@ def test_captured_constants_are_rejected(fake_jax):
     from palladium_amd.jax_adapter import convert_jaxpr
 
     j = FakeJaxpr([FakeVar(FakeShaped((4,), np.float32))], [], [], [])
-    with pytest.raises(TraceError, match="constvars"):
+    with pytest.raises(TraceError, match="captures 1 array"):
         convert_jaxpr(j)
