@@ -134,16 +134,19 @@ size_t ph_noalloc_scratch_bytes(void);
  *  - `k` comes from an earlier ph_get_kernel or ph_load_code_object on the
  *    current device (emitted source carries its math mode);
  *  - operands are staged in one fixed device array of
- *    PH_NOALLOC_SCRATCH_BYTES (64 MiB) per GPU, held until the process
- *    ends, each operand at a 256-byte boundary in argument order; operands
+ *    PH_NOALLOC_SCRATCH_BYTES (64 MiB) per GPU, reserved on every GPU where
+ *    this library's code object loads (whether or not this entry point is
+ *    ever called) and held until the process ends, each operand at a 256-byte boundary in argument order; operands
  *    that do not fit are rejected with PH_ERR_INVALID_ARGUMENT before
  *    anything is queued;
  *  - output slots are cleared to zero before the launch;
  *  - the work is ordered on `stream` (NULL = default stream) and the call
  *    returns once the outputs are in the caller's host buffers.
  * Launch geometry and operand order are ph_dispatch's. Every call on one
- * GPU shares that GPU's array: calls that overlap on one GPU (other
- * threads, other streams) race and must be serialised by the caller. */
+ * GPU shares that GPU's array, so calls on one GPU are serialised by a
+ * per-GPU lock held from the first copy in to the synchronisation after the
+ * last copy out: threads that call at once wait for each other (the array
+ * belongs to this process; other processes have their own). */
 int ph_dispatch_noalloc(ph_kernel *k, int64_t grid_x, int64_t grid_y, int64_t grid_z,
                         int64_t block_x, int64_t lanes, void *stream,
                         const void *const *inputs, const size_t *input_bytes,

@@ -512,6 +512,12 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 std::mutex g_scratch_mutex;
 void *g_scratch_ptr[kMaxDevices] = {};
+// One lock per device's copy of `scratch`: a call holds it from its first
+// copy into the array to the stream synchronisation after its last copy out,
+// so calls that overlap on one GPU (threads of one process) run one after
+// another instead of overwriting each other's operands. Static storage, no
+// allocation.
+std::mutex g_scratch_use[kMaxDevices];
 
 // Looks up this device's copy of `scratch` once, with the device current.
 int scratch_address(int device, void **out, char **err) {
@@ -584,6 +590,7 @@ int ph_dispatch_noalloc(ph_kernel *k, int64_t grid_x, int64_t grid_y, int64_t gr
   if (rc != PH_OK) return rc;
   char *sbase = static_cast<char *>(base);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::mutex> in_use(g_scratch_use[device]);
   // Once work is queued, every exit waits for it: a queued copy must not
   // touch the caller's host buffers after we return.
   auto drain_and = [&](int code) {

@@ -153,3 +153,42 @@ def test_noalloc_rejects_operands_beyond_the_scratch_area():
     assert rc == rt.PH_ERR_INVALID and "operand 1" in msg
     rc, msg = _noalloc(None, attrs, args, outs)
     assert rc == rt.PH_ERR_INVALID and "null kernel" in msg
+
+
+def test_noalloc_from_eight_threads_at_once():
+    """Eight threads call the allocation-free entry point on one GPU at once,
+    each with its own inputs and stream: the per-GPU lock makes them take
+    turns on the shared scratch area, so each result equals ph_dispatch's."""
+    import threading
+
+    n, dt, steps = 20_000, 0.01, 100
+    attrs, _ = _lv_attrs(n, dt, steps)
+    kernel = _get_kernel(attrs)
+    cases = []
+    for t in range(8):
+        args = lv_inputs(n, 100 + t)
+        want = [np.empty(n, F32) for _ in range(3)]
+        _dispatch(attrs, args, want)
+        cases.append((args, want, [np.full(n, np.nan, F32) for _ in range(3)], rt.Stream()))
+    print(f"[noalloc] 8 threads, lv_rk4 SAFE n={n} steps={steps}", flush=True)
+    barrier = threading.Barrier(8)
+    results = [None] * 8
+
+    def run(t):
+        args, _, got, stream = cases[t]
+        barrier.wait()
+        for _ in range(3):
+            results[t] = _noalloc(kernel, attrs, args, got, stream.handle)
+            if results[t][0]:
+                return
+
+    threads = [threading.Thread(target=run, args=(t,)) for t in range(8)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in threads)
+    for t, (args, want, got, _) in enumerate(cases):
+        assert results[t][0] == 0, results[t][1]
+        for g, w in zip(got, want):
+            np.testing.assert_array_equal(g, w)
