@@ -106,6 +106,15 @@ def _declare_more(L):
     L.oracle_pow_log_many.argtypes = [l, _F, ctypes.POINTER(ctypes.c_double)]
     L.oracle_pow_log_many.restype = None
     L.oracle_bs3_vdp.argtypes = [l, _F, _F, _F, f, f, f, f, l, _F, _F, _F, _I, _I]
+    L.oracle_bs3_vdp_r.argtypes = [l, _F, _F, _F, f, f, f, f, l, _F, _F, _F, _I, _I]
+    L.oracle_rpow.argtypes = [f, f]
+    L.oracle_rpow.restype = f
+    L.oracle_rpow_many.argtypes = [l, _F, _F, _F]
+    L.oracle_rpow_many.restype = None
+    L.oracle_rpow_log.argtypes = [f]
+    L.oracle_rpow_log.restype = ctypes.c_double
+    L.oracle_rdiv.argtypes = [f, f]
+    L.oracle_rdiv.restype = f
     L.oracle_gray_scott_step.argtypes = [l, _F, _F, f, f, f, f, f, _F, _F]
     L.oracle_gray_scott.argtypes = [l, l, _F, _F, _F, _F, f, f, f, f, f]
     L.oracle_df32_add.argtypes = [l] + [_F] * 6
@@ -144,15 +153,38 @@ def pow_log(x: np.ndarray) -> np.ndarray:
     return out
 
 
-def bs3_vdp(x0, v0, mu, cfg):
+def bs3_vdp(x0, v0, mu, cfg, mode: str = "safe"):
+    """(t, x, v, accepted, rejected) of the adaptive loop: SAFE order
+    (`mode="safe"`), or the REPRODUCIBLE mode's fused and reciprocal form
+    (`mode="reproducible"`)."""
     n = x0.size
     outs = [np.empty(n, np.float32) for _ in range(3)] + [np.empty(n, np.int32) for _ in range(2)]
     a = [np.ascontiguousarray(v, np.float32) for v in (x0, v0, mu)]
     f32 = lambda v: float(np.float32(v))  # noqa: E731
-    _lib2().oracle_bs3_vdp(n, *[_fp(v) for v in a], f32(cfg.t1), f32(cfg.dt0), f32(cfg.rtol), f32(cfg.atol),
-                           int(cfg.max_attempts), _fp(outs[0]), _fp(outs[1]), _fp(outs[2]),
-                           outs[3].ctypes.data_as(_I), outs[4].ctypes.data_as(_I))
+    fn = {"safe": _lib2().oracle_bs3_vdp, "reproducible": _lib2().oracle_bs3_vdp_r}[mode]
+    fn(n, *[_fp(v) for v in a], f32(cfg.t1), f32(cfg.dt0), f32(cfg.rtol), f32(cfg.atol),
+       int(cfg.max_attempts), _fp(outs[0]), _fp(outs[1]), _fp(outs[2]),
+       outs[3].ctypes.data_as(_I), outs[4].ctypes.data_as(_I))
     return tuple(outs)
+
+
+def rpow(x, y) -> np.ndarray:
+    """The REPRODUCIBLE mode's power, elementwise over float32 arrays."""
+    x, y = np.broadcast_arrays(np.asarray(x, np.float32), np.asarray(y, np.float32))
+    x = np.ascontiguousarray(x.ravel())
+    y = np.ascontiguousarray(y.ravel())
+    out = np.empty(x.size, np.float32)
+    _lib2().oracle_rpow_many(x.size, _fp(x), _fp(y), _fp(out))
+    return out
+
+
+def rdiv(a: float, b: float) -> np.float32:
+    """The REPRODUCIBLE mode's division, a * RN(1/b)."""
+    return np.float32(_lib2().oracle_rdiv(float(a), float(b)))
+
+
+def rpow_log(x: float) -> float:
+    return float(_lib2().oracle_rpow_log(float(x)))
 
 
 def _gs_consts(cfg):

@@ -322,6 +322,165 @@ void oracle_bs3_vdp(long n, const float *x0, const float *v0, const float *mu_in
 }
 
 /* ------------------------------------------------------------------------
+ * REPRODUCIBLE math mode (palladium_amd/emit/prelude.py, PH_MATH_MODE 3):
+ * division a / b is a * RN(1/b); pow is the fast deterministic power below.
+ * The device reaches RN(1/b) by a Newton step from the hardware estimate
+ * (IEEE division where the result is not a normal number); the host divides
+ * (the device sequence is checked against the IEEE quotient on every
+ * float).
+ * ---------------------------------------------------------------------- */
+float oracle_rdiv(float a, float b) { return a * (1.0f / b); }
+
+/* log2 x for a positive normal float x from its bits: x = m 2^e with m in
+   [m0, 2 m0), m0 = 0x1.6a09e6p-1 (the float just above sqrt(1/2)),
+   t = (m - 1) r with r ~ 1/(m + 1) from the quadratic R and two Newton
+   steps, log2 m = t P(t^2) with P of degree 4, log2 x = e + t P by one fma
+   (coefficients: oracle/gen_rpow_coeffs.py). */
+double oracle_rpow_log(float x) {
+  uint32_t bits;
+  memcpy(&bits, &x, 4);
+  uint32_t ix = bits - 0x3f3504f3u;
+  int e = (int32_t)ix >> 23;
+  uint32_t mb = (ix & 0x007fffffu) + 0x3f3504f3u;
+  float m;
+  memcpy(&m, &mb, 4);
+  double dm = (double)m;
+  double d = dm + 1.0;
+  double r = fma(d, 0.116862893757792, -0.722444125812821);
+  r = fma(r, d, 1.4777559273698688);
+  double q = fma(-d, r, 1.0);
+  r = fma(r, q, r);
+  q = fma(-d, r, 1.0);
+  r = fma(r, q, r);
+  double t = (dm - 1.0) * r;
+  double s = t * t;
+  double p = fma(s, 0.3407120415619086, 0.41167376623771057);
+  p = fma(p, s, 0.5770835660048659);
+  p = fma(p, s, 0.9617966734515485);
+  p = fma(p, s, 2.885390081789987);
+  return fma(t, p, (double)e);
+}
+
+/* 2^z, z = k + r with |r| <= 1/2: Q(r) of degree 7 as two Horner halves
+   joined by one fma with r^4, then scaled by 2^k. */
+static double oracle_rexp2(double z) {
+  double kd = rint(z);
+  double r = z - kd;
+  double r2 = r * r;
+  double lo = fma(r, 0.055504109063258665, 0.24022651213498092);
+  double hi = fma(r, 1.5303700711365693e-05, 0.00015469729214118296);
+  lo = fma(lo, r, 0.6931471805568324);
+  hi = fma(hi, r, 0.0013333478473685416);
+  double r4 = r2 * r2;
+  lo = fma(lo, r, 0.9999999999595618);
+  hi = fma(hi, r, 0.009618025613318034);
+  return ldexp(fma(hi, r4, lo), (int)kd);
+}
+
+/* x^y given lg = oracle_rpow_log(x): 2^(y lg) rounded once to float for a
+   positive normal x and |y| < 8192; oracle_pow (with the C99 special
+   cases) for every other operand. */
+float oracle_rpow_with_log(float x, float y, double lg) {
+  int normal_x = x >= 0x1p-126f && x <= 0x1.fffffep127f;
+  if (!normal_x || !(fabsf(y) < 8192.0f)) return oracle_pow(x, y);
+  return (float)oracle_rexp2((double)y * lg);
+}
+
+float oracle_rpow(float x, float y) { return oracle_rpow_with_log(x, y, oracle_rpow_log(x)); }
+
+void oracle_rpow_many(long n, const float *x, const float *y, float *out) {
+  for (long i = 0; i < n; ++i) out[i] = oracle_rpow(x[i], y[i]);
+}
+
+/* ------------------------------------------------------------------------
+ * The adaptive BS3(2)+PI Van der Pol loop of oracle_bs3_vdp under the
+ * REPRODUCIBLE mode: the same statements, with fmaf wherever the emitter's
+ * product contraction (palladium_amd/emit/optimize.py:contract_products)
+ * fuses a single-use product into its add or subtract, both error-norm
+ * divisions and the reciprocal as a * RN(1/b), and the fast pow. Fused
+ * sites, in the kernel's order:
+ *   stage states      x + h k         -> fmaf(h, k, x)
+ *   right-hand side   1 - x*x         -> fmaf(-x, x, 1)
+ *                     (mu a) v - x    -> fmaf(mu a, v, -x)
+ *   weighted sums     p1 + c2 k2      -> fmaf(c2, k2, p1), and so on
+ *   updates           x + dt s        -> fmaf(dt, s, x)
+ *   tolerance         atol + rtol|y|  -> fmaf(rtol, |y|, atol)
+ * ---------------------------------------------------------------------- */
+static inline void vdp_rhs_r(float mu, float x, float v, float *fx, float *fv) {
+  float a = fmaf(-x, x, 1.0f);
+  float b = mu * a;
+  *fx = v;
+  *fv = fmaf(b, v, -x);
+}
+
+void oracle_bs3_vdp_r(long n, const float *x0, const float *v0, const float *mu_in,
+                      float t1, float dt0, float rtol, float atol, long max_attempts,
+                      float *to, float *xo, float *vo, int32_t *acc_out, int32_t *rej_out) {
+  const float coeff1 = (float)((0.3 + 0.4) / 3.0);
+  const float coeff2 = (float)(-0.4 / 3.0);
+  const float b1 = (float)(2.0 / 9.0), b2 = (float)(1.0 / 3.0), b3 = (float)(4.0 / 9.0);
+  const float e1 = (float)(7.0 / 24.0), e2 = 0.25f, e3 = (float)(1.0 / 3.0), e4 = 0.125f;
+#pragma omp parallel for schedule(dynamic, 64)
+  for (long i = 0; i < n; ++i) {
+    const float mu = mu_in[i];
+    float x = x0[i], v = v0[i];
+    float t = 0.0f, dt = dt0, prev = 1.0f;
+    double prev_log = oracle_rpow_log(1.0f);
+    float k1x, k1v;
+    vdp_rhs_r(mu, x, v, &k1x, &k1v);
+    int32_t acc = 0, rej = 0, it = 0;
+    while (t < t1 && it < max_attempts) {
+      float rem = t1 - t;
+      dt = fminf(dt, rem);
+      float h = 0.5f * dt;
+      float xa = fmaf(h, k1x, x), va = fmaf(h, k1v, v);
+      float k2x, k2v;
+      vdp_rhs_r(mu, xa, va, &k2x, &k2v);
+      h = 0.75f * dt;
+      xa = fmaf(h, k2x, x);
+      va = fmaf(h, k2v, v);
+      float k3x, k3v;
+      vdp_rhs_r(mu, xa, va, &k3x, &k3v);
+      float sx = b1 * k1x; sx = fmaf(b2, k2x, sx); sx = fmaf(b3, k3x, sx);
+      float x3 = fmaf(dt, sx, x);
+      float sv = b1 * k1v; sv = fmaf(b2, k2v, sv); sv = fmaf(b3, k3v, sv);
+      float v3 = fmaf(dt, sv, v);
+      float k4x, k4v;
+      vdp_rhs_r(mu, x3, v3, &k4x, &k4v);
+      float qx = e1 * k1x; qx = fmaf(e2, k2x, qx); qx = fmaf(e3, k3x, qx); qx = fmaf(e4, k4x, qx);
+      float x2 = fmaf(dt, qx, x);
+      float qv = e1 * k1v; qv = fmaf(e2, k2v, qv); qv = fmaf(e3, k3v, qv); qv = fmaf(e4, k4v, qv);
+      float v2 = fmaf(dt, qv, v);
+      float ex = x3 - x2, ev = v3 - v2;
+      float nx = oracle_rdiv(fabsf(ex), fmaf(rtol, fabsf(x3), atol));
+      float nv = oracle_rdiv(fabsf(ev), fmaf(rtol, fabsf(v3), atol));
+      float err = fmaxf(nx, nv);
+      int accept = err <= 1.0f;
+      float tn = t + dt;
+      float t2 = accept ? tn : t;
+      float xn = accept ? x3 : x;
+      float vn = accept ? v3 : v;
+      float kx = accept ? k4x : k1x;
+      float kv = accept ? k4v : k1v;
+      err = fmaxf(err, 1e-9f);
+      float inv = oracle_rdiv(1.0f, err);
+      double inv_log = oracle_rpow_log(inv);
+      float f = 0.9f * oracle_rpow_with_log(inv, coeff1, inv_log);
+      f = f * oracle_rpow_with_log(prev, coeff2, prev_log);
+      float pn = accept ? inv : prev;
+      double pln = accept ? inv_log : prev_log;
+      float cl = fminf(10.0f, fmaxf(0.2f, f));
+      dt = dt * cl;
+      acc = acc + (accept ? 1 : 0);
+      rej = rej + (accept ? 0 : 1);
+      it = it + 1;
+      t = t2; x = xn; v = vn; k1x = kx; k1v = kv; prev = pn; prev_log = pln;
+    }
+    to[i] = t; xo[i] = x; vo[i] = v; acc_out[i] = acc; rej_out[i] = rej;
+  }
+}
+
+/* ------------------------------------------------------------------------
  * One Gray-Scott explicit Euler step on an n x n periodic grid, one cell per
  * index, as examples/04_reaction_diffusion.py:61-74: five-point Laplacian
  * ((((u[ip,j] + u[im,j]) + u[i,jp]) + u[i,jm]) - 4u), uvv = (u v) v,

@@ -45,11 +45,13 @@ int hip_fail(char **err, hipError_t e, const char *what) {
                   hipGetErrorString(e) + ")");
 }
 
-const char *kOptions[3] = {
+const char *kOptions[4] = {
     "-ffp-contract=off",
     "-ffp-contract=fast",
     "-ffp-contract=fast -ffast-math -fno-finite-math-only -fgpu-flush-denormals-to-zero "
     "-fno-hip-fp32-correctly-rounded-divide-sqrt",
+    // REPRODUCIBLE: the emitter writes every fused multiply-add itself.
+    "-ffp-contract=off",
 };
 
 std::vector<std::string> build_options(int math_mode, const char *arch) {
@@ -84,7 +86,7 @@ std::vector<std::string> build_options(int math_mode, const char *arch) {
 
 int compile(const char *src, size_t src_len, const char *name, int math_mode,
             const char *arch, std::vector<char> *code, char **err) {
-  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_FAST)
+  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_REPRODUCIBLE)
     return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip: math_mode out of range");
   std::string source(src, src_len);
   std::string fname = std::string(name ? name : "kernel") + ".hip";
@@ -210,7 +212,7 @@ int ph_compile_code_object(const char *src, size_t src_len, const char *name,
 void ph_free_code_object(void *code) { std::free(code); }
 
 const char *ph_compile_options(int math_mode) {
-  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_FAST) return "";
+  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_REPRODUCIBLE) return "";
   return kOptions[math_mode];
 }
 
@@ -218,7 +220,7 @@ int ph_get_kernel(const char *src, size_t src_len, const char *name,
                   int math_mode, ph_kernel **out, char **err) {
   if (!src || !name || !out)
     return fail(err, PH_ERR_INVALID_ARGUMENT, "ph_get_kernel: null argument");
-  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_FAST)
+  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_REPRODUCIBLE)
     return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip: math_mode out of range");
   return KernelCache::instance().get(src, src_len, name, math_mode, out, err);
 }
@@ -277,7 +279,7 @@ namespace {
 int dispatch_geometry(int64_t grid_x, int64_t grid_y, int64_t grid_z, int64_t block_x,
                       int64_t lanes, int64_t math_mode, unsigned int *blocks,
                       unsigned int *block, char **err) {
-  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_FAST)
+  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_REPRODUCIBLE)
     return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: math_mode out of range");
   if (grid_x <= 0 || grid_y <= 0 || grid_z <= 0)
     return fail(err, PH_ERR_INVALID_ARGUMENT, "palladium_hip_dispatch: grid dims must be positive");

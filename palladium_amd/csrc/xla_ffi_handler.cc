@@ -33,7 +33,7 @@ xla::ffi::Error PalladiumHipDispatch(std::string_view hip_source,
                                      int64_t lanes, int64_t math_mode,
                                      xla::ffi::RemainingArgs args,
                                      xla::ffi::RemainingRets rets) {
-  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_FAST)
+  if (math_mode < PH_MATH_SAFE || math_mode > PH_MATH_REPRODUCIBLE)
     return xla::ffi::Error::InvalidArgument(
         "palladium_hip_dispatch: math_mode out of range");
   std::vector<const void *> in_ptrs;

@@ -92,7 +92,7 @@ def epoch_unroll(math_mode: Any = None, body: Any = None) -> int:
         if u < 1 or EPOCH % u:
             raise ValueError(f"PALLADIUM_EPOCH_UNROLL={u} must divide the epoch of {EPOCH} iterations")
         return u
-    safe = math_mode is None or math_mode_ordinal(math_mode) == 0
+    safe = math_mode is None or math_mode_ordinal(math_mode) in (0, 3)
     u = EPOCH_UNROLL["safe" if safe else "other"]
     n = _count_eqns(getattr(body, "jaxpr", body)) if body is not None else 0
     while u > 1 and u * n > EPOCH_UNROLL_OPS:

@@ -466,7 +466,8 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
     (`T* __restrict__`), and nothing else; the grid and block shapes are
     compile-time constants of the source. With `math_mode` FAST the jaxpr
     first goes through the FAST-only algebraic rewrites of
-    `palladium_amd.emit.optimize`.
+    `palladium_amd.emit.optimize`; with REPRODUCIBLE, through its exact
+    product contraction (`contract_products`).
 
     Raises
     ------
@@ -519,13 +520,17 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         rewritten = fast_rewrites(body)
         if keeps_compaction(rewritten):
             body = rewritten
-    elif (math_mode is not None and math_mode_ordinal(math_mode) == 0
+    elif (math_mode is not None and math_mode_ordinal(math_mode) in (0, 3)
           and os.environ.get("PALLADIUM_SHARE_POW_LOGS", "1") != "0"):
         from palladium_amd.emit.optimize import share_pow_logs
 
         shared = share_pow_logs(body)
         if keeps_compaction(shared):
             body = shared
+    if math_mode is not None and math_mode_ordinal(math_mode) == 3:
+        from palladium_amd.emit.optimize import contract_products
+
+        body = contract_products(body)
     # Exact, every mode; after the rewrites that read the or-and-shift form.
     body = funnel_shifts(body)
     if os.environ.get("PALLADIUM_FOLD_COUNTERS", "1") != "0":

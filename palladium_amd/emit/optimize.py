@@ -46,7 +46,7 @@ import numpy as np
 
 from palladium_amd.ir import ClosedJaxpr, Jaxpr, JaxprEqn, Literal, ShapedArray, Var, primitive
 
-__all__ = ["carry_logs", "drop_redundant_clamps", "factor_common_products", "fast_rewrites", "funnel_shifts",
+__all__ = ["carry_logs", "contract_products", "drop_redundant_clamps", "factor_common_products", "fast_rewrites", "funnel_shifts",
            "power_laws_to_exp2", "reuse_affine_shifts", "share_pow_logs", "fold_counters"]
 
 
@@ -876,3 +876,66 @@ def _fold_counters_while(e: JaxprEqn) -> tuple[JaxprEqn, list[JaxprEqn]]:
     k = cn + bn + j
     outs = e.outvars[:j] + e.outvars[j + 1:]
     return JaxprEqn(e.invars[:k] + e.invars[k + 1:], outs, e.primitive, params), post
+
+
+def _product_operands(e: JaxprEqn) -> tuple[Any, Any] | None:
+    """(a, b) when `e` computes a * b: a mul, or integer_pow with y = 2."""
+    if e.primitive.name == "mul" and len(e.invars) == 2:
+        return e.invars[0], e.invars[1]
+    if e.primitive.name == "integer_pow" and int(e.params.get("y", 0)) == 2:
+        return e.invars[0], e.invars[0]
+    return None
+
+
+def contract_products(jaxpr: Jaxpr) -> Jaxpr:
+    """REPRODUCIBLE: fuse a float32 product into the add or subtract that is
+    its only use,
+
+        a*b + c  ->  fma(a, b, c)        c + a*b  ->  fma(a, b, c)
+        a*b - c  ->  fma(a, b, -c)       c - a*b  ->  fma(-a, b, c)
+
+    with `x**2` read as x*x. When both operands of the add are such
+    products, the one computed later in the program is fused (it is the one
+    the sum waits for), so a chain `(p1 + p2) + p3` becomes
+    fma(p3, fma(p2, p1)). The sites are a function of the program alone,
+    and each fma is correctly rounded, so a host restatement that writes
+    C `fmaf` at the same sites reproduces the device bit for bit. Negation
+    is exact, so the signs are carried as parameters `neg_ab`, `neg_c`."""
+    producer = {ov: e for e in jaxpr.eqns for ov in e.outvars}
+    order = {id(e): k for k, e in enumerate(jaxpr.eqns)}
+    uses = _use_counts(jaxpr)
+    f32 = np.dtype(np.float32)
+
+    def is_f32(v: Any) -> bool:
+        return np.dtype(getattr(v.aval, "dtype", np.float64)) == f32
+
+    fused: set = set()
+    new_eqns: list[JaxprEqn] = []
+    for e in jaxpr.eqns:
+        params = {k: _rewrite_sub(v, contract_products) for k, v in e.params.items()}
+        e = JaxprEqn(e.invars, e.outvars, e.primitive, params)
+        name = e.primitive.name
+        out = e.outvars[0] if len(e.outvars) == 1 else None
+        if name in ("add", "sub") and out is not None and is_f32(out) and len(e.invars) == 2:
+            best = None
+            for side, v in enumerate(e.invars):
+                pe = producer.get(v) if isinstance(v, Var) else None
+                if pe is None or uses.get(v, 0) != 1 or v in fused:
+                    continue
+                ab = _product_operands(pe)
+                if ab is None or not is_f32(v) or tuple(v.aval.shape) != tuple(out.aval.shape):
+                    continue
+                if best is None or order[id(pe)] > best[0]:
+                    best = (order[id(pe)], side, v, ab)
+            if best is not None:
+                _, side, v, (a, b) = best
+                other = e.invars[1 - side]
+                neg_ab = name == "sub" and side == 1
+                neg_c = name == "sub" and side == 0
+                fused.add(v)
+                new_eqns.append(JaxprEqn([a, b, other], [out], primitive("fma"),
+                                         {"neg_ab": neg_ab, "neg_c": neg_c}))
+                continue
+        new_eqns.append(e)
+    new_eqns = [e for e in new_eqns if not (len(e.outvars) == 1 and e.outvars[0] in fused)]
+    return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)

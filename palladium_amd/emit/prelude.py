@@ -16,6 +16,15 @@
   2^z by z = k + r, |r| <= 1/2, and a degree-10 polynomial in r; both
   carried in double, so the float result is the double value rounded once
   (correctly rounded on every sampled argument).
+- `ph_rrcp`/`ph_rdiv`/`ph_rpow` (REPRODUCIBLE, `PH_MATH_MODE == 3`): the
+  reciprocal correctly rounded from the hardware estimate by one Newton
+  step (IEEE division, in a branch, for the divisors whose reciprocal is
+  not a normal number), `a / b` as `a * RN(1/b)`, and a fast deterministic power:
+  for a positive normal base and |y| < 8192, log2 x from the float's bits
+  (x = m 2^e, m in [sqrt(1/2), sqrt(2)), t = (m-1)/(m+1) by a quadratic
+  start and two Newton steps, a degree-4 polynomial in t^2) and 2^z
+  (z = k + r, a degree-7 polynomial in r), in double; any other operand takes the SAFE `ph_pow` in a branch that a
+  wavefront enters only when one of its lanes needs it.
 - `ph_exp2`/`ph_log2`: under FAST the hardware base-2 exponential and
   logarithm; libm otherwise.
 - `ph_sin`/`ph_cos`: under FAST the hardware sine/cosine (the reference's
@@ -104,7 +113,7 @@ __device__ __forceinline__ float ph_expm1(float x) { return x == 0.0f ? x : expm
 __device__ __forceinline__ float ph_fmin(float a, float b) { return fminf(a, b); }
 __device__ __forceinline__ float ph_fmax(float a, float b) { return fmaxf(a, b); }
 
-#if PH_MATH_MODE == 0
+#if PH_MATH_MODE == 0 || PH_MATH_MODE == 3
 /* a * b + c, correctly rounded (one v_fma_f64), with the constant c read
    from scalar registers. Written out because the compiler otherwise keeps
    polynomial coefficients in vector registers and copies each into the
@@ -210,6 +219,106 @@ __device__ __forceinline__ float ph_pow_with_log(float x, float y, double lg) {
 }
 
 __device__ __forceinline__ float ph_pow(float x, float y) { return ph_pow_with_log(x, y, ph_pow_log(x)); }
+#endif
+#if PH_MATH_MODE == 3
+/* RN(1/b) for every float b. The hardware estimate (within 1 ulp) and one
+   Newton step y + y (1 - b y), the residual exact in the inner FMA, give
+   the correctly rounded reciprocal whenever the result is a normal
+   number. Any other result (b zero, subnormal, infinite or NaN, or
+   |b| >= 2^126, where 1/b is subnormal) is redone by IEEE division, in a
+   branch a wavefront takes only when one of its lanes needs it (the empty
+   asm keeps the wavefront mask an opaque scalar: one compare and one
+   scalar branch on the common path). Checked against the IEEE quotient on
+   every float on the device. */
+__device__ __noinline__ float ph_rrcp_slow(float b) { return 1.0f / b; }
+
+/* The wavefront mask of lanes whose x is in one of the classes `mask`
+   selects (v_cmp_class bits: 0 sNaN, 1 qNaN, 2 -inf, 3 -normal, 4 -subnormal,
+   5 -0, 6 +0, 7 +subnormal, 8 +normal, 9 +inf), as a scalar: written straight
+   into a scalar register pair, so testing it costs one vector compare and
+   a scalar branch (through a bool and a ballot the compiler spends a
+   select and a second compare). Inactive lanes read 0. */
+__device__ __forceinline__ unsigned long long ph_class_mask(float x, unsigned int mask) {
+    unsigned long long m;
+    __asm__ volatile("v_cmp_class_f32_e64 %0, %1, %2" : "=s"(m) : "v"(x), "s"(mask));
+    return m;
+}
+
+__device__ __forceinline__ float ph_rrcp(float b) {
+    float y = __builtin_amdgcn_rcpf(b);
+    float e = __builtin_fmaf(-b, y, 1.0f);
+    y = __builtin_fmaf(e, y, y);
+    if (__builtin_expect(ph_class_mask(y, 0x2f7) != 0ull, 0))   /* a lane not -normal, not +normal */
+        y = __builtin_amdgcn_classf(y, 0x2f7) ? ph_rrcp_slow(b) : y;
+    return y;
+}
+
+__device__ __forceinline__ float ph_rdiv(float a, float b) { return a * ph_rrcp(b); }
+
+/* log2 x for a positive normal float x; any other x gives a finite or NaN
+   value that ph_rpow_with_log never uses. The exponent split works on the
+   bits: x = m 2^e with m in [m0, 2 m0), m0 = 0x1.6a09e6p-1 (the float just
+   above sqrt(1/2)); t = (m - 1) r with r ~ 1/(m + 1) from a quadratic start
+   (relative error 2^-9.6) and two Newton steps (2^-38); log2 m = t P(t^2)
+   with P of degree 4, log2 x = e + t P by one FMA. Every step is a
+   correctly rounded double operation, so the host repeats it exactly.
+   Coefficients: oracle/gen_rpow_coeffs.py. */
+__device__ __forceinline__ double ph_rpow_log(float x) {
+    unsigned int ix = __float_as_uint(x) - 0x3f3504f3u;
+    int e = (int)ix >> 23;
+    float m = __uint_as_float((ix & 0x007fffffu) + 0x3f3504f3u);
+    double dm = (double)m;
+    double d = dm + 1.0;
+    double r = ph_fma_k(d, 0.116862893757792, -0.722444125812821);
+    r = ph_fma_k(r, d, 1.4777559273698688);
+    double q = fma(-d, r, 1.0);
+    r = fma(r, q, r);
+    q = fma(-d, r, 1.0);
+    r = fma(r, q, r);
+    double t = (dm - 1.0) * r;
+    double s = t * t;
+    double p = ph_fma_k(s, 0.3407120415619086, 0.41167376623771057);
+    p = ph_fma_k(p, s, 0.5770835660048659);
+    p = ph_fma_k(p, s, 0.9617966734515485);
+    p = ph_fma_k(p, s, 2.885390081789987);
+    return fma(t, p, (double)e);
+}
+
+/* 2^z for |z| < 2^21: z = k + r, |r| <= 1/2, Q(r) of degree 7 as two
+   Horner halves (degrees 0-3 and 4-7, independent chains) joined by one
+   FMA with r^4. */
+__device__ __forceinline__ double ph_rexp2(double z) {
+    double kd = __builtin_rint(z);
+    double r = z - kd;
+    double r2 = r * r;
+    double lo = ph_fma_k(r, 0.055504109063258665, 0.24022651213498092);
+    double hi = ph_fma_k(r, 1.5303700711365693e-05, 0.00015469729214118296);
+    lo = ph_fma_k(lo, r, 0.6931471805568324);
+    hi = ph_fma_k(hi, r, 0.0013333478473685416);
+    double r4 = r2 * r2;
+    lo = ph_fma_k(lo, r, 0.9999999999595618);
+    hi = ph_fma_k(hi, r, 0.009618025613318034);
+    return __builtin_ldexp(fma(hi, r4, lo), (int)kd);
+}
+
+__device__ __noinline__ float ph_rpow_slow(float x, float y) { return ph_pow(x, y); }
+
+/* x^y given lg = ph_rpow_log(x). For a positive normal x and |y| < 8192,
+   |z| = |y lg| < 2^20 and 2^z rounded once to float (ldexp in double keeps
+   overflow to inf and underflow to subnormals and zero exact until then).
+   Any other operand (zero, subnormal, negative, infinite or NaN x; large,
+   infinite or NaN y) takes the SAFE pow with its C99 special cases, in a
+   branch taken only by wavefronts holding such a lane. */
+__device__ __forceinline__ float ph_rpow_with_log(float x, float y, double lg) {
+    float r = (float)ph_rexp2((double)y * lg);
+    bool wide_y = !(__builtin_fabsf(y) < 8192.0f);   /* folds away for a literal exponent */
+    unsigned long long any = ph_class_mask(x, 0x2ff) | __builtin_amdgcn_ballot_w64(wide_y);
+    if (__builtin_expect(any != 0ull, 0))
+        r = (__builtin_amdgcn_classf(x, 0x2ff) || wide_y) ? ph_rpow_slow(x, y) : r;
+    return r;
+}
+
+__device__ __forceinline__ float ph_rpow(float x, float y) { return ph_rpow_with_log(x, y, ph_rpow_log(x)); }
 #elif PH_MATH_MODE == 2
 /* FAST: x^y = 2^(y log2 x) on the hardware base-2 logarithm and
    exponential (v_log_f32, v_exp_f32) for a positive normal finite base and
@@ -220,7 +329,7 @@ __device__ __forceinline__ float ph_pow(float x, float y) {
         return __builtin_amdgcn_exp2f(y * __builtin_amdgcn_logf(x));
     return powf(x, y);
 }
-#else
+#elif PH_MATH_MODE == 1
 __device__ __forceinline__ float ph_pow(float x, float y) { return powf(x, y); }
 #endif
 """

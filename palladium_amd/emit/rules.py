@@ -29,11 +29,13 @@ from palladium_amd.emit.core import (
     element_strides,
     emit_jaxpr,
     flat_index,
+    format_float,
     literal_cval,
     ref_view,
     rule,
 )
-from palladium_amd.ir import JaxprEqn, KeyAval, Var
+from palladium_amd.ir import JaxprEqn, KeyAval, Literal, Var
+from palladium_amd.runtime import REPRODUCIBLE_ORDINAL, math_mode_ordinal
 
 F32 = "float"
 F16 = "_Float16"
@@ -190,6 +192,21 @@ def _round_to_even(eqn: JaxprEqn) -> bool:
     return int(eqn.params.get("rounding_method", 0)) == 1
 
 
+# REPRODUCIBLE float32 forms (palladium_amd.runtime.MathMode): division as a
+# times the correctly rounded reciprocal, and the fast deterministic power.
+_REPRODUCIBLE_F32 = {
+    "div": "ph_rdiv({a}, {b})",
+    "pow": "ph_rpow({a}, {b})",
+    "pow_log": "ph_rpow_log({a})",
+    "pow_with_log": "ph_rpow_with_log({a}, {b}, {c})",
+}
+
+
+def _reproducible(env: Environment) -> bool:
+    mode = getattr(env, "math_mode", None)
+    return mode is not None and math_mode_ordinal(mode) == REPRODUCIBLE_ORDINAL
+
+
 def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
     """All pure element-wise primitives (reference: `_rule_elementwise`,
     `src/palladium/emit/rules.py:274-351`). integer_pow expands to repeated
@@ -235,6 +252,19 @@ def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
             for k in reversed(range(n - 1)):
                 expr = "(({a} <= %d) ? {%s} : %s)" % (k, fields[k], expr)
             template = expr
+    elif opname == "fma":
+        if dst_ctype != F32:
+            raise EmitError("fma is emitted for float32 only")
+        na = "-" if eqn.params.get("neg_ab") else ""
+        nc = "-" if eqn.params.get("neg_c") else ""
+        template = f"__builtin_fmaf({na}{{a}}, {{b}}, {nc}{{c}})"
+    elif _reproducible(env) and opname in _REPRODUCIBLE_F32 and ops and ops[0].ctype == F32:
+        template = _REPRODUCIBLE_F32[opname]
+        if opname == "div" and isinstance(eqn.invars[1], Literal) and np.shape(eqn.invars[1].val) == ():
+            # a * RN(1/c) with the reciprocal of a literal divisor rounded here
+            recip = np.float32(1.0) / np.float32(eqn.invars[1].val)
+            template = f"({{a}} * {format_float(float(recip))})"
+            ops = ops[:1]
     else:
         template = _tmpl(opname, ops, dst_ctype)
 
@@ -261,7 +291,7 @@ def _rule_elementwise(env: Environment, cursor: Cursor, eqn: JaxprEqn) -> None:
 
 
 for _name in [*ELEMENTWISE, "integer_pow", "convert_element_type", "bitcast_convert_type", "select_n",
-              "pow_log", "pow_with_log", "alignbit"]:
+              "pow_log", "pow_with_log", "alignbit", "fma"]:
     RULES[_name] = _rule_elementwise
 
 

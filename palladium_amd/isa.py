@@ -131,19 +131,56 @@ def parse(asm: str) -> list[Instr]:
     return out
 
 
+def _hot_trace(instrs: list[Instr], head: int, latch: int, index: dict[int, int]) -> list[Instr] | None:
+    """The instructions one iteration of the loop [head, latch] issues when
+    every conditional branch falls through (the common path: a wavefront
+    skips its rarely-entered cold blocks and stays in the loop) and every
+    unconditional branch is followed; None when that path does not come
+    back to `latch` (a branch into another loop, or out)."""
+    out: list[Instr] = []
+    seen: set[int] = set()
+    k = head
+    while 0 <= k < len(instrs) and k not in seen:
+        seen.add(k)
+        ins = instrs[k]
+        out.append(ins)
+        if k == latch:
+            return out
+        if ins.op == "s_branch" and ins.target is not None:
+            nxt = index.get(ins.target)
+            if nxt is None:
+                return None
+            k = nxt
+        elif ins.op.startswith(("s_endpgm", "s_setpc")):
+            return None
+        else:
+            k += 1
+    return None
+
+
 def loop_body(instrs: list[Instr]) -> list[Instr]:
-    """The hot loop's body. Of the spans from a backward branch's target to
-    the branch holding at least a quarter of the vector instructions of the
-    largest such span, the shortest: an epoch loop around the hot loop is
-    longer, and the short backward branch a
-    `while (true) { if (!any(live)) break; ... }` loop compiles to on its
-    exit path holds too little."""
+    """The hot loop's body: the common path (see `_hot_trace`) of a loop
+    whose back-edge that path returns to, so blocks the compiler placed out
+    of line for rarely-taken branches, and loops around the hot one, are
+    left out. Of several such loops, the shortest holding at least a
+    quarter of the vector instructions of the largest. Without any, the
+    contiguous span from a backward branch's target to the branch, chosen
+    the same way."""
+    index = {x.addr: j for j, x in enumerate(instrs)}
     spans = []
+    traces = []
     for k, ins in enumerate(instrs):
         if ins.target is not None and ins.target <= ins.addr:
-            start = next((j for j, x in enumerate(instrs) if x.addr == ins.target), None)
-            if start is not None:
-                spans.append((start, k, sum(b.op.startswith("v_") for b in instrs[start:k + 1])))
+            start = index.get(ins.target)
+            if start is None:
+                continue
+            spans.append((start, k, sum(b.op.startswith("v_") for b in instrs[start:k + 1])))
+            tr = _hot_trace(instrs, start, k, index)
+            if tr is not None:
+                traces.append((tr, sum(b.op.startswith("v_") for b in tr)))
+    if traces:
+        top = max(t[1] for t in traces)
+        return min((t for t in traces if 4 * t[1] >= top), key=lambda t: len(t[0]))[0]
     if not spans:
         raise ValueError("no backward branch: the kernel has no loop")
     top = max(s[2] for s in spans)

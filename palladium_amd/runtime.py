@@ -55,31 +55,41 @@ class MathMode(str, enum.Enum):
     square root, deterministic `pow`. RELAXED: FMA contraction. FAST
     (default, as in the reference): contraction, reassociation, approximate
     transcendentals and division; infinities and NaNs are still honoured.
+    REPRODUCIBLE (no counterpart in the reference): results a host can
+    restate bit for bit, with fast arithmetic. A float32 `a*b + c` whose
+    product has no other use becomes one fused multiply-add (correctly
+    rounded, so C's `fmaf` gives the same value); float32 `a / b` is
+    `a * RN(1/b)` (the reciprocal correctly rounded, the product rounded
+    once); `pow` is a fast deterministic double-precision power (about
+    2^-34 relative before the float rounding). Everything else is as SAFE.
     """
 
     SAFE = "safe"
     RELAXED = "relaxed"
     FAST = "fast"
+    REPRODUCIBLE = "reproducible"
 
     @property
     def ordinal(self) -> int:
         return _MATH_MODE_ORDINALS[self.value]
 
 
-# Same ordinals as the reference's C API (src/palladium/ffi.py:38).
-_MATH_MODE_ORDINALS = {"safe": 0, "relaxed": 1, "fast": 2}
+# Same ordinals as the reference's C API (src/palladium/ffi.py:38), plus
+# REPRODUCIBLE = 3, which the reference does not have.
+_MATH_MODE_ORDINALS = {"safe": 0, "relaxed": 1, "fast": 2, "reproducible": 3}
+REPRODUCIBLE_ORDINAL = 3
 
 
 def math_mode_ordinal(mode: Any) -> int:
     value = mode.value if hasattr(mode, "value") else mode
     if isinstance(value, int):
-        if value not in (0, 1, 2):
+        if value not in (0, 1, 2, 3):
             raise ValueError(f"math_mode ordinal {value} out of range")
         return value
     try:
         return _MATH_MODE_ORDINALS[str(value).lower()]
     except KeyError:
-        raise ValueError(f"unknown math_mode {mode!r} (safe, relaxed, fast)") from None
+        raise ValueError(f"unknown math_mode {mode!r} (safe, relaxed, fast, reproducible)") from None
 
 
 def library_path() -> Path:
@@ -503,7 +513,7 @@ class Kernel:
 
 
 def _mode_value(m: Any) -> str:
-    return {0: "safe", 1: "relaxed", 2: "fast"}[math_mode_ordinal(m)]
+    return {0: "safe", 1: "relaxed", 2: "fast", 3: "reproducible"}[math_mode_ordinal(m)]
 
 
 def _scalar_ctype(a: np.generic) -> Any:

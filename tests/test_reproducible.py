@@ -1,0 +1,200 @@
+"""The REPRODUCIBLE math mode on the CPU: its power function pinned against
+libm's double pow (every sampled result within 0.505 ulp, C99's special
+cases), the division restatement, the product contraction's choice of
+sites (a function of the program alone, the one C restatement follows),
+and the emitted source."""
+
+import numpy as np
+import pytest
+
+import oracle
+import palladium_amd as pa
+from palladium_amd.emit.core import emit_hip
+from palladium_amd.emit.optimize import contract_products
+from palladium_amd.frontend import jnp, lax, pl
+from palladium_amd.ir import Jaxpr
+from palladium_amd.trace import trace
+from palladium_amd.workloads import BS3_CFG, bs3_inputs, bs3_vdp_call
+
+
+def _ulps(got, ref64):
+    ref32 = ref64.astype(np.float32)
+    return np.abs(got.astype(np.float64) - ref64) / np.spacing(np.abs(ref32)).astype(np.float64)
+
+
+def test_mode_ordinal_and_names():
+    assert pa.MathMode("reproducible").ordinal == 3
+    assert pa.MathMode.REPRODUCIBLE.value == "reproducible"
+
+
+@pytest.mark.parametrize("lo,hi,ylo,yhi", [(-30, 30, -3, 3), (-37, 38, -1, 1), (0, 9, 0.2, 0.25), (-3, 3, -60, 60)])
+def test_rpow_within_half_an_ulp_and_a_bit(lo, hi, ylo, yhi):
+    r = np.random.default_rng(int(1000 * (hi - lo)))
+    n = 400_000
+    x = (10.0 ** r.uniform(lo, hi, n)).astype(np.float32)
+    y = r.uniform(ylo, yhi, n).astype(np.float32)
+    got = oracle.rpow(x, y)
+    with np.errstate(over="ignore", under="ignore"):
+        ref = np.power(x.astype(np.float64), y.astype(np.float64))
+    normal = (ref > 1.2e-38) & (ref < 3.4e38)
+    err = _ulps(got[normal], ref[normal])
+    assert err.max() < 0.505
+    # correctly rounded on all but a few in ten thousand
+    assert np.mean(got[normal] != ref[normal].astype(np.float32)) < 2e-3
+
+
+def test_rpow_overflow_underflow_and_subnormal_results():
+    r = np.random.default_rng(7)
+    x = np.float32(2.0) ** r.uniform(-10, 10, 200_000).astype(np.float32)
+    y = r.uniform(-40, 40, x.size).astype(np.float32)
+    got = oracle.rpow(x, y)
+    with np.errstate(over="ignore", under="ignore"):
+        ref = np.power(x.astype(np.float64), y.astype(np.float64))
+        ref32 = ref.astype(np.float32)
+    # beyond the float range: inf and +0 exactly as the double rounds
+    big = ref > 3.5e38
+    assert np.all(np.isinf(got[big]))
+    tiny = ref < 1e-46
+    assert np.all(got[tiny] == 0.0)
+    sub = (ref >= 1e-44) & (ref < 1.1754943e-38)
+    assert sub.any()
+    assert np.all(np.abs(got[sub].view(np.int32) - ref32[sub].view(np.int32)) <= 1)
+
+
+def test_rpow_special_cases_follow_c99():
+    specials = np.array([0.0, -0.0, 1.0, -1.0, 0.5, 2.0, np.inf, -np.inf, np.nan, 1e-45, -3.0, 3.0, 8192.0,
+                         -8192.0, 1e30, 1e-30], np.float32)
+    x, y = np.meshgrid(specials, specials)
+    x, y = x.ravel(), y.ravel()
+    got = oracle.rpow(x, y)
+    with np.errstate(all="ignore"):
+        ref = np.power(x.astype(np.float64), y.astype(np.float64)).astype(np.float32)
+    same = (got == ref) | (np.isnan(got) & np.isnan(ref))
+    assert same.all(), list(zip(x[~same], y[~same], got[~same], ref[~same]))
+    # signs of zeros and infinities
+    assert np.signbit(oracle.rpow(np.float32(-0.0), np.float32(3.0))[0])
+    assert oracle.rpow(np.float32(-np.inf), np.float32(3.0))[0] == -np.inf
+
+
+def test_rpow_log_exact_at_powers_of_two_and_one():
+    for e in range(-126, 128):
+        assert oracle.rpow_log(np.float32(2.0) ** e) == e
+    assert oracle.rpow_log(1.0) == 0.0
+
+
+def test_rdiv_is_the_product_with_the_rounded_reciprocal():
+    r = np.random.default_rng(5)
+    a = r.standard_normal(2000).astype(np.float32)
+    b = (r.standard_normal(2000) * 10.0 ** r.uniform(-20, 20, 2000)).astype(np.float32)
+    got = np.array([oracle.rdiv(x, y) for x, y in zip(a, b)], np.float32)
+    np.testing.assert_array_equal(got, a * (np.float32(1.0) / b))
+    # at most 1.5 ulp from the correctly rounded quotient
+    q = a.astype(np.float64) / b.astype(np.float64)
+    assert _ulps(got, q).max() <= 1.5
+
+
+def _fma_eqns(j: Jaxpr):
+    out = []
+    for e in j.eqns:
+        if e.primitive.name == "fma":
+            out.append(e)
+        for v in e.params.values():
+            inner = getattr(v, "jaxpr", v)
+            if isinstance(inner, Jaxpr):
+                out.extend(_fma_eqns(inner))
+    return out
+
+
+def test_contraction_sites_of_the_bs3_loop():
+    """The adaptive loop's fused sites, as oracle_bs3_vdp_r restates them:
+    2 in the initial slope; per attempt 2 + 3 per stage (state shifts, 1 -
+    x^2, (mu a) v - x) x 2 stages, 3 for k4, 2 + 1 per 3-term sum pair, 3 +
+    1 per 4-term pair, 2 tolerances."""
+    f = bs3_vdp_call(64, math_mode="reproducible")
+    spec = f.bound(*bs3_inputs(64)).spec
+    j = contract_products(spec.jaxpr)
+    fmas = _fma_eqns(j)
+    assert len(fmas) == 2 + 26
+    negs = sorted((bool(e.params["neg_ab"]), bool(e.params["neg_c"])) for e in fmas)
+    # 1 - x*x four times (-a*b + c), (mu a) v - x four times (a*b - c)
+    assert negs.count((True, False)) == 4 and negs.count((False, True)) == 4
+    # no product is left unfused where it feeds an add or subtract alone
+    src = emit_hip(spec, math_mode="reproducible")
+    assert "ph_rdiv(" in src and "ph_rpow_with_log(" in src and "ph_rpow_log(" in src
+    assert "__builtin_fmaf(-t" in src
+
+
+def _tiny(kernel, n=8):
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    x = np.linspace(0.5, 2.0, n, dtype=np.float32)
+    call = pl.pallas_call(kernel, grid=(n,), in_specs=[s, s, s], out_specs=s,
+                          out_shape=pl.ShapeDtypeStruct((n,), np.float32))
+    return trace(call, x, x, x)
+
+
+def test_contraction_fuses_the_later_product_and_keeps_shared_ones():
+    def k(a_ref, b_ref, c_ref, o_ref):
+        a, b, c = a_ref[...], b_ref[...], c_ref[...]
+        p = a * b            # used twice: stays a product
+        q = b * c
+        o_ref[...] = (p + q) + (p - a * c)
+
+    j = contract_products(_tiny(k).jaxpr)
+    names = [e.primitive.name for e in j.eqns]
+    assert names.count("mul") == 1 and names.count("fma") == 2
+    fmas = [e for e in j.eqns if e.primitive.name == "fma"]
+    # p + q fuses q (p is shared); p - a*c fuses a*c with the product negated
+    assert [bool(e.params["neg_ab"]) for e in fmas] == [False, True]
+
+
+def test_contraction_of_both_products_takes_the_later_one():
+    def k(a_ref, b_ref, c_ref, o_ref):
+        a, b, c = a_ref[...], b_ref[...], c_ref[...]
+        o_ref[...] = a * b + b * c
+
+    j = contract_products(_tiny(k).jaxpr)
+    (f,) = [e for e in j.eqns if e.primitive.name == "fma"]
+    (m,) = [e for e in j.eqns if e.primitive.name == "mul"]
+    assert f.invars[2] is m.outvars[0]          # fma(b, c, a*b)
+    assert f.invars[0] is not m.invars[0] or f.invars[1] is not m.invars[1]
+
+
+def test_contraction_leaves_other_modes_alone():
+    def k(a_ref, b_ref, c_ref, o_ref):
+        o_ref[...] = a_ref[...] * b_ref[...] + c_ref[...]
+
+    spec = _tiny(k)
+
+    def body(mode):
+        src = emit_hip(spec, math_mode=mode)
+        return src[src.index('extern "C"'):]
+
+    for mode in ("safe", "relaxed", "fast"):
+        assert "__builtin_fmaf" not in body(mode)
+    assert "__builtin_fmaf" in body("reproducible")
+
+
+def test_bs3_reproducible_oracle_against_float64_restatement():
+    """The REPRODUCIBLE restatement is no further from the float64 BS3
+    restatement than the SAFE one is, on 40 lanes at the stiff end of config
+    2 (mu >= 50, up to ~2,200 accepted steps each): every lane ends at T1,
+    final states within 2e-5 relative of float64, and the accepted counts'
+    worst and mean relative deviation from float64 at most SAFE's plus a
+    percent. (A count can move by a few percent on one lane under either
+    rounding: rejections sit near err = 1, where float32 and float64
+    decide differently.)"""
+    from test_oracle import _bs3_f64
+
+    x0, v0, mu = bs3_inputs(4096, seed=11)
+    sel = np.where(mu >= 50)[0][:40]
+    x0, v0, mu = x0[sel], v0[sel], mu[sel]
+    F = _bs3_f64(x0, v0, mu, BS3_CFG)
+    s = oracle.bs3_vdp(x0, v0, mu, BS3_CFG)
+    r = oracle.bs3_vdp(x0, v0, mu, BS3_CFG, mode="reproducible")
+    np.testing.assert_array_equal(r[0], np.float32(BS3_CFG.t1))
+    np.testing.assert_allclose(r[1], F[1], rtol=2e-5)
+    np.testing.assert_allclose(r[2], F[2], rtol=5e-5, atol=2e-7)
+    dev = lambda o: np.abs(o[3] - F[3]) / F[3]  # noqa: E731
+    assert dev(r).max() <= dev(s).max() + 0.01
+    assert dev(r).mean() <= dev(s).mean() + 0.01
+    assert r[4].sum() <= 4 * F[4].sum() + 25 * len(sel)
