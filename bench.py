@@ -343,18 +343,26 @@ def bench_gbm(steps: int, warmup: int, cpu: bool) -> dict:
                        "frac": achieved / FP32_PEAK, "traffic": None, "ops_per_path_step": per_step,
                        "ops_note": (f"staged elementwise ops per step, Threefry-2x32-20 = {THREEFRY_OPS} integer ops, "
                                     "each counted once against a peak that counts an FMA twice: frac cannot pass "
-                                    "~0.5; issue.frac_of_sustained_issue is the consistent figure"),
+                                    "~0.5; issue.frac_of_peak_issue is the consistent figure"),
                        "avg_launch_ms": avg,
                        "issue": issue_fraction(rt.compile_code_object(bound.hip_source, bound.spec.name, "fast"),
                                                ps, avg)}
-    if cpu:
-        import oracle
+    import oracle
 
+    # The timed FAST payoffs path by path against the C oracle (all paths).
+    got = ops[1].to_numpy(bound.stream).astype(np.float64)
+    oracle.gbm(cfg, 64)
+    t0 = time.perf_counter()
+    want = oracle.gbm(cfg, cfg.n_paths).astype(np.float64)
+    dt = time.perf_counter() - t0
+    d = np.abs(got - want)
+    big = want > 1.0
+    res["fast_vs_oracle"] = {"paths": cfg.n_paths, "abs_max": float(d.max()),
+                             "rel_max_payoff_above_1": float((d[big] / want[big]).max()),
+                             "zero_nonzero_flips": int(np.sum((got == 0) != (want == 0))),
+                             "mean_payoff_rel_shift": float((got.mean() - want.mean()) / want.mean())}
+    if cpu:
         n_cpu = cfg.n_paths
-        oracle.gbm(cfg, 64)
-        t0 = time.perf_counter()
-        oracle.gbm(cfg, n_cpu)
-        dt = time.perf_counter() - t0
         res["cpu_baseline"] = {"value": n_cpu * cfg.n_steps / dt, "unit": "path-steps/s", "cores": _cpu_cores(),
                                "kind": "port", "sample": f"all {n_cpu} paths x {cfg.n_steps} steps of config 3, C oracle, {dt:.2f} s"}
         # the kernel's own .interpret() (the reference's interpret=True path)
@@ -458,9 +466,9 @@ def bench_mall(steps: int, warmup: int, cpu: bool) -> dict:
                                  "frac_of_8TBps": bw / HBM_PEAK}
     hbm_ceiling = copies["2048MiB"]["GB_per_s"]
     for v in stencils.values():
-        v["frac_of_copy_2GiB"] = v["GB_per_s"] / hbm_ceiling
-    stencils["4096^2"]["frac_of_copy_same_size"] = stencils["4096^2"]["GB_per_s"] / copies["256MiB"]["GB_per_s"]
-    stencils["8192^2"]["frac_of_copy_same_size"] = stencils["8192^2"]["GB_per_s"] / copies["1024MiB"]["GB_per_s"]
+        v["ratio_to_copy_2GiB"] = v["GB_per_s"] / hbm_ceiling
+    stencils["4096^2"]["ratio_to_copy_same_size"] = stencils["4096^2"]["GB_per_s"] / copies["256MiB"]["GB_per_s"]
+    stencils["8192^2"]["ratio_to_copy_same_size"] = stencils["8192^2"]["GB_per_s"] / copies["1024MiB"]["GB_per_s"]
     res = _base("HBM streaming ceiling (emitted copy, 2 GiB working set)", hbm_ceiling, "GB/s", steps, warmup,
                 copies["2048MiB"]["us_per_launch"] / 1e3, {"workload": "copy and Gray-Scott by working-set size"})
     res["copy"] = copies
@@ -565,10 +573,10 @@ def bench_gs(steps: int, warmup: int, cpu: bool) -> dict:
     same = bench_copy(steps, warmup, False, n=cfg.size * cfg.size)["roofline"]["achieved"]
     hbm = bench_copy(max(3, steps // 4), 1, False, n=2048 * 1024 * 1024 // 16)["roofline"]["achieved"]
     res["roofline"].update({
-        "copy_same_working_set_GBps": same, "frac_of_copy": achieved / 1e9 / same,
+        "copy_same_working_set_GBps": same, "ratio_to_copy": achieved / 1e9 / same,
         "hbm_streaming_copy_2GiB_GBps": hbm,
         "mall_note": ("frac is against the published 8 TB/s; the working set (256 MiB) is partly served by the "
-                      "256 MB Infinity Cache, so frac_of_copy (against an emitted copy of the same working set) "
+                      "256 MB Infinity Cache, so ratio_to_copy (against an emitted copy of the same working set) "
                       "is the stencil's efficiency; HBM alone streams hbm_streaming_copy_2GiB_GBps"),
     })
     res["pattern_energy"] = float(np.sum(v, dtype=np.float64))
@@ -692,8 +700,9 @@ def bench_gs_fused(steps: int, warmup: int, cpu: bool) -> dict:
             per[kk] = {"slots_per_iteration": slots, "lane_iterations_per_launch": iters, "launches": count}
             total += slots * iters * count
         sustained = rates["sustained_fma_tflops"] * 1e12 / 2
-        issue = {"per_kernel": per, "achieved_slots_per_s": total / gpu_s, "sustained_fma_slots_per_s": sustained,
-                 "frac_of_sustained_issue": total / gpu_s / sustained}
+        issue = {"per_kernel": per, "achieved_slots_per_s": total / gpu_s,
+                 "peak_issue_slots_per_s": PEAK_ISSUE_SLOTS, "frac_of_peak_issue": total / gpu_s / PEAK_ISSUE_SLOTS,
+                 "sustained_fma_slots_per_s": sustained, "ratio_to_fma_probe": total / gpu_s / sustained}
         # The register pass is bound by VALU issue (its HBM figures go under
         # "hbm"): FMA-equivalent slots, 2 FLOP each, against the FP32 peak.
         hbm_part = {k: res["roofline"][k] for k in ("achieved", "peak", "unit", "frac", "traffic",
@@ -704,8 +713,9 @@ def bench_gs_fused(steps: int, warmup: int, cpu: bool) -> dict:
                            "frac": flops / FP32_PEAK, "traffic": hbm_part["traffic"], "issue": issue,
                            "hbm": hbm_part,
                            "note": ("achieved: the graph's FMA-equivalent VALU issue slots (this build's ISA, measured "
-                                    "per-instruction costs) at 2 FLOP each per second; issue.frac_of_sustained_issue "
-                                    "against the measured sustained rate; hbm: the passes' own traffic")}
+                                    "per-instruction costs) at 2 FLOP each per second; issue.frac_of_peak_issue against the "
+                                    "published peak issue rate, issue.ratio_to_fma_probe against the FMA probe's "
+                                    "sustained rate; hbm: the passes' own traffic")}
     res["pattern_energy"] = float(np.sum(v, dtype=np.float64))
     if cpu:
         import oracle
@@ -1136,11 +1146,20 @@ def valu_costs() -> dict:
     return _RATES
 
 
+# Peak VALU issue: the published FP32 rate counts 2 FLOP per lane-FMA, so
+# 157.3 TFLOP/s is 78.65e12 lane-FMA issues per second at the peak clock.
+PEAK_ISSUE_SLOTS = FP32_PEAK / 2
+
+
 def issue_fraction(code: bytes, units_per_launch: float, avg_ms: float) -> dict:
     """The hot loop's FMA-equivalent issue slots per iteration (this
     build's ISA, measured per-instruction costs) times the iterations of
-    one launch, over the launch time, against the sustained FMA issue rate:
-    how busy the VALUs are in the currency they actually spend."""
+    one launch, over the launch time: how busy the VALUs are in the
+    currency they actually spend. `frac_of_peak_issue` is against the
+    published peak issue rate (a bound). `ratio_to_fma_probe` is against
+    the rate the pure-FMA probe sustains in the same process: not a bound,
+    since that probe runs at the lower clock a full-chip FMA load allows,
+    and a mix of lighter instructions (adds, moves) can run above it."""
     from palladium_amd import isa
 
     rates = valu_costs()
@@ -1148,8 +1167,32 @@ def issue_fraction(code: bytes, units_per_launch: float, avg_ms: float) -> dict:
     sustained = rates["sustained_fma_tflops"] * 1e12 / 2  # lane-FMA issues per second
     achieved = slots * units_per_launch / (avg_ms / 1e3)
     return {"slots_per_iteration": slots, "vector_instructions_per_iteration": sum(hist.values()),
-            "achieved_slots_per_s": achieved, "sustained_fma_slots_per_s": sustained,
-            "frac_of_sustained_issue": achieved / sustained}
+            "achieved_slots_per_s": achieved, "peak_issue_slots_per_s": PEAK_ISSUE_SLOTS,
+            "frac_of_peak_issue": achieved / PEAK_ISSUE_SLOTS,
+            "sustained_fma_slots_per_s": sustained, "ratio_to_fma_probe": achieved / sustained}
+
+
+def fraction_fields(res, path: str = "") -> list[tuple[str, float]]:
+    """Every field of a result whose name says it is a fraction of a bound
+    (`frac`, `frac_*`, `*_frac`), with its dotted path."""
+    out = []
+    if isinstance(res, dict):
+        for k, v in res.items():
+            p = f"{path}.{k}" if path else k
+            if isinstance(v, (dict, list)):
+                out += fraction_fields(v, p)
+            elif (k == "frac" or k.startswith("frac_") or k.endswith("_frac")) and isinstance(v, (int, float)):
+                out.append((p, float(v)))
+    elif isinstance(res, list):
+        for i, v in enumerate(res):
+            out += fraction_fields(v, f"{path}[{i}]")
+    return out
+
+
+def fractions_over_one(res) -> list[str]:
+    """The fraction fields that exceed 1: none should, since each is taken
+    against a bound (published peaks, the issue floor of one wavefront)."""
+    return [f"{p}={v:.4f}" for p, v in fraction_fields(res) if v > 1.0]
 
 
 def bench_valu_rates(steps: int, warmup: int, cpu: bool) -> dict:
@@ -1257,10 +1300,14 @@ def valu_latencies() -> dict:
 
 
 def bs3_latency_bound(call, host, lat: dict, max_attempts: int, kernel_ms: float, mode: str = "fast") -> dict:
-    """The latency floor of the adaptive loop: the slowest lane runs
-    `max_attempts` attempts back to back, and its wavefront can run one no
-    faster than the in-order chain model of this build's own loop body
-    (palladium_amd.isa) with the measured latencies."""
+    """The latency bounds of the adaptive loop: the slowest lane runs
+    `max_attempts` attempts back to back, and its wavefront issues each
+    attempt's instructions one after another. `latency_frac` is against the
+    issue floor (the loop's instructions at one wavefront's measured issue
+    interval, no waiting on results: a bound). `chain_model_ratio` is
+    against the in-order chain model of the same loop (palladium_amd.isa)
+    with the measured result latencies: an estimate, which a wavefront that
+    overlaps more than the model assumes can beat."""
     from palladium_amd import isa
     from palladium_amd import runtime as rt
     from palladium_amd.emit.compact import iterations_per_pass
@@ -1271,12 +1318,14 @@ def bs3_latency_bound(call, host, lat: dict, max_attempts: int, kernel_ms: float
     # a compacted loop runs several attempts per pass of its machine loop
     per = iterations_per_pass(bound.hip_source)
     ns = m.cycles_per_iteration / per
-    floor_ms = max_attempts * ns / 1e6
+    chain_ms = max_attempts * ns / 1e6
+    issue_ms = max_attempts * (m.instructions / per) * lat["issue_ns"] / 1e6
     return {"ns_per_attempt_chain_model": ns, "loop_instructions": m.instructions / per,
             "loop_valu": m.valu / per, "loop_transcendental": m.transcendental / per,
             "attempts_per_machine_iteration": per, "max_attempts_one_lane": max_attempts,
             "measured_ns_per_attempt_slowest_wave": kernel_ms * 1e6 / max_attempts,
-            "latency_floor_ms": floor_ms, "latency_frac": floor_ms / kernel_ms, "latencies_ns": lat}
+            "issue_floor_ms": issue_ms, "latency_frac": issue_ms / kernel_ms,
+            "chain_model_ms": chain_ms, "chain_model_ratio": chain_ms / kernel_ms, "latencies_ns": lat}
 
 
 def bench_valu_latency(steps: int, warmup: int, cpu: bool) -> dict:
@@ -1318,7 +1367,7 @@ def main() -> int:
         # the ceiling the published 157.3 TFLOP/s does not account for.
         fma = valu_costs()["sustained_fma_tflops"]
         res["roofline"]["sustained_fma_tflops"] = fma
-        res["roofline"]["frac_of_sustained"] = res["roofline"]["achieved"] / fma
+        res["roofline"]["ratio_to_sustained_fma"] = res["roofline"]["achieved"] / fma
     if a.workload == "lv" and not a.no_secondary:
         # The headline metric names two rooflines: RK4 LV against FP32 VALU
         # (above) and the Gray-Scott stencil against HBM. The second, and the
@@ -1333,6 +1382,9 @@ def main() -> int:
                                                         "accuracy", "accepted_steps_per_s", "price", "safe", "fast",
                                                         "fast_vs_oracle", "counts_equal_oracle",
                                                         "accuracy_vs_float64") if k in r}
+    over = fractions_over_one(res)
+    if over:
+        res["fractions_over_one"] = over
     if rank == 0:
         print(json.dumps(res), flush=True)
     return 0
