@@ -731,6 +731,52 @@ def bench_gs_fused(steps: int, warmup: int, cpu: bool) -> dict:
     return res
 
 
+WAVE_LANES = 64
+GS_GEOMETRIES = [(64, 4, 6, 1), (40, 4, 6, 1), (48, 4, 6, 1), (32, 4, 6, 1), (36, 4, 6, 1), (40, 4, 4, 1),
+                 (40, 4, 8, 1), (64, 4, 8, 1), (32, 4, 4, 2), (32, 4, 6, 2), (24, 4, 4, 2), (16, 4, 4, 2),
+                 (32, 2, 6, 2), (64, 2, 6, 2)]
+
+
+def bench_gs_geometry(steps: int, warmup: int, cpu: bool) -> dict:
+    """The register pass of config 4 over strip geometries: (rows per
+    strip, rows per load group, steps per pass K, columns per lane), each
+    with its registers and occupancy from the code object, its grid's
+    wavefronts per SIMD, the halo work factor ((rows + 2K) / rows x 64 C /
+    (64 C - 2K) updates per useful one) and the best of three 480-step runs
+    (one HIP graph each). The line's value is the fastest geometry's
+    cell-steps/s."""
+    from palladium_amd import diagnostics, stencil
+    from palladium_amd import runtime as rt
+    from palladium_amd.workloads import GS_CFG, gray_scott_initial
+
+    n = GS_CFG.size
+    u0, v0 = gray_scott_initial(n)
+    n_steps = int(os.environ.get("PALLADIUM_GS_STEPS", 480))
+    rows_out = []
+    for rows, group, k, cols in GS_GEOMETRIES:
+        f = stencil.RegisterGrayScott(n, k=k, rows=rows, group=group, cols=cols)
+        stencil.gray_scott_fused_run(f, u0, v0, 2 * k)
+        stencil.gray_scott_fused_run(f, u0, v0, n_steps)
+        best = min(stencil.gray_scott_fused_run(f, u0, v0, n_steps)[2] for _ in range(3))
+        r = diagnostics.code_object_resources(rt.compile_code_object(f.source(k), "gray_scott_regs", "fast"),
+                                              "gray_scott_regs")
+        waves = stencil.register_geometry(n, k, rows, cols)[0]
+        w = WAVE_LANES * cols - 2 * k
+        rows_out.append({"rows": rows, "group": group, "k": k, "cols": cols, "vgprs": r.vgprs,
+                         "waves_per_simd_max": r.waves_per_simd, "grid_waves": waves,
+                         "grid_waves_per_simd": waves / 1024, "work_factor": (rows + 2 * k) / rows * WAVE_LANES * cols / w,
+                         "us_per_step": best * 1e6 / n_steps})
+        print(f"[gs_geometry] {rows_out[-1]}", file=sys.stderr, flush=True)
+    fastest = min(rows_out, key=lambda g: g["us_per_step"])
+    res = _base("Gray-Scott register pass over strip geometries (4096^2, fp32)", n * n / (fastest["us_per_step"] / 1e6),
+                "cell-steps/s", n_steps, 2, fastest["us_per_step"] / 1e3,
+                {"workload": f"Gray-Scott 4096x4096 register pass, {n_steps} steps per geometry", "size": n,
+                 "math_mode": "fast"})
+    res["geometries"] = rows_out
+    res["roofline"] = {"bound": "issue", "achieved": None, "peak": None, "unit": None, "frac": None, "traffic": None}
+    return res
+
+
 def bench_gs_lds(steps: int, warmup: int, cpu: bool) -> dict:
     """The LDS halo-tiled alternative to the emitted Gray-Scott step, timed
     the same way (all steps as one HIP graph) and checked against it."""
@@ -1111,6 +1157,12 @@ _VALU_PROBES = {
     # read from the next lane over (DPP wave rotation)
     "v_add_f32_dpp": ("float", "v_add_f32_dpp %0, %1, %0 wave_rol:1 row_mask:0xf bank_mask:0xf bound_ctrl:1", False),
     "v_mov_b32": ("unsigned int", "v_mov_b32 %0, %1", False),
+    # the same add with a row-local shift or a quad permutation instead of
+    # the wave rotation, and a 24-bit integer multiply: whether a cheaper
+    # cross-lane form exists (it does not: every one costs what wave_rol does)
+    "v_add_f32_dpp_row_shl": ("float", "v_add_f32_dpp %0, %1, %0 row_shl:1 row_mask:0xf bank_mask:0xf bound_ctrl:1", False),
+    "v_add_f32_dpp_quad_perm": ("float", "v_add_f32_dpp %0, %1, %0 quad_perm:[1,2,3,0] row_mask:0xf bank_mask:0xf", False),
+    "v_mul_u32_u24": ("unsigned int", "v_mul_u32_u24 %0, %0, %1", False),
 }
 _VALU_ITERS = 2048
 
@@ -1358,7 +1410,7 @@ def main() -> int:
     fns = {"lv": bench_lv, "lv0": bench_lv0, "gbm": bench_gbm, "gbm_block": bench_gbm_block, "gbm_fold_in": bench_gbm_fold_in, "gs": bench_gs, "gs_lds": bench_gs_lds, "bs3": bench_bs3,
            "bs3_lockstep": bench_bs3_lockstep, "bs3_sorted": bench_bs3_sorted, "copy": bench_copy, "df32": bench_df32, "dispatch": bench_dispatch,
            "valu_rates": bench_valu_rates, "valu_latency": bench_valu_latency, "mall": bench_mall,
-           "gs_fused": bench_gs_fused}
+           "gs_fused": bench_gs_fused, "gs_geometry": bench_gs_geometry}
     if a.workload not in fns:
         raise SystemExit(f"unknown workload {a.workload} (choose from {', '.join(fns)})")
     res = fns[a.workload](a.steps, a.warmup, cpu=not a.no_cpu and rank == 0)
