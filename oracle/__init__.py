@@ -103,6 +103,8 @@ def _declare_more(L):
     L.oracle_gbm.argtypes = [l, l, l, u, u, f, f, f, f, f, _F]
     L.oracle_pow.argtypes = [f, f]
     L.oracle_pow.restype = f
+    L.oracle_pow_many.argtypes = [l, _F, _F, _F]
+    L.oracle_pow_many.restype = None
     L.oracle_pow_log_many.argtypes = [l, _F, ctypes.POINTER(ctypes.c_double)]
     L.oracle_pow_log_many.restype = None
     L.oracle_bs3_vdp.argtypes = [l, _F, _F, _F, f, f, f, f, l, _F, _F, _F, _I, _I]
@@ -143,6 +145,16 @@ def gbm(cfg, n_paths: int, first_path: int = 0) -> np.ndarray:
 
 def pow32(x: float, y: float) -> np.float32:
     return np.float32(_lib2().oracle_pow(float(x), float(y)))
+
+
+def pow_many(x, y) -> np.ndarray:
+    """The SAFE deterministic pow, elementwise over float32 arrays."""
+    x, y = np.broadcast_arrays(np.asarray(x, np.float32), np.asarray(y, np.float32))
+    x = np.ascontiguousarray(x.ravel())
+    y = np.ascontiguousarray(y.ravel())
+    out = np.empty(x.size, np.float32)
+    _lib2().oracle_pow_many(x.size, _fp(x), _fp(y), _fp(out))
+    return out
 
 
 def pow_log(x: np.ndarray) -> np.ndarray:

@@ -241,6 +241,10 @@ float oracle_pow(float x, float y) {
   return sign * (float)ph_exp2_dbl(z);
 }
 
+void oracle_pow_many(long n, const float *x, const float *y, float *out) {
+  for (long i = 0; i < n; ++i) out[i] = oracle_pow(x[i], y[i]);
+}
+
 /* ------------------------------------------------------------------------
  * Adaptive Bogacki-Shampine 3(2) with FSAL and a PI step controller on Van
  * der Pol, one trajectory per index, as tests/test_08_adaptive.py:76-122
