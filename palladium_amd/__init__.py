@@ -156,9 +156,10 @@ class HipCallable:
                     spec = trace(self._staged, *args)
                     check_block_bounds(spec)
                     log_compile(spec, self._threadgroup, self._math_mode)
-                    from palladium_amd.dispatch import _block_of
+                    from palladium_amd.dispatch import _block_of, _tile_of
 
-                    b = bind(spec, emit_hip(spec, block=_block_of(self._threadgroup), math_mode=self._math_mode),
+                    b = bind(spec, emit_hip(spec, block=_block_of(self._threadgroup), math_mode=self._math_mode,
+                                     tile=_tile_of(self._threadgroup)),
                              math_mode=self._math_mode, threadgroup=self._threadgroup)
                     self.cache[key] = b
         return b
@@ -187,9 +188,10 @@ def debug_hip(kernel: Callable, *example_args: Any, **pallas_kwargs: Any) -> str
     math_mode = pallas_kwargs.pop("math_mode", MathMode.FAST)
     frontend = pallas_kwargs.pop("frontend", "auto")
     staged, _ = _stage(kernel, pallas_kwargs, frontend)
-    from palladium_amd.dispatch import _block_of
+    from palladium_amd.dispatch import _block_of, _tile_of
 
-    return emit_hip(trace(staged, *example_args), block=_block_of(threadgroup), math_mode=math_mode)
+    return emit_hip(trace(staged, *example_args), block=_block_of(threadgroup), math_mode=math_mode,
+                    tile=_tile_of(threadgroup))
 
 
 def hip_call(kernel: Callable, **pallas_kwargs: Any) -> HipCallable:

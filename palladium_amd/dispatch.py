@@ -259,6 +259,19 @@ class BoundKernel:
         self.kernel.launch_ptrs(geo.blocks, geo.block, ptrs, stream if stream is not None else self.stream)
 
 
+def _tile_of(threadgroup: Any) -> tuple[int, int] | None:
+    """The (axis-0, axis-1) instance tile of a 2-D threadgroup: Metal's
+    threadsPerThreadgroup (x, y) over a grid whose x is program_id(0), as
+    the reference dispatches it. None for an int, a 1-D tuple, or a 3-D
+    tuple with z > 1 (those only set the workgroup size)."""
+    if threadgroup is None or isinstance(threadgroup, int):
+        return None
+    tg = [int(t) for t in threadgroup]
+    if len(tg) < 2 or any(t != 1 for t in tg[2:]):
+        return None
+    return tg[0], tg[1]
+
+
 def _block_of(threadgroup: Any) -> int | None:
     if threadgroup is None:
         return None

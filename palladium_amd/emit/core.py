@@ -407,12 +407,20 @@ def _xcd_remap(nblocks: int) -> list[str]:
     ]
 
 
-def _tile2d(grid: tuple[int, ...], block: int) -> tuple[int, int] | None:
+def _tile2d(grid: tuple[int, ...], block: int, tile: tuple[int, int] | None = None) -> tuple[int, int] | None:
     """(rows, cols) of the instance tile one workgroup covers on a 2-D grid,
-    or None to keep the row-major order. Disabled with PALLADIUM_TILE2D=0."""
+    or None to keep the row-major order: `tile` (a 2-D threadgroup, rows of
+    grid axis 0 by columns of axis 1) when it covers the workgroup and
+    divides the grid, else block/64 rows of 64. Disabled with
+    PALLADIUM_TILE2D=0."""
     import os
 
     if os.environ.get("PALLADIUM_TILE2D", "1") == "0" or len(grid) != 2:
+        return None
+    if tile is not None:
+        ti, tj = (int(t) for t in tile)
+        if ti * tj == block and ti >= 1 and tj >= 1 and grid[0] % ti == 0 and grid[1] % tj == 0:
+            return ti, tj
         return None
     tj = int(os.environ.get("PALLADIUM_TILE_COLS", "64"))
     ti = block // tj
@@ -458,7 +466,7 @@ def launch_geometry(spec: KernelSpec, block: int | None = None, lanes: int | Non
 
 
 def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None = None,
-             math_mode: Any = None) -> str:
+             math_mode: Any = None, tile: tuple[int, int] | None = None) -> str:
     """Assemble the complete HIP source for a KernelSpec.
 
     Signature convention (relied on by the launcher): one pointer per
@@ -566,7 +574,7 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
     pid_vals = []
     rem = "_inst" if lanes > 1 else ("_flatc" if getattr(env, "compact_in", None) else "_flat")
     grid = tuple(spec.grid)
-    tile = _tile2d(grid, geo.block) if lanes == 1 else None
+    tile = _tile2d(grid, geo.block, tile) if lanes == 1 else None
     if tile is not None:
         # 2-D grids: a workgroup covers a (block/64) x 64 tile of instances,
         # each wavefront one 64-wide row segment, so vertical neighbours of

@@ -112,14 +112,15 @@ class FfiCallable:
             with self._lock:
                 entry = self._cache.get(key)
                 if entry is None:
-                    from palladium_amd.dispatch import _block_of
+                    from palladium_amd.dispatch import _block_of, _tile_of
 
                     from palladium_amd.interpret import check_block_bounds
 
                     spec = trace(self._staged, *args)
                     check_block_bounds(spec)
                     log_compile(spec, self._threadgroup, self._math_mode)
-                    entry = (spec, emit_hip(spec, block=_block_of(self._threadgroup), math_mode=self._math_mode))
+                    entry = (spec, emit_hip(spec, block=_block_of(self._threadgroup), math_mode=self._math_mode,
+                                     tile=_tile_of(self._threadgroup)))
                     self._cache[key] = entry
         return entry
 

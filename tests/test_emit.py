@@ -229,3 +229,29 @@ def test_two_d_tile_only_when_it_divides():
     assert _tile2d((3, 128), 256) is None  # rows not a multiple of 4
     assert _tile2d((8, 100), 256) is None  # cols not a multiple of 64
     assert _tile2d((8,), 256) is None
+
+
+def test_two_d_threadgroup_sets_the_instance_tile():
+    """A 2-D threadgroup (x, y) tiles a 2-D grid with x instances of
+    program_id(0) by y of program_id(1) per workgroup, as Metal's
+    threadsPerThreadgroup does for the reference; one that does not divide
+    the grid keeps the row-major order. The workgroup size is x * y."""
+    import palladium_amd as pa
+    from palladium_amd.dispatch import _block_of, _tile_of
+
+    def k(x_ref, o_ref):
+        i, j = pl.program_id(0), pl.program_id(1)
+        o_ref[i, j] = x_ref[i, j] * 2.0 + (i * 64 + j).astype(jnp.float32)
+
+    n = 64
+    x = np.arange(n * n, dtype=np.float32).reshape(n, n)
+    full = pl.BlockSpec((n, n), lambda i, j: (0, 0))
+    kw = dict(grid=(n, n), in_specs=[full], out_specs=full, out_shape=pl.ShapeDtypeStruct((n, n), np.float32))
+    assert _tile_of((16, 16)) == (16, 16) and _tile_of((256,)) is None and _tile_of((8, 8, 4)) is None
+    assert _block_of((16, 16)) == 256
+    src = pa.debug_hip(k, x, threadgroup=(16, 16), **kw)
+    assert "threadIdx.x / 16u" in src and "threadIdx.x % 16u" in src
+    default = pa.debug_hip(k, x, **kw)
+    assert "threadIdx.x / 64u" in default
+    ragged = pa.debug_hip(k, x, threadgroup=(48, 4), **kw)   # 48 does not divide 64
+    assert "threadIdx.x / 4u" not in ragged

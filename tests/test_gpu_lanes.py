@@ -93,3 +93,25 @@ def test_two_d_blocks_column_stores():
                        out_shape=pl.ShapeDtypeStruct((512, 2), F))
     x = np.arange(512, dtype=F)
     np.testing.assert_array_equal(call(x), np.stack([x * 2.0, x + 1.0], axis=1))
+
+
+def test_two_d_threadgroups_tile_the_grid_without_changing_results():
+    """A 2-D threadgroup tiles a 2-D grid (x instances of program_id(0) by y
+    of program_id(1) per workgroup): same results as the default tiling and
+    the interpreter, for square, tall and wide tiles."""
+    import palladium_amd as pa
+
+    def k(x_ref, o_ref):
+        i, j = pl.program_id(0), pl.program_id(1)
+        o_ref[i, j] = x_ref[i, j] * 2.0 + (i * 128 + j).astype(jnp.float32)
+
+    n = 128
+    x = np.random.default_rng(6).standard_normal((n, n)).astype(np.float32)
+    full = pl.BlockSpec((n, n), lambda i, j: (0, 0))
+    kw = dict(grid=(n, n), in_specs=[full], out_specs=full, out_shape=pl.ShapeDtypeStruct((n, n), np.float32),
+              math_mode="safe")
+    want = pa.hip_call(k, **kw).interpret(x)
+    for tg in (None, (16, 16), (8, 32), (32, 8), (4, 64)):
+        print(f"[lanes] 2-D threadgroup {tg}", flush=True)
+        got = pa.hip_call(k, threadgroup=tg, **kw)(x)
+        np.testing.assert_array_equal(got, want)
