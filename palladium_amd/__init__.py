@@ -14,6 +14,7 @@ against `jax.experimental.pallas` itself.
 
 from __future__ import annotations
 
+import functools
 import threading
 from collections.abc import Callable
 from typing import Any
@@ -35,7 +36,7 @@ from palladium_amd.errors import (
     UnsupportedPrimitiveError,
 )
 from palladium_amd.ffi import FfiCallable, hip_call_jit
-from palladium_amd.interpret import check_block_bounds
+from palladium_amd.interpret import check_block_bounds, interpret_call
 from palladium_amd.runtime import MathMode
 from palladium_amd.trace import BlockInfo, KernelSpec, trace
 
@@ -117,7 +118,9 @@ class HipCallable:
     Attributes
     ----------
     interpret : callable
-        The same pallas_call with `interpret=True`: the CPU interpreter.
+        The same pallas_call with `interpret=True`: the CPU interpreter (IEEE
+        order; under REPRODUCIBLE math, that mode's fused multiply-adds,
+        division and power, so it reproduces the device bit for bit).
     cache : dict
         Input-shape signature -> compiled `BoundKernel`
         (`cache[key].hip_source` is the emitted text).
@@ -127,6 +130,9 @@ class HipCallable:
                  threadgroup: int | tuple[int, ...] | None, frontend: str = "auto") -> None:
         self._staged, self.interpret = _stage(kernel, pallas_kwargs, frontend)
         self._math_mode = MathMode(runtime._mode_value(math_mode))
+        if self._math_mode == MathMode.REPRODUCIBLE and not _use_jax(frontend):
+            # the interpreter in this mode's arithmetic: device results bit for bit
+            self.interpret = functools.partial(interpret_call, self._staged, math_mode=self._math_mode)
         self._threadgroup = threadgroup
         self.cache: dict[CacheKey, BoundKernel] = {}
         # Guards trace/emit/compile on a miss: concurrent first calls on

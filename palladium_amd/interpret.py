@@ -29,6 +29,7 @@ from typing import Any
 
 import numpy as np
 
+from palladium_amd import exact
 from palladium_amd.dtypes import bits_from_f32, f32_from_bits, from_float, is_bf16, round_f32, to_float
 from palladium_amd.emit.core import check_contiguous
 from palladium_amd.errors import EmitError, UnsupportedPrimitiveError
@@ -106,10 +107,11 @@ def _per_instance(v: Any, n: int) -> np.ndarray:
 
 
 class _Env:
-    def __init__(self, n: int, pids: list[np.ndarray], grid: tuple[int, ...]):
+    def __init__(self, n: int, pids: list[np.ndarray], grid: tuple[int, ...], reproducible: bool = False):
         self.n = n
         self.pids = pids
         self.grid = grid
+        self.reproducible = reproducible
         self.vals: dict[Var, Any] = {}
 
     def read(self, atom: Any) -> Any:
@@ -224,7 +226,7 @@ def _sign(x):
     return np.where((x == 0) | np.isnan(x), x, np.sign(x))
 
 
-def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
+def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int, reproducible: bool = False) -> Any:
     out_aval = eqn.outvars[0].aval
     bf_out = is_bf16(out_aval.dtype)
     dt = np.dtype(np.float32) if bf_out else np.dtype(out_aval.dtype)
@@ -240,6 +242,13 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
             r = a - b
         elif name == "mul":
             r = a * b
+        elif name == "fma":
+            c = ops[2]
+            r = exact.fma_f32(-a if eqn.params.get("neg_ab") else a, b, -c if eqn.params.get("neg_c") else c)
+        elif name == "div" and reproducible and isf and dt == np.float32:
+            r = exact.rdiv(a, b)
+        elif name == "pow" and reproducible and dt == np.float32:
+            r = exact.rpow(a, b)
         elif name == "div":
             r = a / b if isf else _int_div(a, b, dt)
         elif name == "rem":
@@ -340,7 +349,7 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int) -> Any:
 _ELEMENTWISE = set(
     "add sub mul div rem min max pow neg abs sign exp exp2 log log2 log1p expm1 sin cos tan tanh sqrt rsqrt floor "
     "ceil round logistic atan2 lt le gt ge eq ne and or xor not shift_right_logical shift_right_arithmetic "
-    "shift_left clamp select_n integer_pow convert_element_type bitcast_convert_type".split()
+    "shift_left clamp select_n integer_pow convert_element_type bitcast_convert_type fma".split()
 )
 
 
@@ -351,7 +360,7 @@ def _eval(jaxpr: Jaxpr, env: _Env, invals: list[Any], mask: np.ndarray) -> list[
     for eqn in jaxpr.eqns:
         name = eqn.primitive.name
         if name in _ELEMENTWISE:
-            env.write(eqn.outvars[0], _elementwise(name, [env.read(a) for a in eqn.invars], eqn, n))
+            env.write(eqn.outvars[0], _elementwise(name, [env.read(a) for a in eqn.invars], eqn, n, env.reproducible))
         elif name == "get":
             ref: _Ref = env.read(eqn.invars[0])
             tree = eqn.params["tree"].unflatten(eqn.invars[1:])
@@ -644,7 +653,20 @@ def check_block_bounds(spec: KernelSpec) -> None:
         del imj
 
 
-def interpret_spec(spec: KernelSpec, *arrays: np.ndarray) -> tuple[np.ndarray, ...]:
+def interpret_spec(spec: KernelSpec, *arrays: np.ndarray, math_mode: Any = None) -> tuple[np.ndarray, ...]:
+    """Run a KernelSpec on the CPU. Float operations are IEEE, in the traced
+    order (SAFE's semantics). With `math_mode` REPRODUCIBLE the program
+    first goes through the emitter's product contraction and float32
+    division and power take that mode's forms (`palladium_amd.exact`), so the
+    results are the device's bit for bit for everything but the
+    transcendentals."""
+    from palladium_amd.runtime import REPRODUCIBLE_ORDINAL, math_mode_ordinal
+
+    reproducible = math_mode is not None and math_mode_ordinal(math_mode) == REPRODUCIBLE_ORDINAL
+    if reproducible:
+        from palladium_amd.emit.optimize import contract_products
+
+        spec = dataclasses.replace(spec, jaxpr=contract_products(spec.jaxpr))
     n = spec.num_programs
     pids = _grid_pids(tuple(spec.grid))
     refs = []
@@ -673,7 +695,7 @@ def interpret_spec(spec: KernelSpec, *arrays: np.ndarray) -> tuple[np.ndarray, .
         bshape = tuple(info.block_shape) or (1,)
         strides = tuple(math.prod(bshape[d + 1 :]) for d in range(len(bshape)))
         refs.append(_Ref(flat, block_offsets(spec, info, pids), bshape, strides, k < len(spec.inputs)))
-    env = _Env(n, pids, tuple(spec.grid))
+    env = _Env(n, pids, tuple(spec.grid), reproducible)
     _eval(spec.jaxpr, env, refs, np.ones(n, bool))
     return tuple(
         _to_storage(o[: math.prod(info.array_shape)].reshape(info.array_shape), info.dtype)
@@ -686,9 +708,9 @@ def _to_storage(a: np.ndarray, dtype: Any) -> np.ndarray:
     return from_float(a) if is_bf16(dtype) else a
 
 
-def interpret_call(call: Any, *args: Any) -> Any:
+def interpret_call(call: Any, *args: Any, math_mode: Any = None) -> Any:
     """Run a staged pallas_call on the CPU interpreter."""
     arrays = [np.asarray(a) for a in args]
     spec = trace(call, *arrays)
-    outs = interpret_spec(spec, *arrays)
+    outs = interpret_spec(spec, *arrays, math_mode=math_mode)
     return outs if call.multiple_results else outs[0]

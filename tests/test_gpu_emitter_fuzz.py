@@ -21,12 +21,16 @@ pytestmark = pytest.mark.gpu
 F = np.float32
 
 
-def _expr(rng, leaves, depth):
+def _expr(rng, leaves, depth, powers=False):
     if depth == 0 or rng.random() < 0.25:
         return leaves[rng.integers(len(leaves))] if rng.random() < 0.85 else float(np.float32(rng.uniform(-2, 2)))
-    op = rng.integers(9)
-    a = _expr(rng, leaves, depth - 1)
-    b = _expr(rng, leaves, depth - 1)
+    op = rng.integers(11 if powers else 9)
+    a = _expr(rng, leaves, depth - 1, powers)
+    b = _expr(rng, leaves, depth - 1, powers)
+    if op == 9:
+        return (jnp.abs(a) + 0.5) ** jnp.clip(b, -3.0, 3.0)
+    if op == 10:
+        return a * b + a * 0.75 - b * b
     if op == 0:
         return a + b
     if op == 1:
@@ -51,17 +55,17 @@ def _tame(v, dt=F):
     return jnp.broadcast_to(v if v.dtype == dt else v.astype(dt), (1,))
 
 
-def _make_kernel(seed):
+def _make_kernel(seed, powers=False):
     def kernel(x_ref, y_ref, o_ref, p_ref):
         rng = np.random.default_rng(seed)
         x, y = x_ref[...], y_ref[...]
         dt = x.dtype
-        v = _tame(_expr(rng, [x, y], 4), dt)
+        v = _tame(_expr(rng, [x, y], 4, powers), dt)
 
         def body(i, c):
             a, b, c3 = c
             r = np.random.default_rng(seed + 1)
-            na = _tame(_expr(r, [a, b, c3], 3), dt)
+            na = _tame(_expr(r, [a, b, c3], 3, powers), dt)
             return (b, c3, na) if seed % 2 else (na, a, b)  # permuted carries
 
         a, b, c = lax.fori_loop(0, 5 + seed % 7, body, (v, x, y))
@@ -107,3 +111,25 @@ def test_random_program_narrow_float_bit_exact_vs_interpreter(seed, dt):
     want = call.interpret(x, y)
     for g, w in zip(got, want):
         np.testing.assert_array_equal(np.ascontiguousarray(g).view(np.uint16), np.ascontiguousarray(w).view(np.uint16))
+
+
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+def test_random_program_reproducible_bit_exact_vs_interpreter(seed):
+    """The same grammar plus powers and sums of products, under REPRODUCIBLE
+    math: the emitter fuses single-use products into fused multiply-adds,
+    divides by the correctly rounded reciprocal and takes the fast
+    deterministic pow; the interpreter does the same in NumPy
+    (`palladium_amd.exact`), so every result agrees bit for bit."""
+    n = 300
+    rng = np.random.default_rng(300 + seed)
+    x = rng.uniform(-3, 3, n).astype(F)
+    y = rng.uniform(-3, 3, n).astype(F)
+    spec = pl.BlockSpec((1,), lambda i: (i,))
+    call = pa.hip_call(_make_kernel(seed, powers=True), grid=(n,), in_specs=[spec, spec], out_specs=(spec, spec),
+                       out_shape=(pl.ShapeDtypeStruct((n,), F),) * 2, math_mode="reproducible")
+    src = call.bound(x, y).hip_source
+    assert "__builtin_fmaf" in src[src.index('extern "C"'):]
+    got = call(x, y)
+    want = call.interpret(x, y)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)

@@ -198,3 +198,70 @@ def test_bs3_reproducible_oracle_against_float64_restatement():
     assert dev(r).max() <= dev(s).max() + 0.01
     assert dev(r).mean() <= dev(s).mean() + 0.01
     assert r[4].sum() <= 4 * F[4].sum() + 25 * len(sel)
+
+
+def test_exact_fma_f32_against_rational_arithmetic():
+    from fractions import Fraction
+
+    from palladium_amd import exact
+
+    r = np.random.default_rng(1)
+    a = r.standard_normal(3000).astype(np.float32)
+    b = (r.standard_normal(3000) * 10.0 ** r.integers(-20, 20, 3000)).astype(np.float32)
+    # near-cancelling addends, tiny ones, and subnormal results
+    c = np.concatenate([(-(a[:1000].astype(np.float64) * b[:1000]) * (1 + r.standard_normal(1000) * 1e-7)),
+                        r.standard_normal(1000) * 1e-30, np.full(1000, 1e-40)]).astype(np.float32)
+    a[2000:] *= np.float32(1e-20)
+    b[2000:] *= np.float32(1e-20)
+    got = exact.fma_f32(a, b, c)
+    for i in range(a.size):
+        ex = Fraction(float(a[i])) * Fraction(float(b[i])) + Fraction(float(c[i]))
+        cand = np.float32(float(ex))
+        near = [cand, np.nextafter(cand, np.float32(-np.inf)), np.nextafter(cand, np.float32(np.inf))]
+        best = min(near, key=lambda v: (abs(Fraction(float(v)) - ex), int(np.array(v).view(np.uint32)) & 1))
+        assert got[i] == best, (a[i], b[i], c[i])
+
+
+def test_exact_fma_f64_against_rational_arithmetic():
+    from fractions import Fraction
+
+    from palladium_amd import exact
+
+    r = np.random.default_rng(2)
+    a = r.standard_normal(3000) * 10.0 ** r.integers(-30, 30, 3000)
+    b = r.standard_normal(3000)
+    c = np.concatenate([-(a[:1000] * b[:1000]) * (1 + r.standard_normal(1000) * 1e-12),   # cancellation
+                        -(a[1000:2000] * b[1000:2000]) * r.uniform(0.3, 3.0, 1000),          # partial
+                        r.standard_normal(1000)])
+    got = exact.fma_f64(a, b, c)
+    for i in range(a.size):
+        want = float(Fraction(a[i]) * Fraction(b[i]) + Fraction(c[i]))   # correctly rounded
+        assert got[i] == want, (a[i], b[i], c[i])
+
+
+def test_numpy_rpow_equals_the_c_restatement():
+    from palladium_amd import exact
+
+    r = np.random.default_rng(4)
+    x = np.concatenate([(10.0 ** r.uniform(-37, 38, 200_000)), r.uniform(1, 1e9, 100_000)]).astype(np.float32)
+    y = np.concatenate([r.uniform(-5, 5, 200_000), np.full(100_000, 0.23333333)]).astype(np.float32)
+    np.testing.assert_array_equal(exact.rpow(x, y).view(np.uint32), oracle.rpow(x, y).view(np.uint32))
+
+
+def test_reproducible_interpreter_equals_the_c_bs3_restatement():
+    """The interpreter under REPRODUCIBLE math (the emitter's contraction
+    of the traced program, a * RN(1/b), the fast pow) against the hand-written
+    C restatement with fmaf at its 28 sites: every state and count equal,
+    which pins the contraction's site choice on both sides."""
+    n = 96
+    x0, v0, mu = bs3_inputs(n, seed=31)
+    import dataclasses
+
+    cfg = dataclasses.replace(BS3_CFG, t1=2.0)
+    got = bs3_vdp_call(n, cfg, math_mode="reproducible").interpret(x0, v0, mu)
+    want = oracle.bs3_vdp(x0, v0, mu, cfg, mode="reproducible")
+    for g, w, name in zip(got, want, ["t", "x", "v", "accepted", "rejected"]):
+        np.testing.assert_array_equal(g, w, err_msg=name)
+    # the IEEE-order interpreter of the same kernel equals the SAFE restatement instead
+    safe = bs3_vdp_call(n, cfg, math_mode="safe").interpret(x0, v0, mu)
+    assert any(not np.array_equal(a, b) for a, b in zip(safe, want))
