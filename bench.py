@@ -144,6 +144,22 @@ def bench_lv(steps: int, warmup: int, cpu: bool, cfg=None, block: int = 1, track
         safe_outs = [rt.Buffer.empty((n,), np.float32) for _ in outs]
         sms, _ = _timed_launches(safe_bound, [*ins, *safe_outs], max(1, steps // 4), 1)
         result["safe"] = {"ms_per_step": sms, "value": traj_steps / (sms / 1e3), "unit": "trajectory-steps/s"}
+        # REPRODUCIBLE: FAST's algebra with every operation deterministic, so
+        # a host restatement (oracle_lv_rk4_r) matches it bit for bit
+        rep_bound = lv_rk4_call(n, cfg.dt, cfg.steps, track_max=track_max, block=block, math_mode="reproducible",
+                                name="lv_rk4_reproducible").bound(*host)
+        rep_outs = [rt.Buffer.empty((n,), np.float32) for _ in outs]
+        rms, _ = _timed_launches(rep_bound, [*ins, *rep_outs], steps, 1)
+        result["reproducible"] = {"ms_per_step": rms, "value": traj_steps / (rms / 1e3), "unit": "trajectory-steps/s",
+                                  "frac": traj_steps * LV_FLOP_PER_STEP / (rms / 1e3) / FP32_PEAK}
+        if track_max:
+            import oracle
+
+            got = [b.to_numpy() for b in rep_outs]
+            want_r = oracle.lv_rk4_r(*host, cfg.dt, cfg.steps)
+            result["reproducible"]["bit_exact_vs_oracle"] = {
+                "trajectories": n, "against": "oracle_lv_rk4_r",
+                "equal": bool(all(np.array_equal(g, w) for g, w in zip(got, want_r)))}
     if cpu:
         import oracle
 
@@ -1432,6 +1448,7 @@ def main() -> int:
             r = fn(a.steps, a.warmup, cpu=False)
             res["secondary"][key] = {k: r[k] for k in ("metric", "value", "unit", "ms_per_step", "config", "roofline",
                                                         "accuracy", "accepted_steps_per_s", "price", "safe", "fast",
+                                                        "reproducible",
                                                         "fast_vs_oracle", "counts_equal_oracle",
                                                         "accuracy_vs_float64") if k in r}
     over = fractions_over_one(res)

@@ -32,9 +32,10 @@ enum {
  * RELAXED = FMA contraction; FAST = contraction, reassociation and
  * approximate transcendentals/division (infinities and NaNs still honoured).
  * PH_MATH_REPRODUCIBLE (no counterpart in the reference; the reference's
- * handler rejects 3 with InvalidArgument): fused multiply-adds at the sites
- * the emitter writes out, division as a times the correctly rounded 1/b,
- * and a deterministic pow, so a host restates the results bit for bit. */
+ * handler rejects 3 with InvalidArgument): FAST's algebra with fused
+ * multiply-adds at the sites the emitter writes out, division as a times
+ * the correctly rounded 1/b, and deterministic pow/log2/exp2, so a host
+ * restates the results bit for bit (compiled with -ffp-contract=off). */
 enum { PH_MATH_SAFE = 0, PH_MATH_RELAXED = 1, PH_MATH_FAST = 2, PH_MATH_REPRODUCIBLE = 3 };
 
 typedef struct ph_kernel ph_kernel;

@@ -117,6 +117,9 @@ def _declare_more(L):
     L.oracle_rpow_log.restype = ctypes.c_double
     L.oracle_rdiv.argtypes = [f, f]
     L.oracle_rdiv.restype = f
+    L.oracle_dlog2f_many.argtypes = [l, _F, _F]
+    L.oracle_dexp2f_many.argtypes = [l, _F, _F]
+    L.oracle_lv_rk4_r.argtypes = [l, _F, _F, _F, _F, _F, _F, ctypes.c_double, l, _F, _F, _F]
     L.oracle_gray_scott_step.argtypes = [l, _F, _F, f, f, f, f, f, _F, _F]
     L.oracle_gray_scott.argtypes = [l, l, _F, _F, _F, _F, f, f, f, f, f]
     L.oracle_df32_add.argtypes = [l] + [_F] * 6
@@ -187,6 +190,30 @@ def rpow(x, y) -> np.ndarray:
     y = np.ascontiguousarray(y.ravel())
     out = np.empty(x.size, np.float32)
     _lib2().oracle_rpow_many(x.size, _fp(x), _fp(y), _fp(out))
+    return out
+
+
+def lv_rk4_r(x0, y0, a, b, c, d, dt: float, steps: int):
+    """The REPRODUCIBLE mode's RK4 LV (FAST's algebra, fused multiply-adds at
+    the contraction's sites): (x, y, max|y|)."""
+    arrs = [np.ascontiguousarray(v, dtype=np.float32) for v in (x0, y0, a, b, c, d)]
+    n = arrs[0].size
+    outs = [np.empty(n, np.float32) for _ in range(3)]
+    _lib2().oracle_lv_rk4_r(n, *[_fp(v) for v in arrs], float(dt), int(steps), *[_fp(o) for o in outs])
+    return tuple(outs)
+
+
+def dlog2f(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.empty(x.size, np.float32)
+    _lib2().oracle_dlog2f_many(x.size, _fp(x), _fp(out))
+    return out
+
+
+def dexp2f(x) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.empty(x.size, np.float32)
+    _lib2().oracle_dexp2f_many(x.size, _fp(x), _fp(out))
     return out
 
 

@@ -396,19 +396,112 @@ void oracle_rpow_many(long n, const float *x, const float *y, float *out) {
   for (long i = 0; i < n; ++i) out[i] = oracle_rpow(x[i], y[i]);
 }
 
+/* The REPRODUCIBLE mode's float log2 and exp2 (device: ph_dlog2f,
+   ph_dexp2f): the double log2 and 2^z above, each rounded once to float.
+   log2: NaN for NaN and negative x, -inf for +-0, +inf for +inf,
+   log2(x 2^24) - 24 for a subnormal x. exp2: NaN for NaN, +inf or +0 for
+   |x| >= 2^20. */
+float oracle_dlog2f(float x) {
+  if (x != x) return x;
+  if (x < 0.0f) return NAN;
+  if (x == 0.0f) return -INFINITY;
+  if (x == INFINITY) return x;
+  if (x < 0x1p-126f) return (float)(oracle_rpow_log(x * 0x1p24f) - 24.0);
+  return (float)oracle_rpow_log(x);
+}
+
+float oracle_dexp2f(float x) {
+  if (x != x) return x;
+  if (!(fabsf(x) < 0x1p20f)) return x > 0.0f ? INFINITY : 0.0f;
+  return (float)oracle_rexp2((double)x);
+}
+
+void oracle_dlog2f_many(long n, const float *x, float *out) {
+  for (long i = 0; i < n; ++i) out[i] = oracle_dlog2f(x[i]);
+}
+
+void oracle_dexp2f_many(long n, const float *x, float *out) {
+  for (long i = 0; i < n; ++i) out[i] = oracle_dexp2f(x[i]);
+}
+
+/* ------------------------------------------------------------------------
+ * RK4 Lotka-Volterra under the REPRODUCIBLE mode: the program FAST's
+ * rewrites make of the traced step (palladium_amd/emit/optimize.py:
+ * factor_common_products, reuse_affine_shifts), with fmaf wherever the
+ * product contraction fuses a single-use product into its add or
+ * subtract. Per step, with h2 = f32(dt/2), h = f32(dt), h6 = f32(dt/6):
+ *   A = a - b y, C = c x - d          (the rhs as x A, y C)
+ *   stage k: the shifted state's A' = A - (b h_k) k_y, C' = C + (c h_k) k_x
+ *   k4 fused into the weighted sums, x' = x + h6 ((k1 + 2 k2) + 2 k3 + k4)
+ * statement for statement as the rewritten jaxpr.
+ * ---------------------------------------------------------------------- */
+void oracle_lv_rk4_r(long n, const float *x0, const float *y0, const float *a,
+                     const float *b, const float *c, const float *d, double dt,
+                     long steps, float *xo, float *yo, float *ymax) {
+  const float h2 = (float)(0.5 * dt);
+  const float h = (float)dt;
+  const float h6 = (float)(dt / 6.0);
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) {
+    float x = x0[i], y = y0[i];
+    const float ai = a[i], bi = b[i], ci = c[i], di = d[i];
+    float m = fabsf(y);
+    for (long s = 0; s < steps; ++s) {
+      float A = fmaf(-bi, y, ai);
+      float k1x = x * A;
+      float C = fmaf(ci, x, -di);
+      float k1y = y * C;
+      float xa = fmaf(h2, k1x, x);
+      float ya = fmaf(h2, k1y, y);
+      float A2 = fmaf(-(bi * h2), k1y, A);
+      float k2x = xa * A2;
+      float C2 = fmaf(ci * h2, k1x, C);
+      float k2y = ya * C2;
+      float xb = fmaf(h2, k2x, x);
+      float yb = fmaf(h2, k2y, y);
+      float A3 = fmaf(-(bi * h2), k2y, A);
+      float k3x = xb * A3;
+      float C3 = fmaf(ci * h2, k2x, C);
+      float k3y = yb * C3;
+      float xc = fmaf(h, k3x, x);
+      float yc = fmaf(h, k3y, y);
+      float A4 = fmaf(-(bi * h), k3y, A);
+      float C4 = fmaf(ci * h, k3x, C);
+      float sx = fmaf(2.0f, k2x, k1x);
+      sx = fmaf(2.0f, k3x, sx);
+      sx = fmaf(xc, A4, sx);
+      float nx = fmaf(h6, sx, x);
+      float sy = fmaf(2.0f, k2y, k1y);
+      sy = fmaf(2.0f, k3y, sy);
+      sy = fmaf(yc, C4, sy);
+      float ny = fmaf(h6, sy, y);
+      x = nx;
+      y = ny;
+      m = fmaxf(m, fabsf(y));
+    }
+    xo[i] = x;
+    yo[i] = y;
+    if (ymax) ymax[i] = m;
+  }
+}
+
 /* ------------------------------------------------------------------------
  * The adaptive BS3(2)+PI Van der Pol loop of oracle_bs3_vdp under the
  * REPRODUCIBLE mode: the same statements, with fmaf wherever the emitter's
  * product contraction (palladium_amd/emit/optimize.py:contract_products)
  * fuses a single-use product into its add or subtract, both error-norm
- * divisions and the reciprocal as a * RN(1/b), and the fast pow. Fused
- * sites, in the kernel's order:
+ * divisions as a * RN(1/b), and the controller as FAST's power-law rewrite
+ * makes it (power_laws_to_exp2, carry_logs): the factor is
+ * 2^(log2 0.9 - c1 log2 err + c2 L) with L the carried log2 of
+ * prev_inv_err, in the deterministic float log2 and exp2. Fused sites, in
+ * the kernel's order:
  *   stage states      x + h k         -> fmaf(h, k, x)
  *   right-hand side   1 - x*x         -> fmaf(-x, x, 1)
  *                     (mu a) v - x    -> fmaf(mu a, v, -x)
  *   weighted sums     p1 + c2 k2      -> fmaf(c2, k2, p1), and so on
  *   updates           x + dt s        -> fmaf(dt, s, x)
  *   tolerance         atol + rtol|y|  -> fmaf(rtol, |y|, atol)
+ *   controller        log2 0.9 - c1 le, then + c2 L -> two fmaf
  * ---------------------------------------------------------------------- */
 static inline void vdp_rhs_r(float mu, float x, float v, float *fx, float *fv) {
   float a = fmaf(-x, x, 1.0f);
@@ -422,14 +515,15 @@ void oracle_bs3_vdp_r(long n, const float *x0, const float *v0, const float *mu_
                       float *to, float *xo, float *vo, int32_t *acc_out, int32_t *rej_out) {
   const float coeff1 = (float)((0.3 + 0.4) / 3.0);
   const float coeff2 = (float)(-0.4 / 3.0);
+  const float log2_09 = -0x1.374d6ap-3f; /* f32(log2(f32(0.9))), as the rewrite folds it */
   const float b1 = (float)(2.0 / 9.0), b2 = (float)(1.0 / 3.0), b3 = (float)(4.0 / 9.0);
   const float e1 = (float)(7.0 / 24.0), e2 = 0.25f, e3 = (float)(1.0 / 3.0), e4 = 0.125f;
 #pragma omp parallel for schedule(dynamic, 64)
   for (long i = 0; i < n; ++i) {
     const float mu = mu_in[i];
     float x = x0[i], v = v0[i];
-    float t = 0.0f, dt = dt0, prev = 1.0f;
-    double prev_log = oracle_rpow_log(1.0f);
+    float t = 0.0f, dt = dt0;
+    float prev_log = oracle_dlog2f(1.0f);
     float k1x, k1v;
     vdp_rhs_r(mu, x, v, &k1x, &k1v);
     int32_t acc = 0, rej = 0, it = 0;
@@ -467,18 +561,19 @@ void oracle_bs3_vdp_r(long n, const float *x0, const float *v0, const float *mu_
       float kx = accept ? k4x : k1x;
       float kv = accept ? k4v : k1v;
       err = fmaxf(err, 1e-9f);
-      float inv = oracle_rdiv(1.0f, err);
-      double inv_log = oracle_rpow_log(inv);
-      float f = 0.9f * oracle_rpow_with_log(inv, coeff1, inv_log);
-      f = f * oracle_rpow_with_log(prev, coeff2, prev_log);
-      float pn = accept ? inv : prev;
-      double pln = accept ? inv_log : prev_log;
+      /* 0.9 (1/err)^c1 prev^c2 as 2^(log2 0.9 - c1 log2 err + c2 log2 prev),
+         the carry held as its log2 */
+      float le = oracle_dlog2f(err);
+      float z = fmaf(-coeff1, le, log2_09);
+      z = fmaf(coeff2, prev_log, z);
+      float f = oracle_dexp2f(z);
+      float pln = accept ? -le : prev_log;
       float cl = fminf(10.0f, fmaxf(0.2f, f));
       dt = dt * cl;
       acc = acc + (accept ? 1 : 0);
       rej = rej + (accept ? 0 : 1);
       it = it + 1;
-      t = t2; x = xn; v = vn; k1x = kx; k1v = kv; prev = pn; prev_log = pln;
+      t = t2; x = xn; v = vn; k1x = kx; k1v = kv; prev_log = pln;
     }
     to[i] = t; xo[i] = x; vo[i] = v; acc_out[i] = acc; rej_out[i] = rej;
   }

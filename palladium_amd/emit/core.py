@@ -522,13 +522,15 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
     def keeps_compaction(candidate: Jaxpr) -> bool:
         return (plan_for(spec, candidate, lanes, block) is not None) == compacting
 
-    if math_mode is not None and math_mode_ordinal(math_mode) == 2:
+    if math_mode is not None and math_mode_ordinal(math_mode) in (2, 3):
+        # REPRODUCIBLE takes FAST's algebra too; its lowering keeps every
+        # operation deterministic
         from palladium_amd.emit.optimize import fast_rewrites
 
         rewritten = fast_rewrites(body)
         if keeps_compaction(rewritten):
             body = rewritten
-    elif (math_mode is not None and math_mode_ordinal(math_mode) in (0, 3)
+    if (math_mode is not None and math_mode_ordinal(math_mode) in (0, 3)
           and os.environ.get("PALLADIUM_SHARE_POW_LOGS", "1") != "0"):
         from palladium_amd.emit.optimize import share_pow_logs
 

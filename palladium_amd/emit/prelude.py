@@ -24,7 +24,9 @@
   (x = m 2^e, m in [sqrt(1/2), sqrt(2)), t = (m-1)/(m+1) by a quadratic
   start and two Newton steps, a degree-4 polynomial in t^2) and 2^z
   (z = k + r, a degree-7 polynomial in r), in double; any other operand takes the SAFE `ph_pow` in a branch that a
-  wavefront enters only when one of its lanes needs it.
+  wavefront enters only when one of its lanes needs it. `ph_dlog2f` and
+  `ph_dexp2f`, what the power-law rewrite's log2 and exp2 become in this
+  mode, are the same double log2 and 2^z rounded once to float.
 - `ph_exp2`/`ph_log2`: under FAST the hardware base-2 exponential and
   logarithm; libm otherwise.
 - `ph_sin`/`ph_cos`: under FAST the hardware sine/cosine (the reference's
@@ -319,6 +321,45 @@ __device__ __forceinline__ float ph_rpow_with_log(float x, float y, double lg) {
 }
 
 __device__ __forceinline__ float ph_rpow(float x, float y) { return ph_rpow_with_log(x, y, ph_rpow_log(x)); }
+
+/* The wavefront mask of lanes where |x| < limit fails (|x| >= limit or x
+   NaN), as a scalar, like ph_class_mask. */
+__device__ __forceinline__ unsigned long long ph_wide_mask(float x, float limit) {
+    unsigned long long m;
+    __asm__ volatile("v_cmp_nlt_f32_e64 %0, |%1|, %2" : "=s"(m) : "v"(x), "s"(limit));
+    return m;
+}
+
+/* Deterministic float log2 and exp2 (what the power-law rewrite's log2 and
+   exp2 become under REPRODUCIBLE): the double log2 of ph_rpow_log and the
+   double 2^z of ph_rexp2, each rounded once to float. Special operands
+   take a branch a wavefront enters only when one of its lanes needs it:
+   log2 of NaN is NaN, of a negative number NaN, of +-0 -inf, of +inf +inf,
+   of a subnormal x log2(x 2^24) - 24; exp2 of NaN is NaN and of |x| >= 2^20
+   +inf or +0. */
+__device__ __noinline__ float ph_dlog2f_slow(float x) {
+    if (x != x) return x;
+    if (x < 0.0f) return __builtin_nanf("");
+    if (x == 0.0f) return -__builtin_inff();
+    if (x == __builtin_inff()) return x;
+    return (float)(ph_rpow_log(x * 0x1p24f) - 24.0);
+}
+
+__device__ __forceinline__ float ph_dlog2f(float x) {
+    float r = (float)ph_rpow_log(x);
+    if (__builtin_expect(ph_class_mask(x, 0x2ff) != 0ull, 0))
+        r = __builtin_amdgcn_classf(x, 0x2ff) ? ph_dlog2f_slow(x) : r;
+    return r;
+}
+
+__device__ __noinline__ float ph_dexp2f_slow(float x) { return x != x ? x : (x > 0.0f ? __builtin_inff() : 0.0f); }
+
+__device__ __forceinline__ float ph_dexp2f(float x) {
+    float r = (float)ph_rexp2((double)x);
+    if (__builtin_expect(ph_wide_mask(x, 0x1p20f) != 0ull, 0))
+        r = !(__builtin_fabsf(x) < 0x1p20f) ? ph_dexp2f_slow(x) : r;
+    return r;
+}
 #elif PH_MATH_MODE == 2
 /* FAST: x^y = 2^(y log2 x) on the hardware base-2 logarithm and
    exponential (v_log_f32, v_exp_f32) for a positive normal finite base and

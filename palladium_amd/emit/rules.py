@@ -199,6 +199,8 @@ _REPRODUCIBLE_F32 = {
     "pow": "ph_rpow({a}, {b})",
     "pow_log": "ph_rpow_log({a})",
     "pow_with_log": "ph_rpow_with_log({a}, {b}, {c})",
+    "log2": "ph_dlog2f({a})",
+    "exp2": "ph_dexp2f({a})",
 }
 
 

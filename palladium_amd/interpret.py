@@ -249,6 +249,10 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int, reproducible:
             r = exact.rdiv(a, b)
         elif name == "pow" and reproducible and dt == np.float32:
             r = exact.rpow(a, b)
+        elif name == "log2" and reproducible and dt == np.float32:
+            r = exact.dlog2f(a)
+        elif name == "exp2" and reproducible and dt == np.float32:
+            r = exact.dexp2f(a)
         elif name == "div":
             r = a / b if isf else _int_div(a, b, dt)
         elif name == "rem":
@@ -656,17 +660,17 @@ def check_block_bounds(spec: KernelSpec) -> None:
 def interpret_spec(spec: KernelSpec, *arrays: np.ndarray, math_mode: Any = None) -> tuple[np.ndarray, ...]:
     """Run a KernelSpec on the CPU. Float operations are IEEE, in the traced
     order (SAFE's semantics). With `math_mode` REPRODUCIBLE the program
-    first goes through the emitter's product contraction and float32
-    division and power take that mode's forms (`palladium_amd.exact`), so the
-    results are the device's bit for bit for everything but the
-    transcendentals."""
+    first goes through the emitter's rewrites for that mode (FAST's algebra,
+    then the product contraction) and float32 division, power, log2 and exp2
+    take that mode's forms (`palladium_amd.exact`), so the results are the
+    device's bit for bit for everything but the other transcendentals."""
     from palladium_amd.runtime import REPRODUCIBLE_ORDINAL, math_mode_ordinal
 
     reproducible = math_mode is not None and math_mode_ordinal(math_mode) == REPRODUCIBLE_ORDINAL
     if reproducible:
-        from palladium_amd.emit.optimize import contract_products
+        from palladium_amd.emit.optimize import contract_products, fast_rewrites
 
-        spec = dataclasses.replace(spec, jaxpr=contract_products(spec.jaxpr))
+        spec = dataclasses.replace(spec, jaxpr=contract_products(fast_rewrites(spec.jaxpr)))
     n = spec.num_programs
     pids = _grid_pids(tuple(spec.grid))
     refs = []

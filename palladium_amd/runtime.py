@@ -55,13 +55,15 @@ class MathMode(str, enum.Enum):
     square root, deterministic `pow`. RELAXED: FMA contraction. FAST
     (default, as in the reference): contraction, reassociation, approximate
     transcendentals and division; infinities and NaNs are still honoured.
-    REPRODUCIBLE (no counterpart in the reference): results a host can
-    restate bit for bit, with fast arithmetic. A float32 `a*b + c` whose
-    product has no other use becomes one fused multiply-add (correctly
+    REPRODUCIBLE (no counterpart in the reference): FAST's algebra with
+    every operation deterministic, so a host restates the results bit for
+    bit. The program takes FAST's jaxpr rewrites (common factors, affine
+    shifts, power laws as exp2/log2, carried logs); then a float32 `a*b + c`
+    whose product has no other use becomes one fused multiply-add (correctly
     rounded, so C's `fmaf` gives the same value); float32 `a / b` is
-    `a * RN(1/b)` (the reciprocal correctly rounded, the product rounded
-    once); `pow` is a fast deterministic double-precision power (about
-    2^-34 relative before the float rounding). Everything else is as SAFE.
+    `a * RN(1/b)`; `pow`, `log2` and `exp2` are deterministic
+    double-precision functions rounded once to float. Other transcendentals
+    and everything else are as SAFE.
     """
 
     SAFE = "safe"

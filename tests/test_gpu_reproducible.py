@@ -124,3 +124,21 @@ def test_bs3_attempt_cap_exact():
     for g, w in zip(got, want):
         np.testing.assert_array_equal(g, w)
     assert np.all(got[3] + got[4] <= 37)
+
+
+def test_lv_config1_reproducible_bit_exact():
+    """Config 1 in full (10^6 trajectories, 4,000 steps, max|y|) under
+    REPRODUCIBLE: FAST's common-factor and affine-shift rewrites with fused
+    multiply-adds at the contraction's sites, equal bit for bit to
+    oracle_lv_rk4_r, and within FAST's 1e-3 of the SAFE-order oracle."""
+    from palladium_amd.workloads import LV_CFG1, lv_inputs, lv_rk4_call
+
+    n = 1_000_000
+    args = lv_inputs(n, 1)
+    print(f"[reproducible] lv_rk4 n={n} steps={LV_CFG1.steps}", flush=True)
+    got = lv_rk4_call(n, LV_CFG1.dt, LV_CFG1.steps, track_max=True, math_mode="reproducible")(*args)
+    want = oracle.lv_rk4_r(*args, LV_CFG1.dt, LV_CFG1.steps)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g, w)
+    safe = oracle.lv_rk4(*args[:], LV_CFG1.dt, LV_CFG1.steps, track_max=True)
+    np.testing.assert_allclose(got[0], safe[0], rtol=1e-3)
