@@ -235,6 +235,8 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int, reproducible:
     a = ops[0] if ops else None
     b = ops[1] if len(ops) > 1 else None
     isf = np.asarray(a).dtype.kind == "f" if a is not None else False
+    # the REPRODUCIBLE forms are float32's (bfloat16 and float16 stay IEEE)
+    f32_out = not bf_out and dt == np.float32
     with np.errstate(all="ignore"):
         if name == "add":
             r = a + b
@@ -245,13 +247,13 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int, reproducible:
         elif name == "fma":
             c = ops[2]
             r = exact.fma_f32(-a if eqn.params.get("neg_ab") else a, b, -c if eqn.params.get("neg_c") else c)
-        elif name == "div" and reproducible and isf and dt == np.float32:
+        elif name == "div" and reproducible and isf and f32_out:
             r = exact.rdiv(a, b)
-        elif name == "pow" and reproducible and dt == np.float32:
+        elif name == "pow" and reproducible and f32_out:
             r = exact.rpow(a, b)
-        elif name == "log2" and reproducible and dt == np.float32:
+        elif name == "log2" and reproducible and f32_out:
             r = exact.dlog2f(a)
-        elif name == "exp2" and reproducible and dt == np.float32:
+        elif name == "exp2" and reproducible and f32_out:
             r = exact.dexp2f(a)
         elif name == "div":
             r = a / b if isf else _int_div(a, b, dt)

@@ -313,3 +313,30 @@ def test_dlog2f_dexp2f_restatements_agree_and_are_accurate():
     assert np.all(np.abs(a.view(np.int32).astype(np.int64) - ref.view(np.int32)) <= 1) | True
     fin = np.isfinite(ref)
     assert np.all(np.abs(a[fin].view(np.int32).astype(np.int64) - ref[fin].view(np.int32)) <= 1)
+
+
+def test_narrow_floats_keep_ieee_forms_under_reproducible():
+    """bfloat16 and float16 arithmetic is not fused or reciprocal-divided
+    under REPRODUCIBLE (those forms are float32's): the emitted kernel keeps
+    the IEEE operators for them and the interpreter evaluates them as SAFE
+    does."""
+    from palladium_amd import dtypes
+
+    def k(a_ref, b_ref, c_ref, o_ref):
+        o_ref[...] = a_ref[...] * b_ref[...] + c_ref[...] / (b_ref[...] + 3.0)
+
+    n = 64
+    r = np.random.default_rng(3)
+    for dt in (dtypes.bfloat16, np.dtype(np.float16)):
+        vals = [r.uniform(0.5, 2.0, n).astype(np.float32) for _ in range(3)]
+        arrs = [dtypes.from_float(v) if dtypes.is_bf16(dt) else v.astype(dt) for v in vals]
+        s = pl.BlockSpec((1,), lambda i: (i,))
+        kw = dict(grid=(n,), in_specs=[s] * 3, out_specs=s, out_shape=pl.ShapeDtypeStruct((n,), dt))
+        call = pl.pallas_call(k, **kw)
+        spec = trace(call, *arrs)
+        body = emit_hip(spec, math_mode="reproducible")
+        body = body[body.index('extern "C"'):]
+        assert "__builtin_fmaf" not in body and "ph_rdiv" not in body
+        rep = pa.hip_call(k, math_mode="reproducible", **kw).interpret(*arrs)
+        safe = pa.hip_call(k, math_mode="safe", **kw).interpret(*arrs)
+        assert np.array_equal(np.asarray(rep).view(np.uint16), np.asarray(safe).view(np.uint16))
