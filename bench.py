@@ -377,6 +377,19 @@ def bench_gbm(steps: int, warmup: int, cpu: bool) -> dict:
                              "rel_max_payoff_above_1": float((d[big] / want[big]).max()),
                              "zero_nonzero_flips": int(np.sum((got == 0) != (want == 0))),
                              "mean_payoff_rel_shift": float((got.mean() - want.mean()) / want.mean())}
+    # REPRODUCIBLE: FAST's algebra with deterministic log, cos and exp, so a
+    # host restatement (oracle_gbm_r) matches every path bit for bit
+    rep_bound = gbm_call(cfg, math_mode="reproducible", name="gbm_paths_reproducible").bound(key)
+    rep_ops = [ops[0], rt.Buffer.empty((cfg.n_paths,), np.float32)]
+    rms, ravg = _timed_launches(rep_bound, rep_ops, steps, 1)
+    got_r = rep_ops[1].to_numpy(rep_bound.stream)
+    want_r = oracle.gbm(cfg, cfg.n_paths, mode="reproducible")
+    res["reproducible"] = {
+        "ms_per_step": rms, "value": ps / (rms / 1e3), "unit": "path-steps/s",
+        "issue": issue_fraction(rt.compile_code_object(rep_bound.hip_source, rep_bound.spec.name, "reproducible"),
+                                ps, ravg),
+        "bit_exact_vs_oracle": {"paths": cfg.n_paths, "against": "oracle_gbm_r",
+                                "equal": bool(np.array_equal(got_r.view(np.uint32), want_r.view(np.uint32)))}}
     if cpu:
         n_cpu = cfg.n_paths
         res["cpu_baseline"] = {"value": n_cpu * cfg.n_steps / dt, "unit": "path-steps/s", "cores": _cpu_cores(),

@@ -119,6 +119,9 @@ def _declare_more(L):
     L.oracle_rdiv.restype = f
     L.oracle_dlog2f_many.argtypes = [l, _F, _F]
     L.oracle_dexp2f_many.argtypes = [l, _F, _F]
+    for fn in ("dexpf", "dlogf", "dsinf", "dcosf"):
+        getattr(L, f"oracle_{fn}_many").argtypes = [l, _F, _F]
+    L.oracle_gbm_r.argtypes = [l, l, l, u, u, f, f, f, f, f, _F]
     L.oracle_lv_rk4_r.argtypes = [l, _F, _F, _F, _F, _F, _F, ctypes.c_double, l, _F, _F, _F]
     L.oracle_gray_scott_step.argtypes = [l, _F, _F, f, f, f, f, f, _F, _F]
     L.oracle_gray_scott.argtypes = [l, l, _F, _F, _F, _F, f, f, f, f, f]
@@ -135,12 +138,17 @@ def _lib2():
     return L
 
 
-def gbm(cfg, n_paths: int, first_path: int = 0) -> np.ndarray:
-    """Per-path undiscounted call payoff for paths [first, first+n)."""
+def gbm(cfg, n_paths: int, first_path: int = 0, mode: str = "ieee") -> np.ndarray:
+    """Per-path undiscounted call payoff for paths [first, first+n): IEEE
+    float ops with libm's transcendentals ("ieee"), or the REPRODUCIBLE
+    kernel's program bit for bit ("reproducible")."""
+    if mode not in ("ieee", "reproducible"):
+        raise ValueError(f"mode must be 'ieee' or 'reproducible', got {mode!r}")
     out = np.empty(n_paths, np.float32)
     key = (0, cfg.seed)
     two_pi = float(np.float32(2.0 * np.pi))
-    _lib2().oracle_gbm(n_paths, first_path, cfg.n_steps, key[0], key[1], float(np.float32(cfg.s0)),
+    fn = _lib2().oracle_gbm if mode == "ieee" else _lib2().oracle_gbm_r
+    fn(n_paths, first_path, cfg.n_steps, key[0], key[1], float(np.float32(cfg.s0)),
                        float(np.float32(cfg.strike)), float(np.float32(cfg.drift_dt)),
                        float(np.float32(cfg.vol_sqdt)), two_pi, _fp(out))
     return out
@@ -215,6 +223,29 @@ def dexp2f(x) -> np.ndarray:
     out = np.empty(x.size, np.float32)
     _lib2().oracle_dexp2f_many(x.size, _fp(x), _fp(out))
     return out
+
+
+def _many(name: str, x) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32).ravel()
+    out = np.empty(x.size, np.float32)
+    getattr(_lib2(), f"oracle_{name}_many")(x.size, _fp(x), _fp(out))
+    return out
+
+
+def dexpf(x) -> np.ndarray:
+    return _many("dexpf", x)
+
+
+def dlogf(x) -> np.ndarray:
+    return _many("dlogf", x)
+
+
+def dsinf(x) -> np.ndarray:
+    return _many("dsinf", x)
+
+
+def dcosf(x) -> np.ndarray:
+    return _many("dcosf", x)
 
 
 def rdiv(a: float, b: float) -> np.float32:

@@ -424,6 +424,135 @@ void oracle_dexp2f_many(long n, const float *x, float *out) {
   for (long i = 0; i < n; ++i) out[i] = oracle_dexp2f(x[i]);
 }
 
+/* The REPRODUCIBLE mode's float exp, log, sin and cos (device: ph_dexpf,
+   ph_dlogf, ph_dtrig in palladium_amd/emit/prelude.py).
+   exp: 2^(x log2 e), the product rounded to double; NaN for NaN, +inf or
+   +0 for |x| >= 2^19. log: the double log2 times ln 2; special operands as
+   oracle_dlog2f. sin/cos: x = k pi/2 + r, k = rint(x 2/pi) and
+   r = fma(-k, PIO2_LO, fma(-k, PIO2_HI, x)) for |x| < 2^20 (PIO2_HI carries
+   33 bits, so the inner FMA is exact); beyond, the exact reduction
+   x 2/pi mod 4 from a 96-bit window of the bits of 2/pi (x = M 2^e), kept
+   to 2^-62; sin r = r S(r^2), cos r = C(r^2) (degree 5, from
+   oracle/gen_rpow_coeffs.py) and the quadrant picks +-sin r or +-cos r;
+   NaN for infinities and NaN. */
+float oracle_dexpf(float x) {
+  if (x != x) return x;
+  if (!(fabsf(x) < 0x1p19f)) return x > 0.0f ? INFINITY : 0.0f;
+  return (float)oracle_rexp2((double)x * 1.4426950408889634);
+}
+
+float oracle_dlogf(float x) {
+  if (x != x) return x;
+  if (x < 0.0f) return NAN;
+  if (x == 0.0f) return -INFINITY;
+  if (x == INFINITY) return x;
+  if (x < 0x1p-126f) return (float)((oracle_rpow_log(x * 0x1p24f) - 24.0) * 0.6931471805599453);
+  return (float)(oracle_rpow_log(x) * 0.6931471805599453);
+}
+
+static float dtrig_poly(double r, int q) {
+  double s = r * r;
+  double ps = fma(s, -2.47565580235085e-08, 2.7555271883000814e-06);
+  double pc = fma(s, -2.717342886965949e-07, 2.47989287418407e-05);
+  ps = fma(ps, s, -0.0001984126329834066);
+  pc = fma(pc, s, -0.0013888880393711728);
+  ps = fma(ps, s, 0.008333333323878053);
+  pc = fma(pc, s, 0.04166666654390994);
+  ps = fma(ps, s, -0.16666666666616684);
+  pc = fma(pc, s, -0.4999999999935111);
+  ps = fma(ps, s, 0.9999999999999957);
+  pc = fma(pc, s, 0.9999999999999444);
+  double v = (q & 1) ? pc : r * ps;
+  return (float)((q & 2) ? -v : v);
+}
+
+static const uint32_t two_over_pi[7] = {0xA2F9836Eu, 0x4E441529u, 0xFC2757D1u, 0xF534DDC0u,
+                                        0xDB629599u, 0x3C439041u, 0xFE5163ABu};
+
+static float dtrig(float x, int off) {
+  if (!(fabsf(x) < INFINITY)) return NAN;
+  if (fabsf(x) < 0x1p20f) {
+    double xd = (double)x;
+    double k = rint(xd * 0.6366197723675814);
+    double r = fma(-k, 0x1.921fb544p+0, xd);
+    r = fma(-k, 0x1.0b4611a626331p-34, r);
+    return dtrig_poly(r, (int)k + off);
+  }
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  int e = (int)((b >> 23) & 0xffu) - 150;
+  unsigned __int128 m = (b & 0x7fffffu) | 0x800000u;
+  int i0 = e >= 2 ? e - 1 : 1;
+  int j = (i0 - 1) >> 5, sh = (i0 - 1) & 31;
+  unsigned __int128 w = ((unsigned __int128)two_over_pi[j] << 96) | ((unsigned __int128)two_over_pi[j + 1] << 64) |
+                        ((unsigned __int128)two_over_pi[j + 2] << 32) | two_over_pi[j + 3];
+  w = (w << sh) >> 32;
+  int n = 97 - e + i0;
+  unsigned __int128 p = (m * w) & ((((unsigned __int128)1) << n) - 1);
+  int q = (int)(p >> (n - 2)) & 3;
+  long long f = (long long)((uint64_t)(p >> (n - 64)) & ((1ull << 62) - 1));
+  if (f >= (1ll << 61)) { f -= (1ll << 62); q += 1; }
+  double r = (double)f * 0x1.921fb54442d18p-62;
+  if (b >> 31) { r = -r; q = -q; }
+  return dtrig_poly(r, q + off);
+}
+
+float oracle_dsinf(float x) { return dtrig(x, 0); }
+float oracle_dcosf(float x) { return dtrig(x, 1); }
+
+void oracle_dexpf_many(long n, const float *x, float *out) {
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) out[i] = oracle_dexpf(x[i]);
+}
+void oracle_dlogf_many(long n, const float *x, float *out) {
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) out[i] = oracle_dlogf(x[i]);
+}
+void oracle_dsinf_many(long n, const float *x, float *out) {
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) out[i] = oracle_dsinf(x[i]);
+}
+void oracle_dcosf_many(long n, const float *x, float *out) {
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) out[i] = oracle_dcosf(x[i]);
+}
+
+/* ------------------------------------------------------------------------
+ * GBM Monte Carlo under the REPRODUCIBLE mode: the program FAST's rewrites
+ * and the contraction pass make of palladium_amd.workloads.gbm_kernel's
+ * step (the redundant clamp of each uniform at 0 dropped, drift + vol z as
+ * one fmaf), with exp, log and cos the deterministic forms above and sqrtf
+ * correctly rounded, statement for statement. Same counters, conversion
+ * and layout as oracle_gbm.
+ * ---------------------------------------------------------------------- */
+void oracle_gbm_r(long n_paths, long first_path, long n_steps, uint32_t k0, uint32_t k1,
+                  float s0, float strike, float drift, float vol, float two_pi,
+                  float *payoff) {
+#pragma omp parallel for schedule(static)
+  for (long p = 0; p < n_paths; ++p) {
+    uint32_t path = (uint32_t)(first_path + p);
+    float s = s0;
+    for (long i = 0; i < n_steps; ++i) {
+      uint32_t b0, b1, f0, f1;
+      oracle_threefry2x32(k0, k1, path, (uint32_t)i, &b0, &b1);
+      f0 = (b0 >> 9) | 0x3f800000u;
+      f1 = (b1 >> 9) | 0x3f800000u;
+      float u1, u2;
+      memcpy(&u1, &f0, 4);
+      memcpy(&u2, &f1, 4);
+      u1 = fmaxf(fmaf(u1 - 1.0f, 1.0f, 0.0f), 1e-7f);
+      u2 = fmaf(u2 - 1.0f, 1.0f, 0.0f);
+      float l = oracle_dlogf(u1);
+      float r = sqrtf(-2.0f * l);
+      float c = oracle_dcosf(two_pi * u2);
+      float z = r * c;
+      float e = oracle_dexpf(fmaf(vol, z, drift));
+      s = s * e;
+    }
+    payoff[p] = fmaxf(s - strike, 0.0f);
+  }
+}
+
 /* ------------------------------------------------------------------------
  * RK4 Lotka-Volterra under the REPRODUCIBLE mode: the program FAST's
  * rewrites make of the traced step (palladium_amd/emit/optimize.py:

@@ -30,7 +30,11 @@
 - `ph_exp2`/`ph_log2`: under FAST the hardware base-2 exponential and
   logarithm; libm otherwise.
 - `ph_sin`/`ph_cos`: under FAST the hardware sine/cosine (the reference's
-  FAST contract allows approximate transcendentals); libm-accurate otherwise.
+  FAST contract allows approximate transcendentals); libm-accurate under
+  SAFE and RELAXED. Under REPRODUCIBLE, `ph_exp`, `ph_log`, `ph_sin`,
+  `ph_cos`, `ph_exp2` and `ph_log2` are deterministic double-core forms
+  (`ph_dexpf`, `ph_dlogf`, `ph_dtrig`, `ph_dexp2f`, `ph_dlog2f`) that
+  `palladium_amd.exact` and `oracle/oracle.c` restate bit for bit.
 - `ph_fmin`/`ph_fmax`: NaN-suppressing min/max (C fminf/fmaxf), the
   reference's lowering of `min`/`max` (`src/palladium/emit/core.py:574-575`).
 """
@@ -83,12 +87,14 @@ __device__ __forceinline__ float ph_exp(float x) { return __builtin_amdgcn_exp2f
 /* v_exp_f32 / v_log_f32: 2^x and log2(x), 1 ulp, subnormals flushed. */
 __device__ __forceinline__ float ph_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float ph_log2(float x) { return __builtin_amdgcn_logf(x); }
-#else
+__device__ __forceinline__ float ph_log(float x) { return logf(x); }
+#elif PH_MATH_MODE != 3
 __device__ __forceinline__ float ph_exp2(float x) { return exp2f(x); }
 __device__ __forceinline__ float ph_log2(float x) { return log2f(x); }
 __device__ __forceinline__ float ph_sin(float x) { return sinf(x); }
 __device__ __forceinline__ float ph_cos(float x) { return cosf(x); }
 __device__ __forceinline__ float ph_exp(float x) { return expf(x); }
+__device__ __forceinline__ float ph_log(float x) { return logf(x); }
 #endif
 
 /* Integer division and float->integer conversion with every input defined,
@@ -360,6 +366,103 @@ __device__ __forceinline__ float ph_dexp2f(float x) {
         r = !(__builtin_fabsf(x) < 0x1p20f) ? ph_dexp2f_slow(x) : r;
     return r;
 }
+
+/* Deterministic float exp and log on the same double cores: e^x as
+   2^(x log2 e), the product rounded once to double (error below 2^-46
+   absolute in the exponent for |x| < 2^19), and ln x as the double log2
+   times ln 2. Special operands as ph_dexp2f (|x| >= 2^19 here) and
+   ph_dlog2f. */
+__device__ __forceinline__ float ph_dexpf(float x) {
+    float r = (float)ph_rexp2((double)x * 1.4426950408889634);
+    if (__builtin_expect(ph_wide_mask(x, 0x1p19f) != 0ull, 0))
+        r = !(__builtin_fabsf(x) < 0x1p19f) ? ph_dexp2f_slow(x) : r;
+    return r;
+}
+
+__device__ __noinline__ float ph_dlogf_slow(float x) {
+    if (x != x) return x;
+    if (x < 0.0f) return __builtin_nanf("");
+    if (x == 0.0f) return -__builtin_inff();
+    if (x == __builtin_inff()) return x;
+    return (float)((ph_rpow_log(x * 0x1p24f) - 24.0) * 0.6931471805599453);
+}
+
+__device__ __forceinline__ float ph_dlogf(float x) {
+    float r = (float)(ph_rpow_log(x) * 0.6931471805599453);
+    if (__builtin_expect(ph_class_mask(x, 0x2ff) != 0ull, 0))
+        r = __builtin_amdgcn_classf(x, 0x2ff) ? ph_dlogf_slow(x) : r;
+    return r;
+}
+
+/* Deterministic float sine and cosine. x = k pi/2 + r with |r| <= pi/4
+   (plus rounding); sin r = r S(r^2) and cos r = C(r^2), S and C of degree 5
+   in double (relative errors 2^-47.6 and 2^-43.5), and the quadrant
+   (k + off) mod 4 picks +-sin r or +-cos r (off = 0 for sine, 1 for cosine),
+   rounded once to float. For |x| < 2^20, k = rint(x 2/pi) and
+   r = (x - k PIO2_HI) - k PIO2_LO by two FMAs, the first exact (PIO2_HI has
+   33 significant bits and k at most 20). Larger finite x take the exact
+   reduction of the slow path: x 2/pi mod 4 from a 96-bit window of the
+   bits of 2/pi (x = M 2^E, M 24 bits, the product kept to 2^-62 below the
+   binary point), in a branch a wavefront enters only when one of its lanes
+   needs it; infinities and NaN give NaN. Coefficients:
+   oracle/gen_rpow_coeffs.py. */
+__device__ __forceinline__ float ph_dtrig_poly(double r, int q) {
+    double s = r * r;
+    double ps = ph_fma_k(s, -2.47565580235085e-08, 2.7555271883000814e-06);
+    double pc = ph_fma_k(s, -2.717342886965949e-07, 2.47989287418407e-05);
+    ps = ph_fma_k(ps, s, -0.0001984126329834066);
+    pc = ph_fma_k(pc, s, -0.0013888880393711728);
+    ps = ph_fma_k(ps, s, 0.008333333323878053);
+    pc = ph_fma_k(pc, s, 0.04166666654390994);
+    ps = ph_fma_k(ps, s, -0.16666666666616684);
+    pc = ph_fma_k(pc, s, -0.4999999999935111);
+    ps = ph_fma_k(ps, s, 0.9999999999999957);
+    pc = ph_fma_k(pc, s, 0.9999999999999444);
+    double v = (q & 1) ? pc : r * ps;
+    return (float)((q & 2) ? -v : v);
+}
+
+__device__ __constant__ const unsigned int ph_two_over_pi[7] = {
+    0xA2F9836Eu, 0x4E441529u, 0xFC2757D1u, 0xF534DDC0u, 0xDB629599u, 0x3C439041u, 0xFE5163ABu};
+
+__device__ __noinline__ float ph_dtrig_slow(float x, int off) {
+    if (!(__builtin_fabsf(x) < __builtin_inff())) return __builtin_nanf("");
+    unsigned int b = __float_as_uint(x);
+    int e = (int)((b >> 23) & 0xffu) - 150;              /* x = M 2^e, e >= -3 here */
+    unsigned long long m = (b & 0x7fffffu) | 0x800000u;
+    int i0 = e >= 2 ? e - 1 : 1;                         /* first bit of 2/pi that matters mod 4 */
+    int j = (i0 - 1) >> 5, sh = (i0 - 1) & 31;
+    unsigned __int128 w = ((unsigned __int128)ph_two_over_pi[j] << 96) |
+                          ((unsigned __int128)ph_two_over_pi[j + 1] << 64) |
+                          ((unsigned __int128)ph_two_over_pi[j + 2] << 32) | ph_two_over_pi[j + 3];
+    w = (w << sh) >> 32;                                 /* bits i0 .. i0+95 of 2/pi */
+    int n = 97 - e + i0;                                 /* product bits below weight 4 */
+    unsigned __int128 p = (m * w) & ((((unsigned __int128)1) << n) - 1);
+    int q = (int)(p >> (n - 2)) & 3;
+    long long f = (long long)((unsigned long long)(p >> (n - 64)) & ((1ull << 62) - 1));
+    if (f >= (1ll << 61)) { f -= (1ll << 62); q += 1; }
+    double r = (double)f * 0x1.921fb54442d18p-62;        /* pi/2 2^-62 */
+    if (b >> 31) { r = -r; q = -q; }
+    return ph_dtrig_poly(r, q + off);
+}
+
+__device__ __forceinline__ float ph_dtrig(float x, int off) {
+    double xd = (double)x;
+    double k = __builtin_rint(xd * 0.6366197723675814);
+    double r = fma(-k, 0x1.921fb544p+0, xd);
+    r = fma(-k, 0x1.0b4611a626331p-34, r);
+    float v = ph_dtrig_poly(r, (int)k + off);
+    if (__builtin_expect(ph_wide_mask(x, 0x1p20f) != 0ull, 0))
+        v = !(__builtin_fabsf(x) < 0x1p20f) ? ph_dtrig_slow(x, off) : v;
+    return v;
+}
+
+__device__ __forceinline__ float ph_exp(float x) { return ph_dexpf(x); }
+__device__ __forceinline__ float ph_log(float x) { return ph_dlogf(x); }
+__device__ __forceinline__ float ph_sin(float x) { return ph_dtrig(x, 0); }
+__device__ __forceinline__ float ph_cos(float x) { return ph_dtrig(x, 1); }
+__device__ __forceinline__ float ph_exp2(float x) { return ph_dexp2f(x); }
+__device__ __forceinline__ float ph_log2(float x) { return ph_dlog2f(x); }
 #elif PH_MATH_MODE == 2
 /* FAST: x^y = 2^(y log2 x) on the hardware base-2 logarithm and
    exponential (v_log_f32, v_exp_f32) for a positive normal finite base and

@@ -106,7 +106,7 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
     unary_f = {
         "exp": "ph_exp({a})",
         "exp2": "ph_exp2({a})",
-        "log": "logf({a})",
+        "log": "ph_log({a})",
         "log2": "ph_log2({a})",
         "log1p": "log1pf({a})",
         "expm1": "ph_expm1({a})",

@@ -226,6 +226,11 @@ def _sign(x):
     return np.where((x == 0) | np.isnan(x), x, np.sign(x))
 
 
+# REPRODUCIBLE's exp, log, sin and cos (float32 on the device, also where
+# the operands are bfloat16 or float16)
+_DETERMINISTIC = {"exp": exact.dexpf, "log": exact.dlogf, "sin": exact.dsinf, "cos": exact.dcosf}
+
+
 def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int, reproducible: bool = False) -> Any:
     out_aval = eqn.outvars[0].aval
     bf_out = is_bf16(out_aval.dtype)
@@ -255,6 +260,12 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int, reproducible:
             r = exact.dlog2f(a)
         elif name == "exp2" and reproducible and f32_out:
             r = exact.dexp2f(a)
+        elif name in _DETERMINISTIC and reproducible and isf:
+            # computed in float32 on the device for every float type
+            r = _DETERMINISTIC[name](np.asarray(a, np.float32))
+        elif name == "logistic" and reproducible and isf:
+            one = np.float32(1.0)
+            r = one / (one + exact.dexpf(-np.asarray(a, np.float32)))
         elif name == "div":
             r = a / b if isf else _int_div(a, b, dt)
         elif name == "rem":

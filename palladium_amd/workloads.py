@@ -390,8 +390,7 @@ def gbm_call(cfg: GBMConfig = GBM_CFG, n_paths: int | None = None, **kw: Any):
         in_specs=[pl.BlockSpec((2,), lambda i: (0,))],
         out_specs=pl.BlockSpec((1,), lambda i: (i,)),
         out_shape=pl.ShapeDtypeStruct((n,), F32),
-        name="gbm_paths",
-        **kw,
+        **{"name": "gbm_paths", **kw},
     )
 
 

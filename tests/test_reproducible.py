@@ -340,3 +340,118 @@ def test_narrow_floats_keep_ieee_forms_under_reproducible():
         rep = pa.hip_call(k, math_mode="reproducible", **kw).interpret(*arrs)
         safe = pa.hip_call(k, math_mode="safe", **kw).interpret(*arrs)
         assert np.array_equal(np.asarray(rep).view(np.uint16), np.asarray(safe).view(np.uint16))
+
+
+def _same_bits(a, b):
+    return np.all((a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b)))
+
+
+def _ulps32(a, b):
+    return np.abs(a.view(np.int32).astype(np.int64) - b.view(np.int32).astype(np.int64))
+
+
+_SPECIAL = np.array([0.0, -0.0, 1.0, -1.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 1.1754942e-38,
+                     3.4028235e38, -3.4028235e38, 2.0 ** 19, -2.0 ** 19, 2.0 ** 20, -2.0 ** 20, 1048575.9,
+                     88.72283, 88.72284, -103.97208, 0.7853982, 1.5707964, 3.1415927, 1e30, -1e30], np.float32)
+
+
+def test_exp_log_sin_cos_restatements_agree():
+    """NumPy (palladium_amd.exact) and C (oracle.c) restatements of the
+    deterministic exp, log, sin and cos give the same bits on scattered bit
+    patterns over every exponent (the large-argument reduction included),
+    the working ranges and the special values."""
+    from palladium_amd import exact
+
+    r = np.random.default_rng(11)
+    x = np.concatenate([
+        r.integers(0, 2 ** 32, 60_000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+        r.uniform(-10, 10, 200_000).astype(np.float32),
+        r.uniform(-110, 90, 200_000).astype(np.float32),
+        _SPECIAL,
+    ])
+    for name in ("dexpf", "dlogf", "dsinf", "dcosf"):
+        assert _same_bits(getattr(exact, name)(x), getattr(oracle, name)(x)), name
+
+
+def test_exp_log_within_one_ulp_of_the_double_result():
+    from palladium_amd import exact
+
+    r = np.random.default_rng(12)
+    e = np.concatenate([r.uniform(-103, 88.7, 400_000), r.uniform(-1e-3, 1e-3, 100_000)]).astype(np.float32)
+    got = exact.dexpf(e)
+    ref = np.exp(e.astype(np.float64)).astype(np.float32)
+    d = _ulps32(got, ref)
+    assert d.max() <= 1 and np.mean(d == 0) > 0.999
+    x = np.concatenate([np.abs(r.standard_cauchy(300_000)), r.uniform(0.5, 2.0, 200_000),
+                        (10.0 ** r.uniform(-44, 38, 100_000))]).astype(np.float32)
+    x = x[(x > 0) & np.isfinite(x)]
+    got = exact.dlogf(x)
+    ref = np.log(x.astype(np.float64)).astype(np.float32)
+    d = _ulps32(got, ref)
+    assert d.max() <= 1 and np.mean(d == 0) > 0.999
+    with np.errstate(all="ignore"):
+        sp = _SPECIAL
+        np.testing.assert_array_equal(np.isnan(exact.dexpf(sp)), np.isnan(sp))
+        np.testing.assert_array_equal(exact.dexpf(np.float32([np.inf, -np.inf, 2.0 ** 19, -2.0 ** 19, 0.0])),
+                                      np.float32([np.inf, 0.0, np.inf, 0.0, 1.0]))
+        np.testing.assert_array_equal(exact.dlogf(np.float32([0.0, -0.0, np.inf, 1.0, 1e-45])),
+                                      np.log(np.float32([0.0, 0.0, np.inf, 1.0, 1e-45]).astype(np.float64)).astype(np.float32))
+        assert np.isnan(exact.dlogf(np.float32([-1.0, np.nan, -np.inf]))).all()
+
+
+def test_sin_cos_within_one_ulp_and_large_arguments_against_mpmath():
+    """Below 2^20 against the double sin/cos rounded to float; above it
+    (the exact reduction from the bits of 2/pi) against 100-digit mpmath,
+    so a wrong table word, window offset or quadrant fails."""
+    mp = pytest.importorskip("mpmath")
+    from palladium_amd import exact
+
+    r = np.random.default_rng(13)
+    x = np.concatenate([r.uniform(-10, 10, 300_000), r.uniform(-2.0 ** 20, 2.0 ** 20, 100_000),
+                        np.arange(-64, 65) * (np.pi / 4)]).astype(np.float32)
+    x = x[np.abs(x) < 2.0 ** 20]
+    for f, ref in ((exact.dsinf, np.sin), (exact.dcosf, np.cos)):
+        d = _ulps32(f(x), ref(x.astype(np.float64)).astype(np.float32))
+        assert d.max() <= 1 and np.mean(d == 0) > 0.999
+    # every binade from 2^20 to 2^127, both signs, plus the largest floats
+    big = np.concatenate([np.ldexp(r.uniform(1, 2, 4 * 108), np.repeat(np.arange(20, 128), 4)),
+                          [3.4028235e38, 2.0 ** 20, 2.0 ** 20 + 0.125, 1e30]])
+    big = np.concatenate([big, -big]).astype(np.float32)
+    big = big[np.isfinite(big)]
+    with mp.workdps(100):
+        want_s = np.array([float(mp.sin(mp.mpf(float(v)))) for v in big]).astype(np.float32)
+        want_c = np.array([float(mp.cos(mp.mpf(float(v)))) for v in big]).astype(np.float32)
+    assert _ulps32(exact.dsinf(big), want_s).max() <= 1
+    assert _ulps32(exact.dcosf(big), want_c).max() <= 1
+    assert np.isnan(exact.dsinf(np.float32([np.inf, -np.inf, np.nan]))).all()
+    assert np.isnan(exact.dcosf(np.float32([np.inf, -np.inf, np.nan]))).all()
+
+
+def test_reproducible_interpreter_equals_the_c_gbm_restatement():
+    """The GBM kernel's interpreter under REPRODUCIBLE (FAST's rewrites,
+    the contraction pass, the deterministic log/cos/exp) equals
+    oracle_gbm_r path by path."""
+    from palladium_amd.frontend import random
+    from palladium_amd.workloads import GBM_CFG, gbm_call
+
+    n = 384
+    got = np.asarray(gbm_call(GBM_CFG, n_paths=n, math_mode="reproducible").interpret(random.key(GBM_CFG.seed)))
+    want = oracle.gbm(GBM_CFG, n, mode="reproducible")
+    assert _same_bits(got, want)
+    assert np.abs(got - oracle.gbm(GBM_CFG, n)).max() < 1e-2
+
+
+def test_reproducible_transcendentals_in_the_emitted_kernel():
+    """Under REPRODUCIBLE the kernel calls ph_exp/ph_log/ph_cos, which the
+    prelude defines as the deterministic forms in that mode only."""
+    from palladium_amd.emit.prelude import PRELUDE
+    from palladium_amd.frontend import random
+    from palladium_amd.workloads import GBM_CFG, gbm_call
+
+    src = gbm_call(GBM_CFG, n_paths=64, math_mode="reproducible").bound(random.key(1)).hip_source
+    body = src[src.index('extern "C"'):]
+    for f in ("ph_log(", "ph_cos(", "ph_exp(", "sqrtf("):
+        assert f in body
+    mode3 = PRELUDE[PRELUDE.index("#if PH_MATH_MODE == 3"):]
+    for f in ("ph_dlogf(x)", "ph_dtrig(x, 1)", "ph_dexpf(x)"):
+        assert f in mode3
