@@ -7,8 +7,9 @@
  * contraction (built with -ffp-contract=off), the algorithm the reference
  * runs for that kernel, citing the reference file:line it follows. What
  * pins each function (known answers, float64 restatements, invariants) is
- * tested in tests/test_oracle.py, tests/test_oracle_sensitivity.py and
- * tests/test_golden.py.
+ * tested in tests/test_oracle.py, tests/test_oracle_sensitivity.py,
+ * tests/test_golden.py and (the REPRODUCIBLE-mode restatements)
+ * tests/test_reproducible.py.
  */
 #include <math.h>
 #include <omp.h>
