@@ -122,6 +122,18 @@ __device__ __forceinline__ float ph_fmin(float a, float b) { return fminf(a, b);
 __device__ __forceinline__ float ph_fmax(float a, float b) { return fmaxf(a, b); }
 
 #if PH_MATH_MODE == 0 || PH_MATH_MODE == 3
+/* The wavefront mask of lanes whose x is in one of the classes `mask`
+   selects (v_cmp_class bits: 0 sNaN, 1 qNaN, 2 -inf, 3 -normal, 4 -subnormal,
+   5 -0, 6 +0, 7 +subnormal, 8 +normal, 9 +inf), as a scalar: written straight
+   into a scalar register pair, so testing it costs one vector compare and
+   a scalar branch (through a bool and a ballot the compiler spends a
+   select and a second compare). Inactive lanes read 0. */
+__device__ __forceinline__ unsigned long long ph_class_mask(float x, unsigned int mask) {
+    unsigned long long m;
+    __asm__ volatile("v_cmp_class_f32_e64 %0, %1, %2" : "=s"(m) : "v"(x), "s"(mask));
+    return m;
+}
+
 /* a * b + c, correctly rounded (one v_fma_f64), with the constant c read
    from scalar registers. Written out because the compiler otherwise keeps
    polynomial coefficients in vector registers and copies each into the
@@ -135,11 +147,18 @@ __device__ __forceinline__ double ph_fma_k(double a, double b, double c) {
 /* log2 of a positive finite double: x = m 2^e with m in [sqrt(1/2), sqrt(2)),
    log2 m = (2 / ln 2) atanh(t), t = (m - 1) RN(1 / (m + 1)), as an odd series in t
    whose coefficients carry the 2 / ln 2; log2 x = e + t P(t^2), one FMA. */
+__device__ __forceinline__ double ph_log2_core(double m, int e);
+
 __device__ __forceinline__ double ph_log2_pos(double x) {
     int e;
     double m = frexp(x, &e);          /* x = m 2^e, m in [0.5, 1) */
     if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
-    /* t = (m - 1) RN(1 / (m + 1)), the reciprocal without a division. x is a
+    return ph_log2_core(m, e);
+}
+
+/* log2(m 2^e) for m in [sqrt(1/2), sqrt(2)) with at most 24 significant bits. */
+__device__ __forceinline__ double ph_log2_core(double m, int e) {
+    /* t = (m - 1) RN(1 / (m + 1)), the reciprocal without a division. m is a
        float, so d = m + 1 in [1.707, 2.414) has at most 25 significant bits.
        From the hardware float reciprocal (relative error below 2^-22) two
        Newton steps r + r (1 - d r), each two correctly rounded FMAs, leave
@@ -193,17 +212,31 @@ __device__ __forceinline__ double ph_exp2_dbl(double z) {
    override). ph_pow(x, y) == ph_pow_with_log(x, y, ph_pow_log(x)) bit for
    bit, so a loop can compute the log of a base once and use it in several
    powers, or carry it with the base. */
-__device__ __forceinline__ double ph_pow_log(float x) {
+__device__ __noinline__ double ph_pow_log_slow(float x) {
     float ax = fabsf(x);
     bool finite_base = ax > 0.0f && ax < __builtin_inff();
     return ph_log2_pos((double)(finite_base ? ax : 1.0f));
 }
 
-/* Branch-free: the main path runs on a harmless base for special operands
-   and the C99 special cases are selected over it, highest priority last,
-   so the loop around it carries no exec-mask branches. Same results as
-   oracle/oracle.c:oracle_pow, which tests them in order. */
-__device__ __forceinline__ float ph_pow_with_log(float x, float y, double lg) {
+/* For a normal base the split comes from the float's bits: |x| = m 2^e with
+   m in [0x1.6a09e8p-1, 2 * 0x1.6a09e6p-1], the float range frexp's
+   m < sqrt(1/2) doubling gives, so m and e, and the log, are the same bits.
+   A wavefront holding a zero, subnormal, infinite or NaN base takes the
+   frexp form for those lanes in a branch. */
+__device__ __forceinline__ double ph_pow_log(float x) {
+    unsigned int ix = (__float_as_uint(x) & 0x7fffffffu) - 0x3f3504f4u;
+    int e = (int)ix >> 23;
+    float m = __uint_as_float((ix & 0x007fffffu) + 0x3f3504f4u);
+    double lg = ph_log2_core((double)m, e);
+    if (__builtin_expect(ph_class_mask(x, 0x2f7) != 0ull, 0))   /* a lane not -normal, not +normal */
+        lg = __builtin_amdgcn_classf(x, 0x2f7) ? ph_pow_log_slow(x) : lg;
+    return lg;
+}
+
+/* Every operand: the main path on a harmless base for special operands
+   and the C99 special cases selected over it, highest priority last. Same
+   results as oracle/oracle.c:oracle_pow, which tests them in order. */
+__device__ __noinline__ float ph_pow_full(float x, float y, double lg) {
     const float inf = __builtin_inff();
     float ax = fabsf(x);
     float ay = fabsf(y);
@@ -226,6 +259,31 @@ __device__ __forceinline__ float ph_pow_with_log(float x, float y, double lg) {
     return r;
 }
 
+/* The wavefront mask of lanes whose double z lies outside [lo, hi] (or is
+   NaN), as a scalar, like ph_class_mask. */
+__device__ __forceinline__ unsigned long long ph_outside_mask(double z, double lo, double hi) {
+    unsigned long long a, b;
+    __asm__ volatile("v_cmp_nge_f64_e64 %0, %1, %2" : "=s"(a) : "v"(z), "s"(lo));
+    __asm__ volatile("v_cmp_nle_f64_e64 %0, %1, %2" : "=s"(b) : "v"(z), "s"(hi));
+    return a | b;
+}
+
+/* x^y given lg = ph_pow_log(x). For a positive finite base and
+   -151 <= z = y lg <= 129 every special case of ph_pow_full leaves its
+   main path's value, 2^z rounded once to float (x = 1 gives z = 0 and 1;
+   y = 0 gives z = 0 and 1; a NaN or infinite y makes z NaN or infinite),
+   so that value is computed directly, and a wavefront holding any other
+   lane (a zero, negative, infinite or NaN base, or z out of that range)
+   takes ph_pow_full for those lanes in a branch. Bit for bit ph_pow_full. */
+__device__ __forceinline__ float ph_pow_with_log(float x, float y, double lg) {
+    double z = (double)y * lg;
+    float r = (float)ph_exp2_dbl(z);
+    unsigned long long any = ph_class_mask(x, 0x27f) | ph_outside_mask(z, -151.0, 129.0);
+    if (__builtin_expect(any != 0ull, 0))
+        r = (!(x > 0.0f && x < __builtin_inff()) || !(z >= -151.0 && z <= 129.0)) ? ph_pow_full(x, y, lg) : r;
+    return r;
+}
+
 __device__ __forceinline__ float ph_pow(float x, float y) { return ph_pow_with_log(x, y, ph_pow_log(x)); }
 #endif
 #if PH_MATH_MODE == 3
@@ -239,18 +297,6 @@ __device__ __forceinline__ float ph_pow(float x, float y) { return ph_pow_with_l
    scalar branch on the common path). Checked against the IEEE quotient on
    every float on the device. */
 __device__ __noinline__ float ph_rrcp_slow(float b) { return 1.0f / b; }
-
-/* The wavefront mask of lanes whose x is in one of the classes `mask`
-   selects (v_cmp_class bits: 0 sNaN, 1 qNaN, 2 -inf, 3 -normal, 4 -subnormal,
-   5 -0, 6 +0, 7 +subnormal, 8 +normal, 9 +inf), as a scalar: written straight
-   into a scalar register pair, so testing it costs one vector compare and
-   a scalar branch (through a bool and a ballot the compiler spends a
-   select and a second compare). Inactive lanes read 0. */
-__device__ __forceinline__ unsigned long long ph_class_mask(float x, unsigned int mask) {
-    unsigned long long m;
-    __asm__ volatile("v_cmp_class_f32_e64 %0, %1, %2" : "=s"(m) : "v"(x), "s"(mask));
-    return m;
-}
 
 __device__ __forceinline__ float ph_rrcp(float b) {
     float y = __builtin_amdgcn_rcpf(b);
