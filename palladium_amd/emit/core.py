@@ -548,6 +548,12 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         if keeps_compaction(folded):
             body = folded
 
+    from palladium_amd.emit.optimize import drop_dead_code
+
+    pruned = drop_dead_code(body)
+    if keeps_compaction(pruned):
+        body = pruned
+
     cplan = plan_for(spec, body, lanes, block)
     if (cplan is not None) != compacting:
         raise EmitError("internal: while-loop compaction disagrees with the launch geometry")

@@ -46,7 +46,7 @@ import numpy as np
 
 from palladium_amd.ir import ClosedJaxpr, Jaxpr, JaxprEqn, Literal, ShapedArray, Var, primitive
 
-__all__ = ["carry_logs", "contract_products", "drop_redundant_clamps", "factor_common_products", "fast_rewrites", "funnel_shifts",
+__all__ = ["carry_logs", "contract_products", "drop_dead_code", "drop_redundant_clamps", "factor_common_products", "fast_rewrites", "funnel_shifts",
            "power_laws_to_exp2", "reuse_affine_shifts", "share_pow_logs", "fold_counters"]
 
 
@@ -939,3 +939,35 @@ def contract_products(jaxpr: Jaxpr) -> Jaxpr:
         new_eqns.append(e)
     new_eqns = [e for e in new_eqns if not (len(e.outvars) == 1 and e.outvars[0] in fused)]
     return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, new_eqns)
+
+
+# Primitives with no effect beyond their results (stores, lane collectives,
+# loops, calls and user-registered rules are not listed, so they stay).
+_PURE = frozenset((
+    "add sub mul div rem min max pow neg abs sign exp exp2 log log2 log1p expm1 sin cos tan tanh sqrt "
+    "rsqrt floor ceil round logistic atan2 lt le gt ge eq ne and or xor not shift_right_logical "
+    "shift_right_arithmetic shift_left clamp select_n integer_pow convert_element_type "
+    "bitcast_convert_type fma pow_log pow_with_log get broadcast_in_dim reshape squeeze expand_dims "
+    "transpose program_id num_programs random_wrap random_unwrap random_fold_in random_bits "
+    "threefry2x32 iota lane_index"
+).split())
+
+
+def drop_dead_code(jaxpr: Jaxpr) -> Jaxpr:
+    """Every mode: remove the equations of side-effect-free primitives whose
+    results nothing reads (at their own level: a loop body's results are
+    its carries), in nested jaxprs too. Rewrites leave such equations
+    behind (a reciprocal the carried log replaced, say), and the emitted
+    C++ cannot always lose them itself: a helper holding a volatile asm
+    (the wavefront-uniform slow-path tests) is never removed by the
+    compiler. Removing an unread pure value changes no result."""
+    eqns = [JaxprEqn(e.invars, e.outvars, e.primitive,
+                     {k: _rewrite_sub(v, drop_dead_code) for k, v in e.params.items()}) for e in jaxpr.eqns]
+    live = {v for v in jaxpr.outvars if isinstance(v, Var)}
+    kept: list[JaxprEqn] = []
+    for e in reversed(eqns):
+        if e.primitive.name in _PURE and e.outvars and not any(o in live for o in e.outvars):
+            continue
+        kept.append(e)
+        live.update(a for a in e.invars if isinstance(a, Var))
+    return Jaxpr(jaxpr.constvars, jaxpr.invars, jaxpr.outvars, kept[::-1])
