@@ -500,3 +500,39 @@ def test_affine_shift_needs_the_same_coefficient_and_offset():
                           out_shape=(pl.ShapeDtypeStruct((64,), np.float32),) * 2)
     spec = trace(call, v, v, v, v)
     assert reuse_affine_shifts(spec.jaxpr).eqns == spec.jaxpr.eqns
+
+
+from palladium_amd.emit.optimize import drop_dead_code  # noqa: E402
+
+
+def test_dead_code_is_dropped_stores_and_loop_carries_kept():
+    """An unread pure value goes, at the top level and inside a loop body;
+    stores, loops and every value a result reads stay, and the results are
+    unchanged."""
+
+    def kernel(x_ref, o_ref, p_ref):
+        x = x_ref[...]
+        unused = jnp.exp(x) * 3.0  # noqa: F841 - read by nothing
+
+        def body(i, c):
+            dead = c / (c + 1.0)  # noqa: F841 - read by nothing
+            return c * 0.5 + x
+
+        o_ref[...] = lax.fori_loop(0, 8, body, x)
+        p_ref[...] = x + 1.0
+
+    x = np.linspace(0.5, 2.0, 64, dtype=np.float32)
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    call = pl.pallas_call(kernel, grid=(64,), in_specs=[s], out_specs=[s, s],
+                          out_shape=(pl.ShapeDtypeStruct((64,), np.float32),) * 2)
+    spec = trace(call, x)
+    pruned = dataclasses.replace(spec, jaxpr=drop_dead_code(spec.jaxpr))
+    assert _count(spec.jaxpr, "exp") == 1 and _count(pruned.jaxpr, "exp") == 0
+    assert _count(spec.jaxpr, "div") == 1 and _count(pruned.jaxpr, "div") == 0
+    assert _count(pruned.jaxpr, "swap") == _count(spec.jaxpr, "swap") == 2
+    assert _count(pruned.jaxpr, "scan") + _count(pruned.jaxpr, "while") == 1
+    for g, w in zip(interpret_spec(pruned, x), interpret_spec(spec, x)):
+        np.testing.assert_array_equal(g, w)
+    src = emit_hip(spec, math_mode="safe")
+    body = src[src.index('extern "C"'):]
+    assert "expf" not in body and "ph_exp(" not in body
