@@ -354,7 +354,8 @@ def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int, reproducible:
             raise UnsupportedPrimitiveError(f"interpreter has no rule for primitive '{name}'")
     r = np.asarray(r)
     if r.dtype != dt:
-        r = r.astype(dt)
+        with np.errstate(over="ignore", invalid="ignore"):  # narrowing saturates to inf, as on the device
+            r = r.astype(dt)
     if bf_out:
         r = round_f32(r)
     full = (n,) + tuple(out_aval.shape)

@@ -213,3 +213,40 @@ def test_gbm_config3_reproducible_bit_exact():
                       "gbm tail")
     ieee = oracle.gbm(cfg, head)
     np.testing.assert_allclose(got[:head], ieee, atol=2e-2, rtol=1e-3)
+
+
+@pytest.mark.parametrize("narrow", ["bfloat16", "float16"])
+def test_narrow_float_transcendentals_bit_exact_with_the_interpreter(narrow):
+    """bfloat16 and float16 exp, log, sin and cos under REPRODUCIBLE: the
+    device computes them in float32 with the deterministic forms and rounds,
+    and the interpreter does the same, so every bit pattern of the format
+    (NaNs aside, compared as NaN) gives the same result on both."""
+    from palladium_amd import dtypes
+    from palladium_amd.frontend import jnp
+
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    if narrow == "bfloat16":
+        dt = dtypes.bfloat16
+        x = dtypes.from_float((bits.astype(np.uint32) << 16).view(np.float32))
+    else:
+        dt = np.dtype(np.float16)
+        x = bits.view(np.float16)
+    n = 1 << 16
+    print(f"[reproducible] {narrow} exp/log/sin/cos over all {n} patterns", flush=True)
+    s = pl.BlockSpec((1,), lambda i: (i,))
+
+    def k(x_ref, e_ref, l_ref, s_ref, c_ref):
+        v = x_ref[...]
+        e_ref[...] = jnp.exp(v)
+        l_ref[...] = jnp.log(v)
+        s_ref[...] = jnp.sin(v)
+        c_ref[...] = jnp.cos(v)
+
+    call = pa.hip_call(k, grid=(n,), in_specs=[s], out_specs=[s] * 4,
+                       out_shape=tuple(pl.ShapeDtypeStruct((n,), dt) for _ in range(4)), math_mode="reproducible")
+    got = call(x)
+    want = call.interpret(x)
+    for g, w, name in zip(got, want, ("exp", "log", "sin", "cos")):
+        gf = dtypes.to_float(g) if dtypes.is_bf16(g.dtype) else np.asarray(g, np.float32)
+        wf = dtypes.to_float(w) if dtypes.is_bf16(w.dtype) else np.asarray(w, np.float32)
+        _assert_same_bits(gf.astype(np.float32), wf.astype(np.float32), f"{narrow} {name}")
