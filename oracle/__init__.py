@@ -119,7 +119,7 @@ def _declare_more(L):
     L.oracle_rdiv.restype = f
     L.oracle_dlog2f_many.argtypes = [l, _F, _F]
     L.oracle_dexp2f_many.argtypes = [l, _F, _F]
-    for fn in ("dexpf", "dlogf", "dsinf", "dcosf"):
+    for fn in ("dexpf", "dlogf", "dsinf", "dcosf", "dtanhf"):
         getattr(L, f"oracle_{fn}_many").argtypes = [l, _F, _F]
     L.oracle_gbm_r.argtypes = [l, l, l, u, u, f, f, f, f, f, _F]
     L.oracle_lv_rk4_r.argtypes = [l, _F, _F, _F, _F, _F, _F, ctypes.c_double, l, _F, _F, _F]
@@ -246,6 +246,10 @@ def dsinf(x) -> np.ndarray:
 
 def dcosf(x) -> np.ndarray:
     return _many("dcosf", x)
+
+
+def dtanhf(x) -> np.ndarray:
+    return _many("dtanhf", x)
 
 
 def rdiv(a: float, b: float) -> np.float32:

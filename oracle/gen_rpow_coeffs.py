@@ -8,8 +8,9 @@ generator uses).
     2^r    = Q(r),                              r in [-1/2, 1/2]
 
     sin r  = r S(r^2), cos r = C(r^2),          |r| <= pi/4 (+1e-6)
+    tanh a = a T(a^2),                          0 <= a < 1/2
 
-P has degree 4, R degree 2, Q degree 7 and S and C degree 5, each the Chebyshev interpolant
+P has degree 4, R degree 2, Q degree 7, S and C degree 5 and T degree 7, each the Chebyshev interpolant
 of its function on its interval (near-minimax), with coefficients rounded
 to double. R's relative error is 2^-9.6, so the two Newton steps leave
 2^-38. TWO_OVER_PI holds the first 224 fraction bits of 2/pi in 32-bit
@@ -54,6 +55,27 @@ def trig_coefficients():
     sc = mp.chebyfit(_s_target, [0, R_TRIG ** 2], 6)
     cc = mp.chebyfit(_c_target, [0, R_TRIG ** 2], 6)
     return [float(c) for c in reversed(sc)], [float(c) for c in reversed(cc)]
+
+
+TANH_SPLIT = mp.mpf("0.5")
+
+
+def _t_target(s):
+    if s == 0:
+        return mp.mpf(1)
+    a = mp.sqrt(s)
+    return mp.tanh(a) / a
+
+
+def tanh_coefficients():
+    tc = mp.chebyfit(_t_target, [0, TANH_SPLIT ** 2], 8)
+    return [float(c) for c in reversed(tc)]
+
+
+def tanh_error(samples: int = 4001) -> float:
+    T = tanh_coefficients()
+    aa = [TANH_SPLIT * mp.mpf(k) / (samples - 1) for k in range(1, samples)]
+    return float(max(abs(_poly(T, a * a) * a / mp.tanh(a) - 1) for a in aa))
 
 
 def two_over_pi_words(n: int = 7):
@@ -126,6 +148,9 @@ if __name__ == "__main__":
     print("C (r^2, low to high):", ", ".join(repr(c) for c in C))
     es, ec = trig_errors()
     print(f"max |r S(r^2)/sin r - 1| = 2^{float(mp.log(es, 2)):.1f}; max |C(r^2)/cos r - 1| = 2^{float(mp.log(ec, 2)):.1f}")
+    T = tanh_coefficients()
+    print("T (a^2, low to high):", ", ".join(repr(c) for c in T))
+    print(f"max |a T(a^2)/tanh a - 1| = 2^{float(mp.log(tanh_error(), 2)):.1f}")
     print("TWO_OVER_PI:", ", ".join(f"0x{w:08X}" for w in two_over_pi_words()))
     hi, lo = pio2_split()
     print(f"PIO2_HI = {hi.hex()} ({hi!r}); PIO2_LO = {lo.hex()} ({lo!r})")

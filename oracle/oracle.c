@@ -501,6 +501,31 @@ static float dtrig(float x, int off) {
 float oracle_dsinf(float x) { return dtrig(x, 0); }
 float oracle_dcosf(float x) { return dtrig(x, 1); }
 
+/* The REPRODUCIBLE mode's float tanh (device: ph_dtanhf): a = |x|; a T(a^2)
+   below 1/2 (T of degree 7), else 1 - 2 / (e + 1) with e = 2^(2 log2(e)
+   min(a, 10)) on the 2^z core and a double division; rounded once to float,
+   the sign of x, NaN passed through. */
+float oracle_dtanhf(float x) {
+  if (x != x) return x;
+  double a = fabs((double)x);
+  double s = a * a;
+  double p = fma(s, -0.0009849941049264166, 0.003415370282047567);
+  p = fma(p, s, -0.008827257095239422);
+  p = fma(p, s, 0.021865363235290286);
+  p = fma(p, s, -0.053967994875471936);
+  p = fma(p, s, 0.13333332529982497);
+  p = fma(p, s, -0.33333333323808056);
+  p = fma(p, s, 0.9999999999998141);
+  double e = oracle_rexp2(fmin(a, 10.0) * 2.8853900817779268);
+  double t = a < 0.5 ? a * p : 1.0 - 2.0 / (e + 1.0);
+  return copysignf((float)t, x);
+}
+
+void oracle_dtanhf_many(long n, const float *x, float *out) {
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) out[i] = oracle_dtanhf(x[i]);
+}
+
 void oracle_dexpf_many(long n, const float *x, float *out) {
 #pragma omp parallel for schedule(static)
   for (long i = 0; i < n; ++i) out[i] = oracle_dexpf(x[i]);

@@ -32,8 +32,9 @@
 - `ph_sin`/`ph_cos`: under FAST the hardware sine/cosine (the reference's
   FAST contract allows approximate transcendentals); libm-accurate under
   SAFE and RELAXED. Under REPRODUCIBLE, `ph_exp`, `ph_log`, `ph_sin`,
-  `ph_cos`, `ph_exp2` and `ph_log2` are deterministic double-core forms
-  (`ph_dexpf`, `ph_dlogf`, `ph_dtrig`, `ph_dexp2f`, `ph_dlog2f`) that
+  `ph_cos`, `ph_tanh`, `ph_exp2` and `ph_log2` are deterministic double-core
+  forms (`ph_dexpf`, `ph_dlogf`, `ph_dtrig`, `ph_dtanhf`, `ph_dexp2f`,
+  `ph_dlog2f`) that
   `palladium_amd.exact` and `oracle/oracle.c` restate bit for bit.
 - `ph_fmin`/`ph_fmax`: NaN-suppressing min/max (C fminf/fmaxf), the
   reference's lowering of `min`/`max` (`src/palladium/emit/core.py:574-575`).
@@ -88,6 +89,7 @@ __device__ __forceinline__ float ph_exp(float x) { return __builtin_amdgcn_exp2f
 __device__ __forceinline__ float ph_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float ph_log2(float x) { return __builtin_amdgcn_logf(x); }
 __device__ __forceinline__ float ph_log(float x) { return logf(x); }
+__device__ __forceinline__ float ph_tanh(float x) { return tanhf(x); }
 #elif PH_MATH_MODE != 3
 __device__ __forceinline__ float ph_exp2(float x) { return exp2f(x); }
 __device__ __forceinline__ float ph_log2(float x) { return log2f(x); }
@@ -95,6 +97,7 @@ __device__ __forceinline__ float ph_sin(float x) { return sinf(x); }
 __device__ __forceinline__ float ph_cos(float x) { return cosf(x); }
 __device__ __forceinline__ float ph_exp(float x) { return expf(x); }
 __device__ __forceinline__ float ph_log(float x) { return logf(x); }
+__device__ __forceinline__ float ph_tanh(float x) { return tanhf(x); }
 #endif
 
 /* Integer division and float->integer conversion with every input defined,
@@ -509,6 +512,29 @@ __device__ __forceinline__ float ph_sin(float x) { return ph_dtrig(x, 0); }
 __device__ __forceinline__ float ph_cos(float x) { return ph_dtrig(x, 1); }
 __device__ __forceinline__ float ph_exp2(float x) { return ph_dexp2f(x); }
 __device__ __forceinline__ float ph_log2(float x) { return ph_dlog2f(x); }
+
+/* Deterministic float tanh: a = |x|; below 1/2, a T(a^2) with T of degree 7
+   (relative error 2^-42.3); from 1/2 on, 1 - 2 / (e + 1) with e = e^(2a) on
+   the 2^z core (a clamped at 10, where the float result is 1 already) and
+   an IEEE double division; rounded once to float, the sign copied from x,
+   NaN passed through. */
+__device__ __forceinline__ float ph_dtanhf(float x) {
+    double a = __builtin_fabs((double)x);
+    double s = a * a;
+    double p = ph_fma_k(s, -0.0009849941049264166, 0.003415370282047567);
+    p = ph_fma_k(p, s, -0.008827257095239422);
+    p = ph_fma_k(p, s, 0.021865363235290286);
+    p = ph_fma_k(p, s, -0.053967994875471936);
+    p = ph_fma_k(p, s, 0.13333332529982497);
+    p = ph_fma_k(p, s, -0.33333333323808056);
+    p = ph_fma_k(p, s, 0.9999999999998141);
+    double e = ph_rexp2(__builtin_fmin(a, 10.0) * 2.8853900817779268);
+    double t = a < 0.5 ? a * p : 1.0 - 2.0 / (e + 1.0);
+    float r = __builtin_copysignf((float)t, x);
+    return x != x ? x : r;
+}
+
+__device__ __forceinline__ float ph_tanh(float x) { return ph_dtanhf(x); }
 #elif PH_MATH_MODE == 2
 /* FAST: x^y = 2^(y log2 x) on the hardware base-2 logarithm and
    exponential (v_log_f32, v_exp_f32) for a positive normal finite base and

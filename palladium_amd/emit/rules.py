@@ -113,7 +113,7 @@ def _tmpl(opname: str, ops: list[CVal], out_ctype: str) -> str:
         "sin": "ph_sin({a})",
         "cos": "ph_cos({a})",
         "tan": "tanf({a})",
-        "tanh": "tanhf({a})",
+        "tanh": "ph_tanh({a})",
         "sqrt": "sqrtf({a})",
         "rsqrt": "(1.0f / sqrtf({a}))",
         "floor": "floorf({a})",

@@ -226,9 +226,10 @@ def _sign(x):
     return np.where((x == 0) | np.isnan(x), x, np.sign(x))
 
 
-# REPRODUCIBLE's exp, log, sin and cos (float32 on the device, also where
+# REPRODUCIBLE's exp, log, sin, cos and tanh (float32 on the device, also where
 # the operands are bfloat16 or float16)
-_DETERMINISTIC = {"exp": exact.dexpf, "log": exact.dlogf, "sin": exact.dsinf, "cos": exact.dcosf}
+_DETERMINISTIC = {"exp": exact.dexpf, "log": exact.dlogf, "sin": exact.dsinf, "cos": exact.dcosf,
+                  "tanh": exact.dtanhf}
 
 
 def _elementwise(name: str, ops: list[Any], eqn: JaxprEqn, n: int, reproducible: bool = False) -> Any:

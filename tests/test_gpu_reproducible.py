@@ -164,9 +164,9 @@ def _transcendental_operands(seed):
     ])
 
 
-def test_exp_log_sin_cos_sqrt_match_the_oracle():
-    """The REPRODUCIBLE exp, log, sin and cos (ph_dexpf, ph_dlogf,
-    ph_dtrig) equal oracle_dexpf/dlogf/dsinf/dcosf bit for bit on 16.8M
+def test_exp_log_sin_cos_tanh_sqrt_match_the_oracle():
+    """The REPRODUCIBLE exp, log, sin, cos and tanh (ph_dexpf, ph_dlogf,
+    ph_dtrig, ph_dtanhf) equal oracle_dexpf/dlogf/dsinf/dcosf/dtanhf bit for bit on 16.8M
     operands (scattered bit patterns over every exponent, the working
     ranges of exp and of Box-Muller's angle, the large-argument reduction
     and the special values), and sqrtf under this mode's compile options is
@@ -177,22 +177,23 @@ def test_exp_log_sin_cos_sqrt_match_the_oracle():
     n = xs.size
     print(f"[reproducible] exp/log/sin/cos/sqrt over {n} operands", flush=True)
     s = pl.BlockSpec((1,), lambda i: (i,))
-    outs = tuple(pl.ShapeDtypeStruct((n,), np.float32) for _ in range(5))
+    outs = tuple(pl.ShapeDtypeStruct((n,), np.float32) for _ in range(6))
 
-    def k(x_ref, e_ref, l_ref, s_ref, c_ref, q_ref):
+    def k(x_ref, e_ref, l_ref, s_ref, c_ref, t_ref, q_ref):
         x = x_ref[...]
         e_ref[...] = jnp.exp(x)
         l_ref[...] = jnp.log(x)
         s_ref[...] = jnp.sin(x)
         c_ref[...] = jnp.cos(x)
+        t_ref[...] = jnp.tanh(x)
         q_ref[...] = jnp.sqrt(x)
 
-    got = pa.hip_call(k, grid=(n,), in_specs=[s], out_specs=[s] * 5, out_shape=outs,
+    got = pa.hip_call(k, grid=(n,), in_specs=[s], out_specs=[s] * 6, out_shape=outs,
                       math_mode="reproducible")(xs)
-    for g, name in zip(got[:4], ("dexpf", "dlogf", "dsinf", "dcosf")):
+    for g, name in zip(got[:5], ("dexpf", "dlogf", "dsinf", "dcosf", "dtanhf")):
         _assert_same_bits(g, getattr(oracle, name)(xs), name)
     with np.errstate(all="ignore"):
-        _assert_same_bits(got[4], np.sqrt(xs), "sqrtf")
+        _assert_same_bits(got[5], np.sqrt(xs), "sqrtf")
 
 
 def test_gbm_config3_reproducible_bit_exact():
@@ -217,7 +218,7 @@ def test_gbm_config3_reproducible_bit_exact():
 
 @pytest.mark.parametrize("narrow", ["bfloat16", "float16"])
 def test_narrow_float_transcendentals_bit_exact_with_the_interpreter(narrow):
-    """bfloat16 and float16 exp, log, sin and cos under REPRODUCIBLE: the
+    """bfloat16 and float16 exp, log, sin, cos and tanh under REPRODUCIBLE: the
     device computes them in float32 with the deterministic forms and rounds,
     and the interpreter does the same, so every bit pattern of the format
     (NaNs aside, compared as NaN) gives the same result on both."""
@@ -235,18 +236,19 @@ def test_narrow_float_transcendentals_bit_exact_with_the_interpreter(narrow):
     print(f"[reproducible] {narrow} exp/log/sin/cos over all {n} patterns", flush=True)
     s = pl.BlockSpec((1,), lambda i: (i,))
 
-    def k(x_ref, e_ref, l_ref, s_ref, c_ref):
+    def k(x_ref, e_ref, l_ref, s_ref, c_ref, t_ref):
         v = x_ref[...]
         e_ref[...] = jnp.exp(v)
         l_ref[...] = jnp.log(v)
         s_ref[...] = jnp.sin(v)
         c_ref[...] = jnp.cos(v)
+        t_ref[...] = jnp.tanh(v)
 
-    call = pa.hip_call(k, grid=(n,), in_specs=[s], out_specs=[s] * 4,
-                       out_shape=tuple(pl.ShapeDtypeStruct((n,), dt) for _ in range(4)), math_mode="reproducible")
+    call = pa.hip_call(k, grid=(n,), in_specs=[s], out_specs=[s] * 5,
+                       out_shape=tuple(pl.ShapeDtypeStruct((n,), dt) for _ in range(5)), math_mode="reproducible")
     got = call(x)
     want = call.interpret(x)
-    for g, w, name in zip(got, want, ("exp", "log", "sin", "cos")):
+    for g, w, name in zip(got, want, ("exp", "log", "sin", "cos", "tanh")):
         gf = dtypes.to_float(g) if dtypes.is_bf16(g.dtype) else np.asarray(g, np.float32)
         wf = dtypes.to_float(w) if dtypes.is_bf16(w.dtype) else np.asarray(w, np.float32)
         _assert_same_bits(gf.astype(np.float32), wf.astype(np.float32), f"{narrow} {name}")
