@@ -1,5 +1,6 @@
 """Differential test of the emitter: seeded random kernels run on the GPU
-under SAFE math against the NumPy interpreter (`.interpret`). Only IEEE
+under SAFE math against the NumPy interpreter (`.interpret`) (and, with
+powers and transcendentals added, under REPRODUCIBLE). Under SAFE only IEEE
 operations are generated (+ - * / fmin fmax abs neg select), so results
 must agree bit for bit. Programs mix expression trees, fori_loops with
 permuted carries, switch and bounded while loops (after the reference's
@@ -21,12 +22,22 @@ pytestmark = pytest.mark.gpu
 F = np.float32
 
 
-def _expr(rng, leaves, depth, powers=False):
+def _expr(rng, leaves, depth, powers=False, transc=False):
     if depth == 0 or rng.random() < 0.25:
         return leaves[rng.integers(len(leaves))] if rng.random() < 0.85 else float(np.float32(rng.uniform(-2, 2)))
-    op = rng.integers(11 if powers else 9)
-    a = _expr(rng, leaves, depth - 1, powers)
-    b = _expr(rng, leaves, depth - 1, powers)
+    op = rng.integers(16 if transc else (11 if powers else 9))
+    a = _expr(rng, leaves, depth - 1, powers, transc)
+    b = _expr(rng, leaves, depth - 1, powers, transc)
+    if op == 11:
+        return jnp.exp(jnp.clip(a, -20.0, 20.0)) * 0.25
+    if op == 12:
+        return jnp.log(jnp.abs(a) + 0.25)
+    if op == 13:
+        return jnp.sin(a * b)
+    if op == 14:
+        return jnp.cos(a) * b
+    if op == 15:
+        return jnp.tanh(a - b)
     if op == 9:
         return (jnp.abs(a) + 0.5) ** jnp.clip(b, -3.0, 3.0)
     if op == 10:
@@ -55,17 +66,17 @@ def _tame(v, dt=F):
     return jnp.broadcast_to(v if v.dtype == dt else v.astype(dt), (1,))
 
 
-def _make_kernel(seed, powers=False):
+def _make_kernel(seed, powers=False, transc=False):
     def kernel(x_ref, y_ref, o_ref, p_ref):
         rng = np.random.default_rng(seed)
         x, y = x_ref[...], y_ref[...]
         dt = x.dtype
-        v = _tame(_expr(rng, [x, y], 4, powers), dt)
+        v = _tame(_expr(rng, [x, y], 4, powers, transc), dt)
 
         def body(i, c):
             a, b, c3 = c
             r = np.random.default_rng(seed + 1)
-            na = _tame(_expr(r, [a, b, c3], 3, powers), dt)
+            na = _tame(_expr(r, [a, b, c3], 3, powers, transc), dt)
             return (b, c3, na) if seed % 2 else (na, a, b)  # permuted carries
 
         a, b, c = lax.fori_loop(0, 5 + seed % 7, body, (v, x, y))
@@ -115,18 +126,19 @@ def test_random_program_narrow_float_bit_exact_vs_interpreter(seed, dt):
 
 @pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
 def test_random_program_reproducible_bit_exact_vs_interpreter(seed):
-    """The same grammar plus powers and sums of products, under REPRODUCIBLE
-    math: the emitter fuses single-use products into fused multiply-adds,
-    divides by the correctly rounded reciprocal and takes the fast
-    deterministic pow; the interpreter does the same in NumPy
-    (`palladium_amd.exact`), so every result agrees bit for bit."""
+    """The same grammar plus powers, sums of products, exp, log, sin, cos
+    and tanh, under REPRODUCIBLE math: the emitter fuses single-use products
+    into fused multiply-adds, divides by the correctly rounded reciprocal
+    and takes the deterministic pow and transcendentals; the interpreter
+    does the same in NumPy (`palladium_amd.exact`), so every result agrees
+    bit for bit."""
     n = 300
     rng = np.random.default_rng(300 + seed)
     x = rng.uniform(-3, 3, n).astype(F)
     y = rng.uniform(-3, 3, n).astype(F)
     spec = pl.BlockSpec((1,), lambda i: (i,))
-    call = pa.hip_call(_make_kernel(seed, powers=True), grid=(n,), in_specs=[spec, spec], out_specs=(spec, spec),
-                       out_shape=(pl.ShapeDtypeStruct((n,), F),) * 2, math_mode="reproducible")
+    call = pa.hip_call(_make_kernel(seed, powers=True, transc=True), grid=(n,), in_specs=[spec, spec],
+                       out_specs=(spec, spec), out_shape=(pl.ShapeDtypeStruct((n,), F),) * 2, math_mode="reproducible")
     src = call.bound(x, y).hip_source
     assert "__builtin_fmaf" in src[src.index('extern "C"'):]
     got = call(x, y)
