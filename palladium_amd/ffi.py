@@ -16,6 +16,7 @@ buffers (`src/palladium/ffi.py:82-87,118-125`).
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 from collections.abc import Callable
@@ -26,7 +27,7 @@ from palladium_amd.dtypes import name as _dtype_name
 
 from palladium_amd.diagnostics import KernelDiagnostics, explain_spec, log_compile
 from palladium_amd.emit import emit_hip, launch_geometry
-from palladium_amd.runtime import MathMode, math_mode_ordinal
+from palladium_amd.runtime import REPRODUCIBLE_ORDINAL, MathMode, math_mode_ordinal
 from palladium_amd.trace import KernelSpec, trace
 
 __all__ = ["FfiCallable", "hip_call_jit"]
@@ -80,7 +81,8 @@ class FfiCallable:
     Attributes
     ----------
     interpret : callable
-        The same pallas_call with `interpret=True`.
+        The same pallas_call with `interpret=True` (under REPRODUCIBLE math,
+        in that mode's arithmetic, as `HipCallable.interpret`).
     """
 
     def __init__(self, kernel: Callable, pallas_kwargs: dict[str, Any], math_mode: Any,
@@ -93,10 +95,15 @@ class FfiCallable:
                 "dispatch per batch element), or put the batch dimension in the Pallas "
                 "grid instead."
             )
-        from palladium_amd import _stage
+        from palladium_amd import _stage, _use_jax
 
         self._staged, self.interpret = _stage(kernel, pallas_kwargs, "auto")
         self._math_mode = math_mode_ordinal(math_mode)
+        if self._math_mode == REPRODUCIBLE_ORDINAL and not _use_jax("auto"):
+            # the interpreter in this mode's arithmetic, as HipCallable's
+            from palladium_amd.interpret import interpret_call
+
+            self.interpret = functools.partial(interpret_call, self._staged, math_mode=self._math_mode)
         self._vmap_method = vmap_method
         self._threadgroup = threadgroup
         self._cache: dict[tuple, tuple[KernelSpec, str]] = {}

@@ -475,3 +475,19 @@ def test_tanh_within_one_ulp_and_special_values():
     np.testing.assert_array_equal(exact.dtanhf(np.float32([np.inf, -np.inf, 20.0, -1e30])),
                                   np.float32([1.0, -1.0, 1.0, -1.0]))
     assert np.isnan(exact.dtanhf(np.float32([np.nan]))).all()
+
+
+def test_jit_callable_interprets_in_the_mode_too():
+    """hip_call_jit's `.interpret()` follows REPRODUCIBLE as hip_call's does."""
+    from palladium_amd import exact
+
+    def k(x_ref, o_ref):
+        o_ref[...] = jnp.sin(x_ref[...]) / (x_ref[...] + 3.0)
+
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    x = np.linspace(-2, 2, 64, dtype=np.float32)
+    kw = dict(grid=(64,), in_specs=[s], out_specs=s, out_shape=pl.ShapeDtypeStruct((64,), np.float32),
+              math_mode="reproducible")
+    got = np.asarray(pa.hip_call_jit(k, **kw).interpret(x))
+    want = exact.rdiv(exact.dsinf(x), x + np.float32(3.0))
+    assert _same_bits(got, want)
