@@ -27,6 +27,9 @@ from palladium_amd.trace import trace
 
 FP32_PEAK = 157.3e12
 HBM_PEAK = 8.0e12
+# MI355X's published peak engine clock: no wavefront issues faster than its
+# cycles per instruction at this clock
+ENGINE_CLOCK_MAX_HZ = 2.4e9
 # rocprofv3 FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 for one config-1 launch.
 LV_MEASURED_TRAFFIC_BYTES = int((23467.5 + 11718.75) * 1024)
 GS_MEASURED_TRAFFIC_BYTES = int((131612.4 + 131072.0) * 1024)
@@ -1332,13 +1335,17 @@ def _latency_probe_source(op: str, chains: int) -> str:
     init = "\n".join(f"    {ct} a{i} = ({ct})(threadIdx.x + {i + 1});" for i in range(chains))
     total = " + ".join(f"a{i}" for i in range(chains))
     return f"""
-extern "C" __global__ void __launch_bounds__(64) probe(const float* __restrict__ in, float* __restrict__ out) {{
+extern "C" __global__ void __launch_bounds__(64) probe(const float* __restrict__ in, float* __restrict__ out,
+                                                       unsigned long long* __restrict__ cycles) {{
     {ct} b = in[0], c = in[1];
 {init}
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime();
     for (int it = 0; it < {_LAT_ITERS}; ++it) {{
 {body}
     }}
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime();
     out[blockIdx.x * 64 + threadIdx.x] = (float)({total});
+    if (threadIdx.x == 0) cycles[blockIdx.x] = t1 - t0;
 }}
 """
 
@@ -1347,24 +1354,31 @@ def valu_latencies() -> dict:
     """Nanoseconds per instruction for ONE wavefront per SIMD (1,024 single-wave
     workgroups): a dependent chain of v_fma_f32 (result latency), dependent
     chains of v_exp/v_log/v_rcp (transcendental latency), and eight
-    independent v_fma_f32 chains (the issue interval of a lone wavefront)."""
+    independent v_fma_f32 chains (the issue interval of a lone wavefront).
+    The independent chains are also timed inside the kernel in shader-clock
+    cycles (s_memtime), which do not depend on the clock the probe ran at:
+    `issue_cycles` per form and their minimum, `min_issue_cycles`."""
     from palladium_amd import runtime as rt
 
     blocks = 1024
     inb = rt.Buffer.from_numpy(np.array([1, 0], dtype=np.float32))
     outb = rt.Buffer.empty((blocks * 64,), np.float32)
+    cyc = rt.Buffer.empty((blocks,), np.uint64)
     s = rt.Stream()
+    cycles: dict[str, float] = {}
 
     def ns_per_instr(op: str, chains: int) -> float:
         k = rt.Kernel(_latency_probe_source(op, chains), "probe", "fast")
-        k.launch_ptrs(blocks, 64, [inb.ptr, outb.ptr], s)
+        k.launch_ptrs(blocks, 64, [inb.ptr, outb.ptr, cyc.ptr], s)
         s.synchronize()
         e0, e1 = rt.Event(), rt.Event()
         e0.record(s)
         for _ in range(5):
-            k.launch_ptrs(blocks, 64, [inb.ptr, outb.ptr], s)
+            k.launch_ptrs(blocks, 64, [inb.ptr, outb.ptr, cyc.ptr], s)
         e1.record(s)
         e1.synchronize()
+        if chains > 1:
+            cycles[op] = float(np.median(cyc.to_numpy(s))) / (_LAT_ITERS * _LAT_UNROLL)
         return e0.elapsed_ms(e1) / 5 * 1e6 / (_LAT_ITERS * _LAT_UNROLL)
 
     out = {"fma_dependent_ns": ns_per_instr("v_fma_f32", 1),
@@ -1377,18 +1391,27 @@ def valu_latencies() -> dict:
     out["issue_ns_by_op"] = {op: ns_per_instr(op, 8) for op in ("v_add_f32_e32", "v_fmac_f32_e32", "v_fma_f64",
                                                               "v_fmac_f64_e32")}
     out["per_op_dependent_ns"].update({op: ns_per_instr(op, 1) for op in ("v_add_f32_e32", "v_fma_f64")})
+    out["issue_cycles"] = cycles
+    out["min_issue_cycles"] = min(cycles.values())
     return out
 
 
 def bs3_latency_bound(call, host, lat: dict, max_attempts: int, kernel_ms: float, mode: str = "fast") -> dict:
     """The latency bounds of the adaptive loop: the slowest lane runs
     `max_attempts` attempts back to back, and its wavefront issues each
-    attempt's instructions one after another. `latency_frac` is against the
-    issue floor (the loop's instructions at one wavefront's measured issue
-    interval, no waiting on results: a bound). `chain_model_ratio` is
-    against the in-order chain model of the same loop (palladium_amd.isa)
-    with the measured result latencies: an estimate, which a wavefront that
-    overlaps more than the model assumes can beat."""
+    attempt's vector instructions one after another. `latency_frac` is
+    against the issue floor: the loop's vector instructions at the fewest
+    shader-clock cycles any vector form takes between issues
+    (`min_issue_cycles`, counted in the probe by s_memtime), at the
+    published peak engine clock, with scalar and branch instructions taken
+    as free (they can issue in a vector instruction's shadow): no wavefront
+    can do better, whatever clock it gets. `ratio_to_issue_floor_at_probe_clock`
+    prices every instruction at the interval the probe measured in
+    nanoseconds instead, at the clock the probe got (not a bound: the
+    lone wavefront at the end of the launch may run at a higher clock).
+    `chain_model_ratio` is against the in-order chain model of the same loop
+    (palladium_amd.isa) with the measured result latencies: an estimate,
+    which a wavefront that overlaps more than the model assumes can beat."""
     from palladium_amd import isa
     from palladium_amd import runtime as rt
     from palladium_amd.emit.compact import iterations_per_pass
@@ -1400,12 +1423,15 @@ def bs3_latency_bound(call, host, lat: dict, max_attempts: int, kernel_ms: float
     per = iterations_per_pass(bound.hip_source)
     ns = m.cycles_per_iteration / per
     chain_ms = max_attempts * ns / 1e6
-    issue_ms = max_attempts * (m.instructions / per) * lat["issue_ns"] / 1e6
+    probe_ms = max_attempts * (m.instructions / per) * lat["issue_ns"] / 1e6
+    issue_ms = max_attempts * (m.valu / per) * lat["min_issue_cycles"] / ENGINE_CLOCK_MAX_HZ * 1e3
     return {"ns_per_attempt_chain_model": ns, "loop_instructions": m.instructions / per,
             "loop_valu": m.valu / per, "loop_transcendental": m.transcendental / per,
             "attempts_per_machine_iteration": per, "max_attempts_one_lane": max_attempts,
             "measured_ns_per_attempt_slowest_wave": kernel_ms * 1e6 / max_attempts,
+            "min_issue_cycles": lat["min_issue_cycles"], "engine_clock_max_hz": ENGINE_CLOCK_MAX_HZ,
             "issue_floor_ms": issue_ms, "latency_frac": issue_ms / kernel_ms,
+            "issue_floor_ms_at_probe_clock": probe_ms, "ratio_to_issue_floor_at_probe_clock": probe_ms / kernel_ms,
             "chain_model_ms": chain_ms, "chain_model_ratio": chain_ms / kernel_ms, "latencies_ns": lat}
 
 

@@ -95,8 +95,10 @@ def test_latency_bounds_name_the_issue_floor_a_fraction_and_the_chain_model_a_ra
 
     monkeypatch.setattr(rt, "compile_code_object", lambda *a, **k: b"")
     monkeypatch.setattr(isa, "loop_model", lambda *a, **k: isa.LoopModel(100, 90, 2, 10, 400.0))
-    lat = {"fma_dependent_ns": 4.3, "transcendental_dependent_ns": 5.8, "issue_ns": 2.9}
+    lat = {"fma_dependent_ns": 4.3, "transcendental_dependent_ns": 5.8, "issue_ns": 2.9, "min_issue_cycles": 5.4}
     lb = bench.bs3_latency_bound(_Call(), (), lat, 1000, 0.35)   # 350 ns per attempt measured
-    assert abs(lb["issue_floor_ms"] - 1000 * 100 * 2.9 / 1e6) < 1e-12
-    assert lb["latency_frac"] < 1.0 < lb["chain_model_ratio"]
+    # the hard floor: 90 vector instructions per attempt at 5.4 cycles, 2.4 GHz
+    assert abs(lb["issue_floor_ms"] - 1000 * 90 * 5.4 / 2.4e9 * 1e3) < 1e-12
+    assert abs(lb["issue_floor_ms_at_probe_clock"] - 1000 * 100 * 2.9 / 1e6) < 1e-12
+    assert lb["latency_frac"] < lb["ratio_to_issue_floor_at_probe_clock"] < 1.0 < lb["chain_model_ratio"]
     assert bench.fractions_over_one(lb) == []
