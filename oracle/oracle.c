@@ -418,10 +418,12 @@ float oracle_dexp2f(float x) {
 }
 
 void oracle_dlog2f_many(long n, const float *x, float *out) {
+#pragma omp parallel for schedule(static)
   for (long i = 0; i < n; ++i) out[i] = oracle_dlog2f(x[i]);
 }
 
 void oracle_dexp2f_many(long n, const float *x, float *out) {
+#pragma omp parallel for schedule(static)
   for (long i = 0; i < n; ++i) out[i] = oracle_dexp2f(x[i]);
 }
 
