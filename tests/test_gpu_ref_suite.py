@@ -1,9 +1,11 @@
 """The reference's matmul / reduce / transpose / dtype-matrix cases on the
-GPU: against the NumPy closed form (FAST), and bit for bit against the
+GPU: against the NumPy closed form (FAST), bit for bit against the
 interpreter under SAFE wherever the device and host compute the same
 operations (everything except softmax, whose exp may differ by a float32
-ulp between device and host libm). Float sums are bit-exact because the
-interpreter adds in the emitted order."""
+ulp between device and host libm), and bit for bit under REPRODUCIBLE for
+every case, softmax included (its exp and division are restated there).
+Float sums are bit-exact because the interpreter adds in the emitted
+order."""
 
 import numpy as np
 import pytest
@@ -27,6 +29,16 @@ def test_safe_bit_exact_vs_interpreter(name):
     kernel, out_shape, args, _ = CASES[name]()
     f = pa.hip_call(kernel, out_shape=out_shape, math_mode="safe")
     np.testing.assert_array_equal(f(*args), f.interpret(*args))
+
+
+@pytest.mark.parametrize("name", sorted(CASES))
+def test_reproducible_bit_exact_vs_interpreter(name):
+    kernel, out_shape, args, _ = CASES[name]()
+    f = pa.hip_call(kernel, out_shape=out_shape, math_mode="reproducible")
+    got, want = f(*args), f.interpret(*args)
+    for g, w in zip(got if isinstance(got, tuple) else (got,), want if isinstance(want, tuple) else (want,)):
+        np.testing.assert_array_equal(g, w)
+    check(name, got)
 
 
 def test_preferred_element_type_accumulates_in_float32_on_device():
