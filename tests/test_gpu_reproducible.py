@@ -252,3 +252,39 @@ def test_narrow_float_transcendentals_bit_exact_with_the_interpreter(narrow):
         gf = dtypes.to_float(g) if dtypes.is_bf16(g.dtype) else np.asarray(g, np.float32)
         wf = dtypes.to_float(w) if dtypes.is_bf16(w.dtype) else np.asarray(w, np.float32)
         _assert_same_bits(gf.astype(np.float32), wf.astype(np.float32), f"{narrow} {name}")
+
+
+def _butterfly_block_sums(v: np.ndarray, block: int) -> np.ndarray:
+    """The device's cross-lane sum of each block of `block` float32 values:
+    a __shfl_xor butterfly inside each 64-lane wavefront (lane i adds lane
+    i ^ off, off = 32 .. 1), then the wavefronts' partials added in order."""
+    w = v.reshape(-1, block // 64, 64)
+    off = 32
+    while off >= 1:
+        w = w[..., :off] + w[..., off:2 * off]
+        off //= 2
+    parts = w[..., 0]
+    acc = parts[:, 0].copy()
+    for k in range(1, parts.shape[1]):
+        acc = acc + parts[:, k]
+    return acc
+
+
+def test_gbm_block_sums_config3_reproducible_bit_exact():
+    """Config 3's stated output (the discounted payoff summed per block of
+    256 paths, the paths spread over the block's lanes) under REPRODUCIBLE:
+    all 16,384 block sums equal oracle_gbm_r's payoffs, discounted and summed
+    in the device's cross-lane order, bit for bit."""
+    import math
+
+    from palladium_amd.frontend import random
+    from palladium_amd.workloads import GBM_CFG, gbm_block_call
+
+    cfg = GBM_CFG
+    block = 256
+    print(f"[reproducible] gbm_block_sums n={cfg.n_paths} block={block}", flush=True)
+    got = gbm_block_call(cfg, block=block, math_mode="reproducible")(random.key(cfg.seed))
+    payoff = oracle.gbm(cfg, cfg.n_paths, mode="reproducible")
+    disc = np.float32(math.exp(-cfg.r * cfg.t))
+    want = _butterfly_block_sums(disc * payoff, block)
+    _assert_same_bits(np.asarray(got, np.float32), want.astype(np.float32), "gbm block sums")
