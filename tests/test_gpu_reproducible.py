@@ -308,3 +308,18 @@ def test_gray_scott_reproducible_bit_exact_vs_interpreter():
         hu, hv = call.interpret(hu, hv)
     np.testing.assert_array_equal(du, hu)
     np.testing.assert_array_equal(dv, hv)
+
+
+def test_lv_config0_blocks_reproducible_bit_exact():
+    """Config 0 (N = 100,000, dt = 0.01, 1,000 steps, 256-trajectory blocks
+    spread over lanes, the last block ragged) under REPRODUCIBLE: final
+    states equal oracle_lv_rk4_r's bit for bit."""
+    from palladium_amd.workloads import LV_CFG0, lv_inputs, lv_rk4_call
+
+    cfg = LV_CFG0
+    args = lv_inputs(cfg.n, cfg.seed)
+    print(f"[reproducible] lv_rk4 config 0 n={cfg.n} blocks of 256", flush=True)
+    got = lv_rk4_call(cfg.n, cfg.dt, cfg.steps, track_max=False, block=256, math_mode="reproducible")(*args)
+    want = oracle.lv_rk4_r(*args, cfg.dt, cfg.steps)
+    np.testing.assert_array_equal(got[0], want[0])
+    np.testing.assert_array_equal(got[1], want[1])
