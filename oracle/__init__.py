@@ -115,6 +115,8 @@ def _declare_more(L):
     L.oracle_rpow_many.restype = None
     L.oracle_rpow_log.argtypes = [f]
     L.oracle_rpow_log.restype = ctypes.c_double
+    L.oracle_rpow_log_many.argtypes = [l, _F, ctypes.POINTER(ctypes.c_double)]
+    L.oracle_rpow_log_many.restype = None
     L.oracle_rdiv.argtypes = [f, f]
     L.oracle_rdiv.restype = f
     L.oracle_dlog2f_many.argtypes = [l, _F, _F]
@@ -259,6 +261,14 @@ def rdiv(a: float, b: float) -> np.float32:
 
 def rpow_log(x: float) -> float:
     return float(_lib2().oracle_rpow_log(float(x)))
+
+
+def rpow_log_many(x: np.ndarray) -> np.ndarray:
+    """oracle_rpow_log elementwise (the REPRODUCIBLE pow's double log2)."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty(x.size, np.float64)
+    _lib2().oracle_rpow_log_many(x.size, _fp(x), out.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+    return out
 
 
 def _gs_consts(cfg):

@@ -218,6 +218,7 @@ double oracle_pow_log(float x) {
 }
 
 void oracle_pow_log_many(long n, const float *x, double *out) {
+#pragma omp parallel for schedule(static)
   for (long i = 0; i < n; ++i) out[i] = oracle_pow_log(x[i]);
 }
 
@@ -364,6 +365,11 @@ double oracle_rpow_log(float x) {
   p = fma(p, s, 0.9617966734515485);
   p = fma(p, s, 2.885390081789987);
   return fma(t, p, (double)e);
+}
+
+void oracle_rpow_log_many(long n, const float *x, double *out) {
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; ++i) out[i] = oracle_rpow_log(x[i]);
 }
 
 /* 2^z, z = k + r with |r| <= 1/2: Q(r) of degree 7 as two Horner halves
