@@ -255,3 +255,21 @@ def test_two_d_threadgroup_sets_the_instance_tile():
     assert "threadIdx.x / 64u" in default
     ragged = pa.debug_hip(k, x, threadgroup=(48, 4), **kw)   # 48 does not divide 64
     assert "threadIdx.x / 4u" not in ragged
+
+
+def test_empty_grid_is_a_clear_error_and_interprets_to_empty():
+    """A grid with no program instances cannot launch: emission names the
+    grid instead of handing the runtime a zero-block launch, while the
+    interpreter returns the empty result."""
+    import palladium_amd as pa
+    from palladium_amd.errors import EmitError
+
+    def k(x_ref, o_ref):
+        o_ref[...] = x_ref[...] * 2.0
+
+    s = pl.BlockSpec((1,), lambda i: (i,))
+    x = np.zeros(0, np.float32)
+    f = pa.hip_call(k, grid=(0,), in_specs=[s], out_specs=s, out_shape=pl.ShapeDtypeStruct((0,), np.float32))
+    assert np.asarray(f.interpret(x)).shape == (0,)
+    with pytest.raises(EmitError, match="no program instances"):
+        f.explain(x, compile=False)
