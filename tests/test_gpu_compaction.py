@@ -115,7 +115,7 @@ def _fuzz_kernel(seed):
     return kernel
 
 
-@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", os.environ.get("PALLADIUM_FUZZ_EXAMPLES", "12")))))
 def test_random_compacted_loops_bit_exact_vs_interpreter(seed):
     n = 2048
     rng = np.random.default_rng(700 + seed)

@@ -4,9 +4,10 @@ powers and transcendentals added, under REPRODUCIBLE). Under SAFE only IEEE
 operations are generated (+ - * / fmin fmax abs neg select), so results
 must agree bit for bit. Programs mix expression trees, fori_loops with
 permuted carries, switch and bounded while loops (after the reference's
-tests/test_fuzz_emitter.py grammar). The same programs run in bfloat16,
-where each operation is evaluated in float32 and rounded to bfloat16 on
-both sides."""
+tests/test_fuzz_emitter.py grammar; seeds per test from PALLADIUM_FUZZ_SEEDS
+or the reference's PALLADIUM_FUZZ_EXAMPLES, 12 by default). The same programs
+run in bfloat16, where each operation is evaluated in float32 and rounded
+to bfloat16 on both sides."""
 
 import os
 
@@ -93,7 +94,7 @@ def _make_kernel(seed, powers=False, transc=False):
     return kernel
 
 
-@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", os.environ.get("PALLADIUM_FUZZ_EXAMPLES", "12")))))
 def test_random_program_bit_exact_vs_interpreter(seed):
     n = 300
     rng = np.random.default_rng(100 + seed)
@@ -109,7 +110,7 @@ def test_random_program_bit_exact_vs_interpreter(seed):
 
 
 @pytest.mark.parametrize("dt", [dtypes.bfloat16, np.dtype(np.float16)], ids=["bf16", "f16"])
-@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", os.environ.get("PALLADIUM_FUZZ_EXAMPLES", "12")))))
 def test_random_program_narrow_float_bit_exact_vs_interpreter(seed, dt):
     n = 300
     rng = np.random.default_rng(200 + seed)
@@ -124,7 +125,7 @@ def test_random_program_narrow_float_bit_exact_vs_interpreter(seed, dt):
         np.testing.assert_array_equal(np.ascontiguousarray(g).view(np.uint16), np.ascontiguousarray(w).view(np.uint16))
 
 
-@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", os.environ.get("PALLADIUM_FUZZ_EXAMPLES", "12")))))
 def test_random_program_reproducible_bit_exact_vs_interpreter(seed):
     """The same grammar plus powers, sums of products, exp, log, sin, cos
     and tanh, under REPRODUCIBLE math: the emitter fuses single-use products

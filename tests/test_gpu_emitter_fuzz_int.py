@@ -11,7 +11,7 @@ from fuzz_int import make_call, make_inputs
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", os.environ.get("PALLADIUM_FUZZ_EXAMPLES", "12")))))
 def test_integer_program_bit_exact_vs_interpreter(seed):
     print(f"fuzz_int seed={seed}", flush=True)
     call = make_call(seed, math_mode="safe")

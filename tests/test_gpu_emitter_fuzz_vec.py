@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("lanes", [False, True], ids=["instance", "lanes"])
-@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", os.environ.get("PALLADIUM_FUZZ_EXAMPLES", "12")))))
 def test_vector_program_bit_exact_vs_interpreter(seed, lanes):
     print(f"fuzz_vec seed={seed} lanes={lanes}", flush=True)
     call = make_call(seed, lanes=lanes, math_mode="safe")
@@ -28,7 +28,7 @@ def test_vector_program_bit_exact_vs_interpreter(seed, lanes):
 
 @pytest.mark.parametrize("dt", [dtypes.bfloat16, np.dtype(np.float16)], ids=["bf16", "f16"])
 @pytest.mark.parametrize("lanes", [False, True], ids=["instance", "lanes"])
-@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", os.environ.get("PALLADIUM_FUZZ_EXAMPLES", "12")))))
 def test_vector_program_narrow_float_bit_exact_vs_interpreter(seed, lanes, dt):
     print(f"fuzz_vec {dtypes.name(dt)} seed={seed} lanes={lanes}", flush=True)
     call = make_call(seed, lanes=lanes, dtype=dt, math_mode="safe")

@@ -56,7 +56,7 @@ def _inputs(n, seed):
     return x
 
 
-@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", "12"))))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("PALLADIUM_FUZZ_SEEDS", os.environ.get("PALLADIUM_FUZZ_EXAMPLES", "12")))))
 def test_random_loop_shared_equals_unshared(seed, monkeypatch):
     n = 2048
     print(f"[share_pow_logs fuzz] seed={seed}", flush=True)
