@@ -465,6 +465,23 @@ def launch_geometry(spec: KernelSpec, block: int | None = None, lanes: int | Non
     return LaunchGeometry(b, (threads + b - 1) // b, n, lanes)
 
 
+_TRANSCENDENTAL = frozenset("exp exp2 log log2 log1p expm1 sin cos tan tanh pow logistic atan2 pow_log "
+                            "pow_with_log".split())
+
+
+def _has_transcendental(jaxpr: Jaxpr) -> bool:
+    for e in jaxpr.eqns:
+        if e.primitive.name in _TRANSCENDENTAL:
+            return True
+        for v in e.params.values():
+            subs = v if isinstance(v, tuple) else (v,)
+            for sub in subs:
+                inner = getattr(sub, "jaxpr", sub)
+                if isinstance(inner, Jaxpr) and _has_transcendental(inner):
+                    return True
+    return False
+
+
 def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None = None,
              math_mode: Any = None, tile: tuple[int, int] | None = None) -> str:
     """Assemble the complete HIP source for a KernelSpec.
@@ -537,7 +554,13 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
         shared = share_pow_logs(body)
         if keeps_compaction(shared):
             body = shared
-    if math_mode is not None and math_mode_ordinal(math_mode) == 3:
+    if math_mode is not None and (math_mode_ordinal(math_mode) == 3 or
+                                  (math_mode_ordinal(math_mode) == 2 and not _has_transcendental(body)
+                                   and os.environ.get("PALLADIUM_FAST_CONTRACT", "1") != "0")):
+        # FAST pins the fused sites only where nothing transcendental
+        # follows: the compiler folds a transcendental's input scaling
+        # (exp's log2 e, say) into the FMA before it, which an explicit site
+        # prevents
         from palladium_amd.emit.optimize import contract_products
 
         body = contract_products(body)

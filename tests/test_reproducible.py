@@ -162,19 +162,27 @@ def test_contraction_of_both_products_takes_the_later_one():
     assert f.invars[0] is not m.invars[0] or f.invars[1] is not m.invars[1]
 
 
-def test_contraction_leaves_other_modes_alone():
+def test_contraction_by_mode():
+    """SAFE and RELAXED never pin fused sites; REPRODUCIBLE always does;
+    FAST does where no transcendental function is in the kernel (the
+    compiler folds a transcendental's input scaling into the FMA before it,
+    which an explicit site would prevent)."""
     def k(a_ref, b_ref, c_ref, o_ref):
         o_ref[...] = a_ref[...] * b_ref[...] + c_ref[...]
 
-    spec = _tiny(k)
+    def kt(a_ref, b_ref, c_ref, o_ref):
+        o_ref[...] = jnp.exp(a_ref[...] * b_ref[...] + c_ref[...])
 
-    def body(mode):
-        src = emit_hip(spec, math_mode=mode)
+    def body(kernel, mode):
+        src = emit_hip(_tiny(kernel), math_mode=mode)
         return src[src.index('extern "C"'):]
 
-    for mode in ("safe", "relaxed", "fast"):
-        assert "__builtin_fmaf" not in body(mode)
-    assert "__builtin_fmaf" in body("reproducible")
+    for mode in ("safe", "relaxed"):
+        assert "__builtin_fmaf" not in body(k, mode)
+        assert "__builtin_fmaf" not in body(kt, mode)
+    assert "__builtin_fmaf" in body(k, "reproducible") and "__builtin_fmaf" in body(kt, "reproducible")
+    assert "__builtin_fmaf" in body(k, "fast")
+    assert "__builtin_fmaf" not in body(kt, "fast")
 
 
 def test_bs3_reproducible_oracle_against_float64_restatement():
