@@ -490,9 +490,10 @@ def emit_hip(spec: KernelSpec, kernel_name: str | None = None, block: int | None
     operand in jaxpr order, inputs (`const T* __restrict__`) then outputs
     (`T* __restrict__`), and nothing else; the grid and block shapes are
     compile-time constants of the source. With `math_mode` FAST the jaxpr
-    first goes through the FAST-only algebraic rewrites of
-    `palladium_amd.emit.optimize`; with REPRODUCIBLE, through its exact
-    product contraction (`contract_products`).
+    first goes through the FAST algebraic rewrites of
+    `palladium_amd.emit.optimize`, and, in a kernel with no transcendental
+    function, through the product contraction (`contract_products`);
+    REPRODUCIBLE takes the same rewrites and always the contraction.
 
     Raises
     ------
