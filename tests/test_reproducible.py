@@ -11,7 +11,7 @@ import oracle
 import palladium_amd as pa
 from palladium_amd.emit.core import emit_hip
 from palladium_amd.emit.optimize import contract_products
-from palladium_amd.frontend import jnp, lax, pl
+from palladium_amd.frontend import jnp, pl
 from palladium_amd.ir import Jaxpr
 from palladium_amd.trace import trace
 from palladium_amd.workloads import BS3_CFG, bs3_inputs, bs3_vdp_call
